@@ -1,0 +1,208 @@
+#!/usr/bin/env python3
+"""Decode benchmark of the int4 hot path on one MI355X.
+
+Workload: a random-init 36-layer Qwen3-4B-shaped
+int4 model (hidden 2560, 32 q / 8 kv heads x 128, SwiGLU 9728, tied int4
+embedding/LM head 151936 x 2560), fp16 KV cache, batch 1, greedy decoding
+after a 64-token random prompt.  A "step" is one decode token: 144 body
+GEMVs + 36 attentions + LM head + argmax, replayed from a HIP graph with the
+greedy token fed back on the device.
+
+Printed as one JSON line: tok/s (value), the body-GEMV roofline of the
+dominant kernel measured live with HIP events, the aggregate body-GEMV
+bandwidth, and the CPU oracle's tok/s on this host's cores for the same
+model and context (cpu_baseline, a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tok/s @ Qwen3-4B batch 1; body-GEMV HBM GB/s as % of peak"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=64)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--gemv-reps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def algorithmic_bytes(config):
+    """Bytes one launch of each body GEMV kind must move (weights + scales +
+    fp32 activations in + fp32 outputs + norm weights)."""
+    from harsh4b_amd.config import shapes
+    sh = shapes(config)
+    h = int(config["hidden_size"])
+    i = int(config["intermediate_size"])
+    q = int(config["num_attention_heads"]) * int(config["head_dim"])
+    out = {}
+    r, w = sh["qkv"]
+    out["qkv"] = r * w // 2 + 4 * r + 4 * w + 4 * w + 4 * r          # W, scales, x, gamma, out
+    r, w = sh["o"]
+    out["o"] = r * w // 2 + 4 * r + 4 * q + 4 * r + 4 * r             # W, scales, attended, x r+w
+    r, w = sh["gate_up"]
+    out["gate_up"] = r * w // 2 + 4 * r + 4 * w + 4 * w + 4 * i       # W, scales, x, gamma, act
+    r, w = sh["down"]
+    out["down"] = r * w // 2 + 4 * r + 4 * i + 4 * h + 4 * h          # W, scales, act, x r+w
+    return out
+
+
+def time_graph(lib, model, state, launches, reps, torch):
+    """Capture `launches` (list of (layer, kind)) into a HIP graph on the
+    state's stream, replay it `reps` times between two HIP events and
+    return the mean time of one replay in ms."""
+    s = state.stream
+    handle = ctypes.c_void_p()
+    # capture through the library's own step hooks
+    err = 0
+    torch.cuda.synchronize()
+    cap = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cap, stream=s):
+        for layer, kind in launches:
+            err |= lib.hq_step_gemv(ctypes.byref(model.struct), ctypes.byref(state.struct),
+                                    layer, kind, s.cuda_stream)
+    if err:
+        raise RuntimeError("hq_step_gemv failed during capture")
+    del handle
+    cap.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        cap.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def cpu_baseline(model, state, ctx, seconds):
+    """The CPU oracle (C restatement of the reference path, OpenMP) decoding
+    from the same model and KV cache on this host."""
+    import numpy as np
+    import oracle
+    from harsh4b_amd.synthetic import host_arrays
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    ref = oracle.OracleModel(model.config, host_arrays(model))
+    rs = ref.new_state(state.capacity)
+    rs.keys[:, :ctx] = state.keys[:, :ctx].cpu().numpy().view(np.uint16)
+    rs.values[:, :ctx] = state.values[:, :ctx].cpu().numpy().view(np.uint16)
+    rs.position = ctx
+    token = 1000
+    token = ref.forward_token(token, rs)      # warm-up step (page-in, thread spin-up)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        token = ref.forward_token(token, rs)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 2) or rs.position >= rs.struct.capacity:
+            break
+    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps of the same 36-layer model at context {ctx}+, "
+                      f"{el:.1f} s, OpenMP over GEMV rows (oracle/hq_oracle.c)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from harsh4b_amd import _native
+    from harsh4b_amd.config import QWEN3_4B, body_bytes
+    from harsh4b_amd.synthetic import random_model
+
+    cfg = QWEN3_4B
+    lib = _native.lib()
+    print(f"# building random Qwen3-4B int4 model (seed {args.seed})", file=sys.stderr, flush=True)
+    model = random_model(cfg, seed=args.seed)
+    cap = args.ctx + args.warmup + args.steps + 4
+    state = model.new_state(cap)
+    prompt = np.random.default_rng(3).integers(0, int(cfg["vocab_size"]), args.ctx)
+    for t in prompt:
+        model.forward_token(int(t), state)
+    state.synchronize()
+    print(f"# prefilled {args.ctx} tokens", file=sys.stderr, flush=True)
+
+    model.decode_greedy(state, args.warmup)          # captures the step graph
+    state.synchronize()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(state.stream)
+    model.decode_greedy(state, args.steps)
+    e1.record(state.stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    state.check_status()
+    tok_s = args.steps / (ms / 1e3)
+    print(f"# decode: {args.steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
+
+    # body-GEMV kernels measured live: graphs of the step's own GEMV launches
+    L = int(cfg["num_hidden_layers"])
+    kinds = {"qkv": 0, "o": 1, "gate_up": 2, "down": 3}
+    per_kind_ms = {}
+    for name, kind in kinds.items():
+        per_kind_ms[name] = time_graph(lib, model, state, [(l, kind) for l in range(L)],
+                                       args.gemv_reps, torch) / L
+    body_ms = time_graph(lib, model, state, [(l, k) for l in range(L) for k in range(4)],
+                         args.gemv_reps, torch)
+    state.check_status()
+    alg = algorithmic_bytes(cfg)
+    dominant = max(per_kind_ms, key=lambda k: per_kind_ms[k])
+    achieved = alg[dominant] / (per_kind_ms[dominant] * 1e-3) / 1e9
+    body_gbs = body_bytes(cfg) / (body_ms * 1e-3) / 1e9
+    for k in kinds:
+        print(f"# {k:8s} GEMV: {per_kind_ms[k] * 1e3:8.2f} us/launch, "
+              f"{alg[k] / (per_kind_ms[k] * 1e-3) / 1e9:8.1f} GB/s", file=sys.stderr)
+    print(f"# body GEMV per token: {body_ms * 1e3:.1f} us -> {body_gbs:.1f} GB/s", file=sys.stderr, flush=True)
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: random-init int4 weights, random prompt token ids",
+        "config": {"workload": "configs[2]: 36-layer Qwen3-4B-shaped int4 decode, batch 1, "
+                               f"context {args.ctx}, greedy, fp16 KV cache",
+                   "global_batch": 1, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
+        "roofline": {"kernel": f"gemv_kernel ({dominant})", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "body_gemv": {"bytes_per_token": body_bytes(cfg), "us_per_token": round(body_ms * 1e3, 2),
+                      "achieved": round(body_gbs, 1), "unit": "GB/s",
+                      "frac": round(body_gbs / HBM_PEAK_GBS, 4)},
+    }
+    if not args.no_cpu_baseline:
+        print("# timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(model, state, args.ctx, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

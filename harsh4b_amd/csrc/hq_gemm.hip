@@ -1,0 +1,290 @@
+// hq_gemm.hip - batched decode: packed-int4 weights x M int8 activation
+// vectors on gfx950 int8 MFMA (v_mfma_i32_16x16x64_i8).
+//
+// The reference decodes one sequence at a time (cpu_lightspark.py:424 in the
+// reference repository); M sequences are defined as M independent GEMVs of
+// cpu_kernels/litespark_int4.cpp:22-76, and this kernel returns exactly
+// those integers: out[m,n] = ((float)acc[m,n] * act[m]) * scale[n].
+//
+// Mapping onto the MFMA: weight rows go on the 16-row A side, the batch on
+// the 16-column B side (M = 8 fills half of B; M = 32 uses two B tiles).
+// A lane of the A operand carries 16 K values of one weight row; the nibbles
+// of a packed dword become signed bytes (w << 4) & 0xF0F0F0F0 (16 * even
+// columns) and w & 0xF0F0F0F0 (16 * odd columns), so the MFMA accumulates
+// 16 * acc exactly.  The B operand is the activation slice stored in LDS with
+// the same per-8-column even/odd order, so A and B agree on the K order.
+// K is split across blocks so that small row counts still fill the chip;
+// split partial sums meet in an int32 workspace through atomic adds, and the
+// last split to arrive at a row tile writes the epilogue and re-zeroes its
+// part of the workspace (no waiting anywhere).
+#include "hq_device.h"
+#include "hq_internal.h"
+
+namespace hq {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileRows = 64;     // 4 waves x 16 rows
+constexpr int kSlice = 256;       // K columns staged per iteration
+constexpr int kMaxBatch = 32;     // sequences per launch (two 16-wide B tiles)
+
+struct GemmParams {
+    const int8_t* x;          // [m, K] natural order
+    const float* act;         // [m]
+    const uint8_t* w;         // [N, K/2]
+    const float* ws;          // [N]
+    float* out;               // [m, N]
+    int32_t* acc_out;         // nullable [m, N]
+    int32_t* acc;             // workspace [m, N] (zero between calls)
+    int32_t* counters;        // workspace [tiles]
+    int m, n, k;
+    int slices_per_split;
+    int splits;
+};
+
+// De-interleave 8 int8 columns (a, b = the two little-endian dwords) into
+// [even columns | odd columns].
+__device__ __forceinline__ void deinterleave8(uint32_t a, uint32_t b, uint32_t& ev, uint32_t& od)
+{
+    ev = (a & 0xFFu) | ((a >> 8) & 0xFF00u) | ((b & 0xFFu) << 16) | ((b & 0xFF0000u) << 8);
+    od = ((a >> 8) & 0xFFu) | ((a >> 16) & 0xFF00u) | ((b & 0xFF00u) << 8) | (b & 0xFF000000u);
+}
+
+template <int BT>
+__global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmParams p)
+{
+    constexpr int MP = 16 * BT;                 // padded batch
+    __shared__ __align__(16) uint8_t xs[MP * kSlice];
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
+    const int tile = blockIdx.x;
+    const int split = blockIdx.y;
+    const int row0 = tile * kTileRows + wave * 16;
+    const int arow = row0 + (lane & 15);        // A row of this lane
+    const int kb = lane >> 4;                   // 0..3: 64-column quarter of a slice
+    const bool arow_ok = arow < p.n;
+    const int half = p.k >> 1;
+    const uint8_t* wrow = p.w + size_t(arow_ok ? arow : 0) * size_t(half);
+    const int nslices = (p.k + kSlice - 1) / kSlice;
+    const int s_begin = split * p.slices_per_split;
+    const int s_end = min(nslices, s_begin + p.slices_per_split);
+
+    i32x4 acc[BT];
+#pragma unroll
+    for (int b = 0; b < BT; ++b) acc[b] = i32x4{0, 0, 0, 0};
+
+    for (int sl = s_begin; sl < s_end; ++sl) {
+        const int k0 = sl * kSlice;
+        // A: 32 packed bytes (64 columns) of row `arow` per lane
+        uint4 wa = make_uint4(0, 0, 0, 0), wb = make_uint4(0, 0, 0, 0);
+        const int col = k0 + 64 * kb;
+        if (arow_ok && col < p.k) wa = *reinterpret_cast<const uint4*>(wrow + (col >> 1));
+        if (arow_ok && col + 32 < p.k) wb = *reinterpret_cast<const uint4*>(wrow + (col >> 1) + 16);
+
+        // stage x[:, k0:k0+256] de-interleaved; rows >= m and columns >= K are zero
+        for (int e = tid; e < MP * (kSlice / 16); e += kBlock) {
+            const int mm = e / (kSlice / 16);
+            const int c16 = (e % (kSlice / 16)) * 16;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (mm < p.m && k0 + c16 < p.k)
+                v = *reinterpret_cast<const uint4*>(p.x + size_t(mm) * p.k + k0 + c16);
+            uint4 o;
+            deinterleave8(v.x, v.y, o.x, o.y);
+            deinterleave8(v.z, v.w, o.z, o.w);
+            *reinterpret_cast<uint4*>(xs + mm * kSlice + c16) = o;
+        }
+        __syncthreads();
+
+        const uint32_t wd[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t m4 = 0xF0F0F0F0u;
+            const i32x4 a = {int((wd[2 * j] << 4) & m4), int(wd[2 * j] & m4),
+                             int((wd[2 * j + 1] << 4) & m4), int(wd[2 * j + 1] & m4)};
+            const int cofs = 64 * kb + 16 * j;
+#pragma unroll
+            for (int b = 0; b < BT; ++b) {
+                const uint4 xv = *reinterpret_cast<const uint4*>(xs + (16 * b + (lane & 15)) * kSlice + cofs);
+                const i32x4 bv = {int(xv.x), int(xv.y), int(xv.z), int(xv.w)};
+                acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bv, acc[b], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    // D layout: lane holds rows 4*(lane/16) + r, column lane % 16.
+    const int col_m = lane & 15;
+    const int rbase = row0 + 4 * (lane >> 4);
+    if (p.splits == 1) {
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+            const int mm = 16 * b + col_m;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = rbase + r;
+                if (mm < p.m && n < p.n) {
+                    const int a = acc[b][r] >> 4;
+                    p.out[size_t(mm) * p.n + n] = (float(a) * p.act[mm]) * p.ws[n];
+                    if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+        const int mm = 16 * b + col_m;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = rbase + r;
+            if (mm < p.m && n < p.n) atomicAdd(p.acc + size_t(mm) * p.n + n, acc[b][r] >> 4);
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const int ticket = atomicAdd(p.counters + tile, 1);
+        last_flag = (ticket == p.splits - 1);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+    const int trows = min(kTileRows, p.n - tile * kTileRows);
+    for (int e = tid; e < p.m * trows; e += kBlock) {
+        const int mm = e / trows;
+        const int n = tile * kTileRows + e % trows;
+        int32_t* cell = p.acc + size_t(mm) * p.n + n;
+        const int a = __hip_atomic_load(cell, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        p.out[size_t(mm) * p.n + n] = (float(a) * p.act[mm]) * p.ws[n];
+        if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
+        __hip_atomic_store(cell, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0) p.counters[tile] = 0;
+}
+
+// Per-sequence spec quantization: block m quantizes row m.
+__global__ __launch_bounds__(kBlock) void batch_quant_kernel(const float* x, int k, int8_t* q,
+                                                             float* act, int8_t* q_out,
+                                                             float* act_out)
+{
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const float* xr = x + size_t(m) * k;
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < k; i += kBlock) amax = fmaxf(amax, fabsf(xr[i]));
+    amax = block_max_nonneg(amax, red);
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+    for (int i = threadIdx.x; i < k; i += kBlock) {
+        const int8_t v = quant_i8(xr[i], inv);
+        q[size_t(m) * k + i] = v;
+        if (q_out) q_out[size_t(m) * k + i] = v;
+    }
+    if (threadIdx.x == 0) {
+        act[m] = amax / 127.0f;
+        if (act_out) act_out[m] = amax / 127.0f;
+    }
+}
+
+struct GemmLayout {
+    size_t acc_off, counter_off, q_off, act_off, total;
+};
+
+static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static GemmLayout gemm_layout(int m, int n, int k)
+{
+    const int mb = m < kMaxBatch ? m : kMaxBatch;
+    GemmLayout L{};
+    L.acc_off = 0;
+    L.counter_off = al256(size_t(mb) * size_t(n) * 4);
+    L.q_off = L.counter_off + al256(size_t((n + kTileRows - 1) / kTileRows) * 4);
+    L.act_off = L.q_off + al256(size_t(m) * size_t(k));
+    L.total = L.act_off + al256(size_t(m) * 4);
+    return L;
+}
+
+static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, const float* ws,
+                           float* out, int m, int n, int k, int32_t* acc_out, char* workspace,
+                           hipStream_t s)
+{
+    const GemmLayout L = gemm_layout(m, n, k);
+    const int tiles = (n + kTileRows - 1) / kTileRows;
+    const int nslices = (k + kSlice - 1) / kSlice;
+    // enough blocks for ~2 per CU on 256 CUs
+    int want = (512 + tiles - 1) / tiles;
+    if (want < 1) want = 1;
+    if (want > nslices) want = nslices;
+    const int per = (nslices + want - 1) / want;
+    const int splits = (nslices + per - 1) / per;
+    for (int m0 = 0; m0 < m; m0 += kMaxBatch) {
+        GemmParams p{};
+        p.m = m - m0 < kMaxBatch ? m - m0 : kMaxBatch;
+        p.x = x + size_t(m0) * k;
+        p.act = act + m0;
+        p.w = w; p.ws = ws;
+        p.out = out + size_t(m0) * n;
+        p.acc_out = acc_out ? acc_out + size_t(m0) * n : nullptr;
+        p.acc = reinterpret_cast<int32_t*>(workspace + L.acc_off);
+        p.counters = reinterpret_cast<int32_t*>(workspace + L.counter_off);
+        p.n = n; p.k = k;
+        p.slices_per_split = per;
+        p.splits = splits;
+        if (p.m <= 16)
+            hipLaunchKernelGGL(gemm_mfma_kernel<1>, dim3(tiles, splits), dim3(kBlock), 0, s, p);
+        else
+            hipLaunchKernelGGL(gemm_mfma_kernel<2>, dim3(tiles, splits), dim3(kBlock), 0, s, p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace hq
+
+using namespace hq;
+
+extern "C" size_t hq_gemm_workspace_bytes(int m, int rows, int width)
+{
+    if (m <= 0 || rows <= 0 || width <= 0) return 0;
+    return gemm_layout(m, rows, width).total;
+}
+
+extern "C" int hq_int4_i8_gemm(const int8_t* x, const float* act_scales, const uint8_t* weights,
+                               const float* scales, float* output, int m, int rows, int width,
+                               int32_t* acc_out, void* workspace, void* stream)
+{
+    if (m <= 0 || rows < 0 || width <= 0 || (width & 31)) return HQ_ERR_ARG;
+    if (rows == 0) return HQ_OK;
+    if (!x || !act_scales || !weights || !scales || !output || !workspace) return HQ_ERR_ARG;
+    if (!al16(weights) || !al16(x) || !al16(workspace)) return HQ_ERR_ALIGN;
+    const hipError_t e = run_gemm(x, act_scales, weights, scales, output, m, rows, width, acc_out,
+                                  static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+extern "C" int hq_quant_int4_gemm(const float* x, const uint8_t* weights, const float* scales,
+                                  float* output, int m, int rows, int width, int8_t* q_out,
+                                  float* act_scales_out, int32_t* acc_out, void* workspace,
+                                  void* stream)
+{
+    if (m <= 0 || rows < 0 || width <= 0 || (width & 31)) return HQ_ERR_ARG;
+    if (rows == 0) return HQ_OK;
+    if (!x || !weights || !scales || !output || !workspace) return HQ_ERR_ARG;
+    if (!al16(weights) || !al16(workspace)) return HQ_ERR_ALIGN;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    const GemmLayout L = gemm_layout(m, rows, width);
+    int8_t* q = reinterpret_cast<int8_t*>(ws + L.q_off);
+    float* act = reinterpret_cast<float*>(ws + L.act_off);
+    hipLaunchKernelGGL(batch_quant_kernel, dim3(m), dim3(kBlock), 0, s, x, width, q, act, q_out,
+                       act_scales_out);
+    if (hipGetLastError() != hipSuccess) return HQ_ERR_LAUNCH;
+    const hipError_t e = run_gemm(q, act, weights, scales, output, m, rows, width, acc_out, ws, s);
+    return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}

@@ -1,0 +1,532 @@
+// hq_gemv.hip - batch-1 packed-int4 x int8 GEMV for gfx950, with the
+// per-token int8 activation quantization (and optionally the RMSNorm in
+// front of it) fused into the prologue and the residual add, SwiGLU or
+// argmax fused into the epilogue.
+//
+// Restates cpu_kernels/litespark_int4.cpp:22-76 (reference repository):
+// acc[n] = sum_k W[n,k] * x[k] in int32, out[n] = ((float)acc * act) * s[n].
+//
+// Kernel shape (256 threads = 32 lane groups of 8):
+//   * each block owns RB output rows; a row is read by 8*KP lanes
+//     (KP = 32/RB K-parts), each lane loading whole 16-byte chunks
+//     (32 int4 values) with 128-bit loads, so the 8 lanes of a group read
+//     128 contiguous bytes of one row;
+//   * all weight loads of a lane are issued before the activation prologue,
+//     so the HBM stream is in flight while the block quantizes x;
+//   * the prologue writes x as int8 into LDS, de-interleaved per 8 columns
+//     (4 even columns, then 4 odd) to match the nibble order of a weight
+//     dword;
+//   * nibbles are decoded in registers right before the dot products:
+//     for a weight dword w, (w << 4) & 0xF0F0F0F0 holds 16*low nibbles and
+//     w & 0xF0F0F0F0 holds 16*high nibbles as signed bytes, so two
+//     v_dot4_i32_i8 give 16 * sum(w*x) exactly; the 8-lane xor reduction
+//     and a shift by 4 give the int32 accumulator (|16*acc| < 2^31 for
+//     K <= 9728*2 with |w| <= 7, |x| <= 127).
+#include "hq_device.h"
+#include "hq_internal.h"
+
+namespace hq {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Weights are read exactly once per step: stream them past the caches.
+__device__ __forceinline__ uint4 load_w16(const uint8_t* p)
+{
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ int dot_chunk(uint4 w, const uint8_t* xs_chunk, int acc)
+{
+    const uint4 xa = *reinterpret_cast<const uint4*>(xs_chunk);
+    const uint4 xb = *reinterpret_cast<const uint4*>(xs_chunk + 16);
+    const int m = int(0xF0F0F0F0u);
+    acc = __builtin_amdgcn_sdot4(int(w.x << 4) & m, int(xa.x), acc, false);
+    acc = __builtin_amdgcn_sdot4(int(w.x) & m, int(xa.y), acc, false);
+    acc = __builtin_amdgcn_sdot4(int(w.y << 4) & m, int(xa.z), acc, false);
+    acc = __builtin_amdgcn_sdot4(int(w.y) & m, int(xa.w), acc, false);
+    acc = __builtin_amdgcn_sdot4(int(w.z << 4) & m, int(xb.x), acc, false);
+    acc = __builtin_amdgcn_sdot4(int(w.z) & m, int(xb.y), acc, false);
+    acc = __builtin_amdgcn_sdot4(int(w.w << 4) & m, int(xb.z), acc, false);
+    acc = __builtin_amdgcn_sdot4(int(w.w) & m, int(xb.w), acc, false);
+    return acc;
+}
+
+// Activation prologue: fills xs (width bytes, de-interleaved int8) and
+// returns the act scale.  Element i is handled by thread i % 256, which for
+// PRO_RMSNORM is exactly the spec's 256-lane partial sum of squares.
+template <int XJ, int PRO>
+__device__ __forceinline__ float activation_prologue(const GemvParams& p, uint8_t* xs,
+                                                     float* red)
+{
+    const int tid = threadIdx.x;
+    const int K = p.width;
+    if constexpr (PRO == PRO_I8) {
+        for (int i = tid; i < K; i += kBlock) {
+            const int8_t q = p.xq[i];
+            xs[xq_offset(i)] = uint8_t(q);
+        }
+        return p.act_scale;
+    } else {
+        float xr[XJ];
+#pragma unroll
+        for (int j = 0; j < XJ; ++j) {
+            const int i = tid + kBlock * j;
+            xr[j] = (i < K) ? p.xf[i] : 0.0f;
+        }
+        if constexpr (PRO == PRO_RMSNORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < XJ; ++j)
+                if (tid + kBlock * j < K) ss = __builtin_fmaf(xr[j], xr[j], ss);
+            const float total = block_tree_sum256(ss, red);
+            const float ms = total / float(K);
+            const float r = __builtin_sqrtf(ms + p.eps);
+#pragma unroll
+            for (int j = 0; j < XJ; ++j) {
+                const int i = tid + kBlock * j;
+                if (i < K) xr[j] = (xr[j] / r) * p.gamma[i];
+            }
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < XJ; ++j) amax = fmaxf(amax, fabsf(xr[j]));
+        amax = block_max_nonneg(amax, red);
+        amax = fmaxf(amax, 1e-5f);
+        const float inv = 127.0f / amax;
+        const bool write_q = p.q_out != nullptr && blockIdx.x == 0;
+#pragma unroll
+        for (int j = 0; j < XJ; ++j) {
+            const int i = tid + kBlock * j;
+            if (i < K) {
+                const int8_t q = quant_i8(xr[j], inv);
+                xs[xq_offset(i)] = uint8_t(q);
+                if (write_q) p.q_out[i] = q;
+            }
+        }
+        const float act = amax / 127.0f;
+        if (p.act_out != nullptr && blockIdx.x == 0 && tid == 0) *p.act_out = act;
+        return act;
+    }
+}
+
+template <int RB, int MAXC, int XJ, int PRO, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
+{
+    constexpr int KP = 32 / RB;
+    constexpr int LPR = 8 * KP;
+    extern __shared__ __align__(16) uint8_t xs[];
+    __shared__ float red[kBlock];
+    __shared__ int part[32];
+    __shared__ int accs[32];
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x;
+    const int grp = tid >> 3;
+    const int li = tid & 7;
+    const int slot = grp % RB;
+    const int kp = grp / RB;
+    const int lir = kp * 8 + li;
+    const int K = p.width;
+    const int nchunks = K >> 5;
+
+    int row;
+    bool valid;
+    if constexpr (EPI == EPI_SWIGLU) {
+        constexpr int HALF = RB / 2;
+        const int pair = blockIdx.x * HALF + (slot % HALF);
+        valid = pair < p.half_rows;
+        row = (slot < HALF) ? pair : p.half_rows + pair;
+    } else {
+        row = blockIdx.x * RB + slot;
+        valid = row < p.rows;
+    }
+    const uint8_t* wrow = p.w + size_t(valid ? row : 0) * size_t(K >> 1);
+
+    // 1. first batch of weight loads (in flight during the prologue)
+    uint4 wv[MAXC];
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lir + j * LPR;
+        wv[j] = (valid && c < nchunks) ? load_w16(wrow + size_t(c) * 16) : make_uint4(0, 0, 0, 0);
+    }
+
+    // 2. activations -> LDS
+    const float act = activation_prologue<XJ, PRO>(p, xs, red);
+    __syncthreads();
+
+    // 3. int4 x int8 dot products
+    int acc16 = 0;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lir + j * LPR;
+        if (c < nchunks) acc16 = dot_chunk(wv[j], xs + c * 32, acc16);
+    }
+    for (int base = MAXC * LPR; base < nchunks; base += MAXC * LPR) {
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j) {
+            const int c = base + lir + j * LPR;
+            wv[j] = (valid && c < nchunks) ? load_w16(wrow + size_t(c) * 16) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j) {
+            const int c = base + lir + j * LPR;
+            if (c < nchunks) acc16 = dot_chunk(wv[j], xs + c * 32, acc16);
+        }
+    }
+    acc16 = isum<8>(acc16);
+    if (li == 0) part[grp] = acc16 >> 4;
+    __syncthreads();
+    if (tid < RB) {
+        int a = 0;
+#pragma unroll
+        for (int k = 0; k < KP; ++k) a += part[tid + RB * k];
+        accs[tid] = a;
+    }
+    __syncthreads();
+
+    // 4. epilogue
+    if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
+        if (tid < RB) {
+            const int r = blockIdx.x * RB + tid;
+            if (r < p.rows) {
+                const int a = accs[tid];
+                const float v = (float(a) * act) * p.ws[r];
+                if (p.acc_out) p.acc_out[r] = a;
+                if constexpr (EPI == EPI_STORE) {
+                    p.out[r] = v;
+                } else {
+                    if (p.out_aux) p.out_aux[r] = v;
+                    p.out[r] = p.out[r] + v;
+                }
+            }
+        }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        constexpr int HALF = RB / 2;
+        if (tid < HALF) {
+            const int pair = blockIdx.x * HALF + tid;
+            if (pair < p.half_rows) {
+                const int gr = pair, ur = p.half_rows + pair;
+                const float g = (float(accs[tid]) * act) * p.ws[gr];
+                const float u = (float(accs[tid + HALF]) * act) * p.ws[ur];
+                if (p.acc_out) { p.acc_out[gr] = accs[tid]; p.acc_out[ur] = accs[tid + HALF]; }
+                if (p.out_aux) { p.out_aux[gr] = g; p.out_aux[ur] = u; }
+                const float t = 1.0f + spec_expf(-g);
+                p.out[pair] = (g / t) * u;
+            }
+        }
+    } else {  // EPI_ARGMAX
+        if (tid < kWave) {
+            float v = -__builtin_inff();
+            int idx = 0x7FFFFFFF;
+            if (tid < RB) {
+                const int r = blockIdx.x * RB + tid;
+                if (r < p.rows) {
+                    v = (float(accs[tid]) * act) * p.ws[r];
+                    idx = r;
+                    p.out[r] = v;
+                    if (p.acc_out) p.acc_out[r] = accs[tid];
+                }
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float ov = __shfl_xor(v, o, kWave);
+                const int oi = __shfl_xor(idx, o, kWave);
+                if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
+            }
+            if (tid == 0) {
+                p.part_val[blockIdx.x] = v;
+                p.part_idx[blockIdx.x] = idx;
+                __threadfence();
+                const int ticket = atomicAdd(p.counter, 1);
+                last_flag = (ticket == int(gridDim.x) - 1);
+            }
+        }
+        __syncthreads();
+        if (last_flag) {
+            __threadfence();
+            float v = -__builtin_inff();
+            int idx = 0x7FFFFFFF;
+            for (int b = tid; b < int(gridDim.x); b += kBlock) {
+                const float bv = __hip_atomic_load(p.part_val + b, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                const int bi = __hip_atomic_load(p.part_idx + b, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+                if (argmax_better(bv, bi, v, idx)) { v = bv; idx = bi; }
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float ov = __shfl_xor(v, o, kWave);
+                const int oi = __shfl_xor(idx, o, kWave);
+                if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
+            }
+            if ((tid & (kWave - 1)) == 0) { red[tid / kWave] = v; part[tid / kWave] = idx; }
+            __syncthreads();
+            if (tid == 0) {
+#pragma unroll
+                for (int w = 1; w < kBlock / kWave; ++w)
+                    if (argmax_better(red[w], part[w], v, idx)) { v = red[w]; idx = part[w]; }
+                *p.token = idx;
+                *p.position = *p.position + 1;
+                *p.counter = 0;
+            }
+        }
+    }
+}
+
+// Plain fallback for the reference-signature entry when the fast path's
+// layout conditions (width % 32 == 0, 16-byte aligned rows) do not hold:
+// one wave per row, byte loads, same integer result and epilogue.
+__global__ __launch_bounds__(kBlock) void gemv_generic_kernel(
+    const int8_t* x, const uint8_t* w, const float* ws, float act, float* out, int rows,
+    int width, int32_t* acc_out)
+{
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * (kBlock / kWave) + wave;
+    if (row >= rows) return;
+    const int half = width >> 1;
+    const uint8_t* wr = w + size_t(row) * size_t(half);
+    int acc = 0;
+    for (int j = lane; j < half; j += kWave) {
+        const uint8_t b = wr[j];
+        const int lo = int(int8_t(uint8_t(b << 4))) >> 4;
+        const int hi = int(int8_t(b)) >> 4;
+        acc += lo * int(x[2 * j]) + hi * int(x[2 * j + 1]);
+    }
+    acc = isum<kWave>(acc);
+    if (lane == 0) {
+        out[row] = (float(acc) * act) * ws[row];
+        if (acc_out) acc_out[row] = acc;
+    }
+}
+
+// Single-block spec quantizer (hq_quantize_activation).
+__global__ __launch_bounds__(kBlock) void quantize_kernel(const float* x, int n, int8_t* q,
+                                                          float* act_out)
+{
+    __shared__ float red[4];
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kBlock) amax = fmaxf(amax, fabsf(x[i]));
+    amax = block_max_nonneg(amax, red);
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+    for (int i = threadIdx.x; i < n; i += kBlock) q[i] = quant_i8(x[i], inv);
+    if (threadIdx.x == 0) *act_out = amax / 127.0f;
+}
+
+// Single-block spec RMSNorm (hq_rmsnorm): 256-lane fmaf partials, tree.
+__global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* x, const float* gamma,
+                                                         float* y, int n, float eps)
+{
+    __shared__ float red[kBlock];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kBlock) ss = __builtin_fmaf(x[i], x[i], ss);
+    const float total = block_tree_sum256(ss, red);
+    const float r = __builtin_sqrtf(total / float(n) + eps);
+    for (int i = threadIdx.x; i < n; i += kBlock) y[i] = (x[i] / r) * gamma[i];
+}
+
+// Device argmax with np.argmax's order (hq_argmax): each block reduces 4096
+// values to a (value, index) partial; the last block to arrive reduces the
+// partials, writes the index and re-zeroes its arrival counter.
+constexpr int kArgmaxPerBlock = kBlock * 16;
+
+__global__ __launch_bounds__(kBlock) void argmax_kernel(const float* x, int n, float* pval,
+                                                        int32_t* pidx, int32_t* counter,
+                                                        int32_t* out)
+{
+    __shared__ float sv[kBlock / kWave];
+    __shared__ int si[kBlock / kWave];
+    __shared__ int last_flag;
+    const int tid = threadIdx.x;
+    float v = -__builtin_inff();
+    int idx = 0x7FFFFFFF;
+    const int base = blockIdx.x * kArgmaxPerBlock;
+    for (int i = base + tid; i < min(n, base + kArgmaxPerBlock); i += kBlock)
+        if (argmax_better(x[i], i, v, idx)) { v = x[i]; idx = i; }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o, kWave);
+        const int oi = __shfl_xor(idx, o, kWave);
+        if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
+    }
+    if ((tid & (kWave - 1)) == 0) { sv[tid / kWave] = v; si[tid / kWave] = idx; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kBlock / kWave; ++w)
+            if (argmax_better(sv[w], si[w], v, idx)) { v = sv[w]; idx = si[w]; }
+        pval[blockIdx.x] = v;
+        pidx[blockIdx.x] = idx;
+        __threadfence();
+        last_flag = (atomicAdd(counter, 1) == int(gridDim.x) - 1);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+    v = -__builtin_inff();
+    idx = 0x7FFFFFFF;
+    for (int b = tid; b < int(gridDim.x); b += kBlock) {
+        const float bv = __hip_atomic_load(pval + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int bi = __hip_atomic_load(pidx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (argmax_better(bv, bi, v, idx)) { v = bv; idx = bi; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o, kWave);
+        const int oi = __shfl_xor(idx, o, kWave);
+        if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
+    }
+    __syncthreads();
+    if ((tid & (kWave - 1)) == 0) { sv[tid / kWave] = v; si[tid / kWave] = idx; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kBlock / kWave; ++w)
+            if (argmax_better(sv[w], si[w], v, idx)) { v = sv[w]; idx = si[w]; }
+        *out = idx;
+        *counter = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host-side dispatch
+// ---------------------------------------------------------------------------
+template <int RB, int MAXC, int XJ, int PRO, int EPI>
+static hipError_t launch(const GemvParams& p, int blocks, hipStream_t s)
+{
+    hipLaunchKernelGGL((gemv_kernel<RB, MAXC, XJ, PRO, EPI>), dim3(blocks), dim3(kBlock),
+                       size_t(p.width), s, p);
+    return hipGetLastError();
+}
+
+// XJ (register-resident activations per thread) is picked from the width.
+template <int RB, int MAXC, int PRO, int EPI>
+static hipError_t launch_xj(const GemvParams& p, int blocks, hipStream_t s)
+{
+    if (PRO == PRO_I8) return launch<RB, MAXC, 1, PRO, EPI>(p, blocks, s);
+    if (p.width <= 10 * kBlock) return launch<RB, MAXC, 10, PRO, EPI>(p, blocks, s);
+    if (p.width <= 16 * kBlock) return launch<RB, MAXC, 16, PRO, EPI>(p, blocks, s);
+    return launch<RB, MAXC, 40, PRO, EPI>(p, blocks, s);
+}
+
+constexpr int kMaxWidth = 40 * kBlock;   // 10240: register-resident activation limit
+
+int step_gemv_blocks(StepGemv kind, int rows, int half_rows)
+{
+    switch (kind) {
+    case StepGemv::Qkv: return (rows + 15) / 16;
+    case StepGemv::OResidual: return (rows + 7) / 8;
+    case StepGemv::GateUpSwiglu: return (half_rows + 15) / 16;
+    case StepGemv::DownResidual: return (rows + 7) / 8;
+    case StepGemv::LmHead: return (rows + 31) / 32;
+    }
+    return 0;
+}
+
+hipError_t launch_step_gemv(StepGemv kind, const GemvParams& p, hipStream_t s)
+{
+    const int blocks = step_gemv_blocks(kind, p.rows, p.half_rows);
+    switch (kind) {
+    case StepGemv::Qkv: return launch_xj<16, 5, PRO_RMSNORM, EPI_STORE>(p, blocks, s);
+    case StepGemv::OResidual: return launch_xj<8, 4, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
+    case StepGemv::GateUpSwiglu: return launch_xj<32, 10, PRO_RMSNORM, EPI_SWIGLU>(p, blocks, s);
+    case StepGemv::DownResidual: return launch_xj<8, 10, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
+    case StepGemv::LmHead: return launch_xj<32, 10, PRO_RMSNORM, EPI_ARGMAX>(p, blocks, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace hq
+
+using namespace hq;
+
+extern "C" int hq_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const float* scales,
+                               float activation_scale, float* output, int rows, int width,
+                               void* stream)
+{
+    if (rows < 0 || width <= 0 || (width & 1)) return HQ_ERR_ARG;
+    if (rows == 0) return HQ_OK;
+    if (!x || !weights || !scales || !output) return HQ_ERR_ARG;
+    if (width > 32768) return HQ_ERR_ARG;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if ((width & 31) == 0 && aligned16(weights)) {
+        GemvParams p{};
+        p.w = weights; p.ws = scales; p.rows = rows; p.width = width;
+        p.xq = x; p.act_scale = activation_scale; p.out = output;
+        const int rb = rows >= 4096 ? 32 : 8;
+        e = rb == 32 ? launch<32, 8, 1, PRO_I8, EPI_STORE>(p, (rows + 31) / 32, s)
+                     : launch<8, 8, 1, PRO_I8, EPI_STORE>(p, (rows + 7) / 8, s);
+    } else {
+        const int per = kBlock / kWave;
+        hipLaunchKernelGGL(gemv_generic_kernel, dim3((rows + per - 1) / per), dim3(kBlock), 0, s,
+                           x, weights, scales, activation_scale, output, rows, width,
+                           static_cast<int32_t*>(nullptr));
+        e = hipGetLastError();
+    }
+    return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+extern "C" int hq_quant_int4_gemv(const float* x, const uint8_t* weights, const float* scales,
+                                  float* output, int rows, int width, int8_t* q_out,
+                                  float* act_scale_out, int32_t* acc_out, void* stream)
+{
+    if (rows < 0 || width <= 0 || (width & 1)) return HQ_ERR_ARG;
+    if (rows == 0) return HQ_OK;
+    if (!x || !weights || !scales || !output) return HQ_ERR_ARG;
+    if (width > kMaxWidth) return HQ_ERR_ARG;
+    if ((width & 31) != 0 || !aligned16(weights)) return HQ_ERR_ALIGN;
+    GemvParams p{};
+    p.w = weights; p.ws = scales; p.rows = rows; p.width = width;
+    p.xf = x; p.out = output; p.q_out = q_out; p.act_out = act_scale_out; p.acc_out = acc_out;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (rows >= 8192)
+        e = launch_xj<32, 10, PRO_QUANT, EPI_STORE>(p, (rows + 31) / 32, s);
+    else if (rows >= 4096)
+        e = launch_xj<16, 10, PRO_QUANT, EPI_STORE>(p, (rows + 15) / 16, s);
+    else
+        e = launch_xj<8, 10, PRO_QUANT, EPI_STORE>(p, (rows + 7) / 8, s);
+    return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+extern "C" int hq_quantize_activation(const float* x, int n, int8_t* q, float* act_scale,
+                                      void* stream)
+{
+    if (n <= 0 || !x || !q || !act_scale) return HQ_ERR_ARG;
+    hipLaunchKernelGGL(quantize_kernel, dim3(1), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), x, n, q, act_scale);
+    return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+extern "C" int hq_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps,
+                          void* stream)
+{
+    if (n <= 0 || !x || !gamma || !y) return HQ_ERR_ARG;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), x, gamma, y, n, eps);
+    return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+extern "C" size_t hq_argmax_workspace_bytes(int n)
+{
+    if (n <= 0) return 0;
+    const size_t blocks = (size_t(n) + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
+    return 256 + blocks * 8;   // counter first (fixed place), then the partials
+}
+
+extern "C" int hq_argmax(const float* x, int n, int32_t* out_index, void* workspace, void* stream)
+{
+    if (n <= 0 || !x || !out_index || !workspace) return HQ_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return HQ_ERR_ALIGN;
+    const int blocks = (n + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
+    char* ws = static_cast<char*>(workspace);
+    int32_t* counter = reinterpret_cast<int32_t*>(ws);
+    float* pval = reinterpret_cast<float*>(ws + 256);
+    int32_t* pidx = reinterpret_cast<int32_t*>(ws + 256 + size_t(blocks) * 4);
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), x, n, pval, pidx, counter, out_index);
+    return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}

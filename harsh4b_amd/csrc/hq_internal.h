@@ -1,0 +1,73 @@
+// hq_internal.h - launch interfaces shared by the translation units of libhq.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hq.h"
+
+namespace hq {
+
+// ---- GEMV ------------------------------------------------------------------
+enum Prologue { PRO_I8 = 0, PRO_QUANT = 1, PRO_RMSNORM = 2 };
+enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+
+struct GemvParams {
+    const uint8_t* w;       // [rows, width/2] packed int4
+    const float* ws;        // [rows] row scales
+    int rows;               // output rows (EPI_SWIGLU: 2 * half_rows)
+    int width;              // K
+    const float* xf;        // fp32 activations (PRO_QUANT, PRO_RMSNORM)
+    const int8_t* xq;       // int8 activations (PRO_I8)
+    float act_scale;        // PRO_I8 multiplier
+    const float* gamma;     // PRO_RMSNORM weight [width]
+    float eps;
+    float* out;             // STORE/ARGMAX: [rows]; RESIDUAL: x += ; SWIGLU: [half_rows]
+    float* out_aux;         // nullable: RESIDUAL projection [rows]; SWIGLU gate|up [rows]
+    int32_t* acc_out;       // nullable: int32 accumulators [rows]
+    int8_t* q_out;          // nullable: quantized activations [width] (block 0)
+    float* act_out;         // nullable: act scale [1] (block 0)
+    int half_rows;          // EPI_SWIGLU
+    float* part_val;        // EPI_ARGMAX partials [blocks]
+    int32_t* part_idx;
+    int32_t* counter;       // EPI_ARGMAX arrival counter (zero between launches)
+    int32_t* token;         // EPI_ARGMAX result
+    int32_t* position;      // EPI_ARGMAX: advanced by one
+};
+
+enum class StepGemv { Qkv, OResidual, GateUpSwiglu, DownResidual, LmHead };
+
+// Number of blocks a step GEMV launches (sizes the argmax partials).
+int step_gemv_blocks(StepGemv kind, int rows, int half_rows);
+hipError_t launch_step_gemv(StepGemv kind, const GemvParams& p, hipStream_t s);
+
+// ---- attention ---------------------------------------------------------------
+constexpr int kAttnChunk = 64;   // positions per split (the spec's chunk)
+
+struct AttnParams {
+    // PLAIN mode: q given; STEP mode: raw qkv + norms + rope + KV write
+    const float* q;             // PLAIN: [kv*groups, D]
+    const float* qkv;           // STEP: [(heads + 2*kv) * D]
+    const float* q_norm;        // STEP
+    const float* k_norm;        // STEP
+    const float* rope_cos;      // STEP [positions, D/2]
+    const float* rope_sin;
+    float eps;
+    uint16_t* keys;             // fp16 cache base of this layer
+    uint16_t* values;
+    long long time_stride;      // elements between consecutive positions
+    const int32_t* position;    // STEP: device position (context = pos + 1)
+    int32_t capacity;           // STEP: bound for the KV write
+    int32_t* status;            // STEP: error flag
+    int context;                // PLAIN
+    int kv_heads, groups, head_dim;
+    int max_chunks;             // grid.y
+    float* part;                // [heads, max_chunks, head_dim + 2]
+    int32_t* counters;          // [kv_heads], zero between launches
+    float* out;                 // [heads, D]
+};
+
+size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);
+hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s);
+
+}  // namespace hq

@@ -1,0 +1,463 @@
+"""MI355X decode runtime with the call surface of cpu_lightspark.py.
+
+Mirrors the reference's decode path (cpu_lightspark.py in the reference
+repository) on one gfx950 GPU:
+
+  reference (CPU, numpy + ctypes)          here (HIP via libhq.so + torch plumbing)
+  _pack_int4                 :139-146      pack_int4 (same layout, same errors)
+  LiteSparkProjection        :246-260      LiteSparkProjection (device buffers)
+  combine                    :638-645      combine
+  QwenLayer                  :263-272      QwenLayer
+  QwenDecodeState            :275-309      QwenDecodeState (fp16 KV cache on HBM)
+  LiteSparkQwen.__init__     :315-336      LiteSparkQwen (RoPE tables as :329-336)
+  new_state / forward_token  :338, :424    new_state / forward_token
+  _projection                :351-371      _projection (hq_int4_i8_gemv)
+  _attention                 :389-422      _attention (hq_gqa_decode)
+  sample_logits (argmax)     :700-705      sample_logits (argmax branch)
+
+All arithmetic runs in libhq.so; torch only allocates device memory and
+provides the stream.  There is no CPU fallback: a missing library or GPU is
+an error.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _native
+from ._native import HqLayer, HqModel, HqState, check
+
+DEFAULT_GEMV_KERNEL = "hip-gfx950"
+
+
+# --------------------------------------------------------------------------- A1
+def pack_int4(weights: np.ndarray) -> np.ndarray:
+    """Pack signed [-7,+7] values as low/high nibbles (cpu_lightspark.py:139-146)."""
+    if weights.dtype != np.int8 or weights.ndim != 2 or weights.shape[1] % 2:
+        raise ValueError("int4 matrix must be int8 with even width")
+    if np.any(weights < -7) or np.any(weights > 7):
+        raise ValueError("int4 values must be in [-7,+7]")
+    return ((weights[:, 0::2].view(np.uint8) & 15)
+            | ((weights[:, 1::2].view(np.uint8) & 15) << 4))
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("harsh4b_amd needs a ROCm GPU (gfx950); none is visible")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream_handle(stream: torch.cuda.Stream | None) -> int | None:
+    return None if stream is None else stream.cuda_stream
+
+
+# --------------------------------------------------------------------------- A4
+@dataclass(frozen=True)
+class LiteSparkProjection:
+    """One row-scaled int4 matrix held on the device (cpu_lightspark.py:246-260)."""
+
+    weights: torch.Tensor          # uint8 [rows, width/2]
+    scales: torch.Tensor           # float32 [rows]
+    layout: str = "int4"
+
+    def __post_init__(self):
+        if self.layout != "int4":
+            raise ValueError("only the packed int4 layout is supported on the GPU")
+        w, s = self.weights, self.scales
+        if w.dtype != torch.uint8 or w.ndim != 2 or not w.is_cuda or not w.is_contiguous():
+            raise ValueError("weights must be a contiguous uint8 [rows, width/2] device tensor")
+        if s.dtype != torch.float32 or s.shape != (w.shape[0],) or not s.is_cuda:
+            raise ValueError("scales must be a float32 [rows] device tensor")
+
+    @property
+    def input_size(self) -> int:
+        return self.weights.shape[1] * 2
+
+    @property
+    def output_size(self) -> int:
+        return self.weights.shape[0]
+
+
+def combine(*projections: LiteSparkProjection) -> LiteSparkProjection:
+    """Concatenate rows of projections sharing an input (cpu_lightspark.py:638-645)."""
+    if len({item.input_size for item in projections}) != 1:
+        raise ValueError("cannot fuse LiteSpark projections with different input widths")
+    return LiteSparkProjection(
+        torch.cat([item.weights for item in projections], dim=0).contiguous(),
+        torch.cat([item.scales for item in projections]).contiguous(),
+        projections[0].layout,
+    )
+
+
+@dataclass(frozen=True)
+class QwenLayer:
+    qkv: LiteSparkProjection
+    o: LiteSparkProjection
+    gate_up: LiteSparkProjection
+    down: LiteSparkProjection
+    input_norm: torch.Tensor
+    post_norm: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+
+
+def rope_tables(config: dict) -> tuple[np.ndarray, np.ndarray]:
+    """cos/sin [max_position_embeddings, head_dim/2] exactly as cpu_lightspark.py:329-336."""
+    head_dim = int(config["head_dim"])
+    positions = np.arange(int(config["max_position_embeddings"]), dtype=np.float32)[:, None]
+    inv_freq = np.float32(1.0) / np.float32(config["rope_theta"]) ** (
+        np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim)
+    )
+    angles = positions * inv_freq[None, :]
+    return np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
+
+
+# --------------------------------------------------------------------------- A9
+class QwenDecodeState:
+    """Caller-owned device state for one sequence (cpu_lightspark.py:275-309).
+
+    The KV cache is fp16 [layers, capacity, kv_heads, head_dim] (the reference
+    keeps fp32; the benchmark configurations specify fp16).  Position and the
+    current token also live on the device so a captured HIP graph of a step is
+    valid at every position; ``position`` here is the host's mirror of it.
+    """
+
+    def __init__(self, model: "LiteSparkQwen", capacity: int):
+        if capacity < 1:
+            raise ValueError("decode capacity must be positive")
+        c = model.config
+        dev = model.device
+        layers = int(c["num_hidden_layers"])
+        hidden = int(c["hidden_size"])
+        intermediate = int(c["intermediate_size"])
+        heads = int(c["num_attention_heads"])
+        kv_heads = int(c["num_key_value_heads"])
+        head_dim = int(c["head_dim"])
+        if capacity > model.rope_positions:
+            raise ValueError("decode capacity exceeds max_position_embeddings")
+        self.model = model
+        self.capacity = capacity
+        self.position = 0
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.keys = torch.zeros((layers, capacity, kv_heads, head_dim), dtype=torch.float16, device=dev)
+        self.values = torch.zeros_like(self.keys)
+        self.device_position = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.x = torch.zeros(hidden, **f32)
+        q_size, kv_size = heads * head_dim, kv_heads * head_dim
+        self.qkv = torch.zeros(q_size + 2 * kv_size, **f32)
+        self.q = self.qkv[:q_size].view(heads, head_dim)
+        self.k = self.qkv[q_size:q_size + kv_size].view(kv_heads, head_dim)
+        self.v = self.qkv[q_size + kv_size:].view(kv_heads, head_dim)
+        self.attended = torch.zeros(q_size, **f32)
+        self.activated = torch.zeros(intermediate, **f32)
+        self.logits = torch.zeros(int(c["vocab_size"]), **f32)
+        nbytes = _native.lib().hq_step_workspace_bytes(ctypes.byref(model.struct), capacity)
+        if nbytes == 0:
+            raise ValueError("model shape is not supported by the decode step")
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        self.stream = torch.cuda.Stream(device=dev)
+        self.stream.wait_stream(torch.cuda.current_stream(dev))
+        s = HqState()
+        s.capacity = capacity
+        s.keys, s.values = self.keys.data_ptr(), self.values.data_ptr()
+        s.position, s.token, s.status = (self.device_position.data_ptr(), self.token.data_ptr(),
+                                         self.status.data_ptr())
+        s.x, s.qkv, s.attended = self.x.data_ptr(), self.qkv.data_ptr(), self.attended.data_ptr()
+        s.activated, s.logits = self.activated.data_ptr(), self.logits.data_ptr()
+        s.workspace = self.workspace.data_ptr()
+        self.struct = s
+        self._graph = None
+
+    def synchronize(self) -> None:
+        self.stream.synchronize()
+
+    def check_status(self) -> None:
+        self.synchronize()
+        code = int(self.status.item())
+        if code & _native.HQ_STEP_BAD_TOKEN:
+            raise ValueError("a token ID outside the vocabulary reached the device")
+        if code & _native.HQ_STEP_FULL:
+            raise ValueError("decode state capacity exhausted")
+
+    def close(self) -> None:
+        if self._graph is not None:
+            _native.lib().hq_graph_destroy(self._graph)
+            self._graph = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# --------------------------------------------------------------------------- A12
+class LiteSparkQwen:
+    """Qwen3 decode runtime on one MI355X (cpu_lightspark.py:312-468)."""
+
+    def __init__(self, config: dict, layers: list[QwenLayer], embedding: torch.Tensor,
+                 embedding_scales: torch.Tensor, final_norm: torch.Tensor,
+                 gemv_kernel: str = DEFAULT_GEMV_KERNEL):
+        self.device = _device()
+        _native.lib()
+        self.config = config
+        self.layers = layers
+        self.embedding = embedding
+        self.embedding_scales = embedding_scales
+        self.lm_head = LiteSparkProjection(embedding, embedding_scales)
+        self.final_norm = final_norm
+        self.gemv_kernel = gemv_kernel
+        cos, sin = rope_tables(config)
+        self.rope_cos_host, self.rope_sin_host = cos, sin
+        self.rope_cos = torch.from_numpy(cos).to(self.device)
+        self.rope_sin = torch.from_numpy(sin).to(self.device)
+        self.rope_positions = cos.shape[0]
+        n = int(config["num_hidden_layers"])
+        if len(layers) != n:
+            raise ValueError(f"expected {n} layers, found {len(layers)}")
+        self._layer_structs = (HqLayer * n)()
+        for i, layer in enumerate(layers):
+            ls = self._layer_structs[i]
+            for name in ("qkv", "o", "gate_up", "down"):
+                proj = getattr(layer, name)
+                setattr(ls, name, proj.weights.data_ptr())
+                setattr(ls, name + "_scales", proj.scales.data_ptr())
+            for name in ("input_norm", "post_norm", "q_norm", "k_norm"):
+                setattr(ls, name, getattr(layer, name).data_ptr())
+        m = HqModel()
+        m.layers = n
+        m.hidden = int(config["hidden_size"])
+        m.intermediate = int(config["intermediate_size"])
+        m.heads = int(config["num_attention_heads"])
+        m.kv_heads = int(config["num_key_value_heads"])
+        m.head_dim = int(config["head_dim"])
+        m.vocab = int(config["vocab_size"])
+        m.rope_positions = self.rope_positions
+        m.eps = float(config["rms_norm_eps"])
+        m.layer = self._layer_structs
+        m.embedding = embedding.data_ptr()
+        m.embedding_scales = embedding_scales.data_ptr()
+        m.final_norm = final_norm.data_ptr()
+        m.rope_cos = self.rope_cos.data_ptr()
+        m.rope_sin = self.rope_sin.data_ptr()
+        self.struct = m
+
+    def new_state(self, capacity: int) -> QwenDecodeState:
+        return QwenDecodeState(self, capacity)
+
+    # -- one step -------------------------------------------------------------
+    def _check_token(self, token_id: int, state: QwenDecodeState) -> None:
+        if state.position >= state.capacity:
+            raise ValueError("decode state capacity exhausted")
+        if token_id < 0 or token_id >= int(self.config["vocab_size"]):
+            raise ValueError(f"token ID {token_id} is outside the vocabulary")
+
+    def forward_token(self, token_id: int, state: QwenDecodeState) -> torch.Tensor:
+        """Consume one token and return its next-token logits (device tensor).
+
+        The step is enqueued on ``state.stream``; the greedy (argmax) token
+        of the logits is written to ``state.token`` by the same step.
+        """
+        self._check_token(token_id, state)
+        with torch.cuda.stream(state.stream):
+            state.token.fill_(int(token_id))
+        check(_native.lib().hq_decode_step(ctypes.byref(self.struct), ctypes.byref(state.struct),
+                                           state.stream.cuda_stream), "hq_decode_step")
+        state.position += 1
+        return state.logits
+
+    def greedy_token(self, state: QwenDecodeState) -> int:
+        state.synchronize()
+        return int(state.token.item())
+
+    def decode_greedy(self, state: QwenDecodeState, steps: int, use_graph: bool = True) -> None:
+        """Run `steps` greedy steps feeding each argmax token back on the device
+        (the token already in ``state.token`` is consumed first)."""
+        if state.position + steps > state.capacity:
+            raise ValueError("decode state capacity exhausted")
+        lib = _native.lib()
+        if use_graph:
+            if state._graph is None:
+                handle = ctypes.c_void_p()
+                check(lib.hq_graph_capture(ctypes.byref(self.struct), ctypes.byref(state.struct), 1,
+                                           state.stream.cuda_stream, ctypes.byref(handle)),
+                      "hq_graph_capture")
+                state._graph = handle.value
+            for _ in range(steps):
+                check(lib.hq_graph_launch(state._graph, state.stream.cuda_stream), "hq_graph_launch")
+        else:
+            for _ in range(steps):
+                check(lib.hq_decode_step(ctypes.byref(self.struct), ctypes.byref(state.struct),
+                                         state.stream.cuda_stream), "hq_decode_step")
+        state.position += steps
+
+    # -- the reference's per-op surface ---------------------------------------
+    def _projection(self, projection: LiteSparkProjection, values, quantized: torch.Tensor,
+                    activation_scale: float, out: torch.Tensor,
+                    stream: torch.cuda.Stream | None = None) -> None:
+        """int8 activations x packed int4 weights (cpu_lightspark.py:351-371)."""
+        if quantized.dtype != torch.int8 or quantized.numel() < projection.input_size:
+            raise ValueError("quantized activations must be int8 [input_size]")
+        if out.dtype != torch.float32 or out.numel() < projection.output_size:
+            raise ValueError("output must be float32 [output_size]")
+        check(_native.lib().hq_int4_i8_gemv(
+            quantized.data_ptr(), projection.weights.data_ptr(), projection.scales.data_ptr(),
+            float(activation_scale), out.data_ptr(), projection.output_size, projection.input_size,
+            _stream_handle(stream)), "hq_int4_i8_gemv")
+
+    def _attention(self, state: QwenDecodeState, layer_index: int) -> None:
+        """GQA over the state's cache up to its position (cpu_lightspark.py:389-422),
+        from ``state.q`` into ``state.attended``."""
+        c = self.config
+        kv_heads = int(c["num_key_value_heads"])
+        groups = int(c["num_attention_heads"]) // kv_heads
+        head_dim = int(c["head_dim"])
+        end = state.position + 1
+        gqa_decode(state.q, state.keys[layer_index], state.values[layer_index],
+                   state.attended.view(-1, head_dim), end, kv_heads, groups, head_dim,
+                   stream=state.stream)
+
+
+def sample_logits(logits, generated, args, generator=None) -> int:
+    """Greedy branch of cpu_lightspark.py:700-705 (first maximal index).
+
+    The stochastic branch (:706-726) is not part of this GPU path.
+    """
+    if not getattr(args, "argmax", False):
+        raise NotImplementedError("only greedy (argmax) sampling runs on the GPU path")
+    return argmax(logits)
+
+
+# --------------------------------------------------------------------------- ops
+_workspaces: dict[tuple, torch.Tensor] = {}
+
+
+def _zeroed_workspace(key: tuple, nbytes: int, device) -> torch.Tensor:
+    """A zero-filled device workspace kept for reuse under `key` (the library
+    returns the regions it needs zeroed to zero after every call)."""
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def quant_int4_gemv(x: torch.Tensor, projection: LiteSparkProjection, out: torch.Tensor | None = None,
+                    q_out: torch.Tensor | None = None, act_out: torch.Tensor | None = None,
+                    acc_out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Fused per-token int8 quantization + int4 GEMV (hq_quant_int4_gemv)."""
+    if x.dtype != torch.float32 or x.numel() != projection.input_size or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float32 [input_size] device tensor")
+    if out is None:
+        out = torch.empty(projection.output_size, dtype=torch.float32, device=x.device)
+    check(_native.lib().hq_quant_int4_gemv(
+        x.data_ptr(), projection.weights.data_ptr(), projection.scales.data_ptr(), out.data_ptr(),
+        projection.output_size, projection.input_size, _ptr(q_out), _ptr(act_out), _ptr(acc_out),
+        _stream_handle(stream)), "hq_quant_int4_gemv")
+    return out
+
+
+def int4_i8_gemv(x_q: torch.Tensor, projection: LiteSparkProjection, activation_scale: float,
+                 out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    if out is None:
+        out = torch.empty(projection.output_size, dtype=torch.float32, device=x_q.device)
+    check(_native.lib().hq_int4_i8_gemv(
+        x_q.data_ptr(), projection.weights.data_ptr(), projection.scales.data_ptr(),
+        float(activation_scale), out.data_ptr(), projection.output_size, projection.input_size,
+        _stream_handle(stream)), "hq_int4_i8_gemv")
+    return out
+
+
+def quantize_activation(x: torch.Tensor, q: torch.Tensor | None = None, stream=None):
+    """Per-token int8 quantization on the device; returns (q, act_scale tensor[1])."""
+    if q is None:
+        q = torch.empty(x.numel(), dtype=torch.int8, device=x.device)
+    act = torch.empty(1, dtype=torch.float32, device=x.device)
+    check(_native.lib().hq_quantize_activation(x.data_ptr(), x.numel(), q.data_ptr(), act.data_ptr(),
+                                               _stream_handle(stream)), "hq_quantize_activation")
+    return q, act
+
+
+def rmsnorm(x: torch.Tensor, gamma: torch.Tensor, eps: float, out: torch.Tensor | None = None,
+            stream=None) -> torch.Tensor:
+    if out is None:
+        out = torch.empty_like(x)
+    check(_native.lib().hq_rmsnorm(x.data_ptr(), gamma.data_ptr(), out.data_ptr(), x.numel(), float(eps),
+                                   _stream_handle(stream)), "hq_rmsnorm")
+    return out
+
+
+def gqa_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, out: torch.Tensor,
+               context: int, kv_heads: int, groups: int, head_dim: int, stream=None) -> torch.Tensor:
+    """Fused GQA decode over an fp16 [time, kv_heads, head_dim] cache (hq_gqa_decode)."""
+    if keys.dtype != torch.float16 or values.dtype != torch.float16:
+        raise ValueError("keys/values must be float16")
+    if context < 1 or context > keys.shape[0]:
+        raise ValueError("context outside the cache")
+    lib = _native.lib()
+    nbytes = lib.hq_gqa_workspace_bytes(context, kv_heads, groups, head_dim)
+    ws = _zeroed_workspace(("gqa", query.device.index), nbytes, query.device)
+    check(lib.hq_gqa_decode(query.data_ptr(), keys.data_ptr(), values.data_ptr(), ws.data_ptr(),
+                            out.data_ptr(), context, kv_heads, groups, head_dim,
+                            keys.stride(0), _stream_handle(stream)), "hq_gqa_decode")
+    return out
+
+
+def int4_i8_gemm(x_q: torch.Tensor, act_scales: torch.Tensor, projection: LiteSparkProjection,
+                 out: torch.Tensor | None = None, acc_out: torch.Tensor | None = None,
+                 stream=None) -> torch.Tensor:
+    """M sequences x one int4 matrix on int8 MFMA (hq_int4_i8_gemm)."""
+    m = x_q.shape[0]
+    if out is None:
+        out = torch.empty((m, projection.output_size), dtype=torch.float32, device=x_q.device)
+    lib = _native.lib()
+    nbytes = lib.hq_gemm_workspace_bytes(m, projection.output_size, projection.input_size)
+    ws = _zeroed_workspace(("gemm", x_q.device.index, m, projection.output_size,
+                            projection.input_size), nbytes, x_q.device)
+    check(lib.hq_int4_i8_gemm(x_q.data_ptr(), act_scales.data_ptr(), projection.weights.data_ptr(),
+                              projection.scales.data_ptr(), out.data_ptr(), m, projection.output_size,
+                              projection.input_size, _ptr(acc_out), ws.data_ptr(),
+                              _stream_handle(stream)), "hq_int4_i8_gemm")
+    return out
+
+
+def quant_int4_gemm(x: torch.Tensor, projection: LiteSparkProjection, out: torch.Tensor | None = None,
+                    q_out=None, act_out=None, acc_out=None, stream=None) -> torch.Tensor:
+    """Per-sequence quantization + int4 GEMM on int8 MFMA (hq_quant_int4_gemm)."""
+    m = x.shape[0]
+    if out is None:
+        out = torch.empty((m, projection.output_size), dtype=torch.float32, device=x.device)
+    lib = _native.lib()
+    nbytes = lib.hq_gemm_workspace_bytes(m, projection.output_size, projection.input_size)
+    ws = _zeroed_workspace(("gemm", x.device.index, m, projection.output_size,
+                            projection.input_size), nbytes, x.device)
+    check(lib.hq_quant_int4_gemm(x.data_ptr(), projection.weights.data_ptr(), projection.scales.data_ptr(),
+                                 out.data_ptr(), m, projection.output_size, projection.input_size,
+                                 _ptr(q_out), _ptr(act_out), _ptr(acc_out), ws.data_ptr(),
+                                 _stream_handle(stream)), "hq_quant_int4_gemm")
+    return out
+
+
+def argmax(logits: torch.Tensor, stream=None) -> int:
+    """First maximal index, as np.argmax (cpu_lightspark.py:704-705), on the device."""
+    if logits.dtype != torch.float32 or not logits.is_cuda or not logits.is_contiguous():
+        raise ValueError("logits must be a contiguous float32 device tensor")
+    lib = _native.lib()
+    n = logits.numel()
+    ws = _zeroed_workspace(("argmax", logits.device.index), lib.hq_argmax_workspace_bytes(n),
+                           logits.device)
+    out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    check(lib.hq_argmax(logits.data_ptr(), n, out.data_ptr(), ws.data_ptr(), _stream_handle(stream)),
+          "hq_argmax")
+    if stream is not None:
+        stream.synchronize()
+    return int(out.item())

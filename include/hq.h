@@ -1,0 +1,197 @@
+/*
+ * hq.h - C ABI of libhq.so, the MI355X (gfx950) int4 decode hot path.
+ *
+ * Every entry point takes DEVICE pointers (HIP device memory, e.g. a
+ * tensor's data_ptr()), plain sizes, and a HIP stream passed as `void*`
+ * (NULL = the default stream).  Work is enqueued asynchronously on that
+ * stream; nothing is allocated, freed or retained by the library.  Each call
+ * returns HQ_OK or an HQ_ERR_* code; shapes are validated on the host before
+ * any launch, so a bad call launches nothing.
+ *
+ * Reference citations are file:line in the reference repository
+ * (OneBit-AI/Harsh4B).  The reference binds its native library through
+ * ctypes with host pointers and no return value (cpu_lightspark.py:71-111);
+ * this ABI keeps each function's argument order and meaning and adds the
+ * stream and the status return.
+ */
+#ifndef HQ_H
+#define HQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HQ_OK 0
+#define HQ_ERR_ARG 1      /* bad shape, size or null pointer */
+#define HQ_ERR_ALIGN 2    /* pointer alignment a kernel needs is not met */
+#define HQ_ERR_LAUNCH 3   /* the HIP launch failed */
+#define HQ_ERR_DEVICE 4   /* no usable gfx950 device */
+
+/* Text for a status code (static storage). */
+const char* hq_status_string(int status);
+/* ABI version: 100 * major + minor. */
+int hq_abi_version(void);
+
+/* ------------------------------------------------------------------ A4 --
+ * Packed signed-int4 x int8 GEMV.  Replaces litespark_int4_i8_gemv,
+ * _nopf, _pf256 and _pf512 (cpu_kernels/litespark_int4.cpp:78-108; the four
+ * differ only in a CPU prefetch distance), bound at cpu_lightspark.py:71-93:
+ *   output[n] = ((float)sum_k W[n,k] * x[k] * activation_scale) * scales[n]
+ * x: int8 [width]; weights: uint8 [rows, width/2], two's-complement nibbles,
+ * low nibble = even column (cpu_lightspark.py:139-146); scales: fp32 [rows];
+ * output: fp32 [rows].  width must be even and <= 32768. */
+int hq_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const float* scales,
+                    float activation_scale, float* output, int rows, int width,
+                    void* stream);
+
+/* ---------------------------------------------------------------- A3+A4 --
+ * The fused hot-path projection: per-token int8 quantization of fp32 x
+ * (replaces the third-party kernel.quantize_activation called at
+ * cpu_lightspark.py:433,443,449,457,463) followed by the GEMV above, as
+ * LiteSparkQwen._projection does it (cpu_lightspark.py:351-371).
+ * Optional outputs (NULL to skip): q_out int8 [width], act_scale_out fp32
+ * [1], acc_out int32 [rows] (the exact integer accumulators). */
+int hq_quant_int4_gemv(const float* x, const uint8_t* weights, const float* scales,
+                       float* output, int rows, int width, int8_t* q_out,
+                       float* act_scale_out, int32_t* acc_out, void* stream);
+
+/* ------------------------------------------------------------------ A3 --
+ * Per-token int8 quantization alone (kernel.quantize_activation,
+ * cpu_lightspark.py:433): q int8 [n], act_scale fp32 [1] on the device. */
+int hq_quantize_activation(const float* x, int n, int8_t* q, float* act_scale, void* stream);
+
+/* ------------------------------------------------------------------ A7 --
+ * RMSNorm y = (x / sqrt(mean(x^2) + eps)) * gamma over n values
+ * (kernel.rmsnorm_into, cpu_lightspark.py:431,447,461). */
+int hq_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps, void* stream);
+
+/* ----------------------------------------------------------------- A10 --
+ * Fused single-token GQA attention (score, softmax and V accumulation in
+ * one kernel).  Replaces litespark_gqa_decode (cpu_kernels/
+ * litespark_int4.cpp:160-171, bound at cpu_lightspark.py:102-111).
+ * query fp32 [kv_heads*groups, head_dim], heads ordered [kv_head, group];
+ * keys/values fp16 (IEEE binary16 bits) with element (t, h, d) at
+ * t*kv_time_stride + h*head_dim + d (the reference's [time, kv_head, dim]
+ * layout when kv_time_stride = kv_heads*head_dim); output fp32 like query.
+ * `workspace` takes the place of the reference's `scores` scratch: at least
+ * hq_gqa_workspace_bytes(context, ...) bytes, 256-byte aligned, zero-filled
+ * before its first use; every call leaves its counter words at zero, so one
+ * workspace serves any later call whose context needs no more bytes.
+ * head_dim in {16, 32, 64, 128}; groups <= 8; context >= 1; keys/values
+ * aligned to head_dim/16 halves. */
+size_t hq_gqa_workspace_bytes(int context, int kv_heads, int groups, int head_dim);
+int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* values,
+                  void* workspace, float* output, int context, int kv_heads, int groups,
+                  int head_dim, int kv_time_stride, void* stream);
+
+/* ----------------------------------------------------------------- A13 --
+ * Device argmax with np.argmax's order: the first maximal index, a NaN
+ * beating every number (cpu_lightspark.py:704-705, the greedy branch of
+ * sample_logits).  out_index int32 [1].  `workspace`:
+ * hq_argmax_workspace_bytes(n) bytes, 256-byte aligned, zero-filled before
+ * its first use; it serves any later call with no larger n. */
+size_t hq_argmax_workspace_bytes(int n);
+int hq_argmax(const float* x, int n, int32_t* out_index, void* workspace, void* stream);
+
+/* ----------------------------------------------------------------- A14 --
+ * Batched decode (M concurrent sequences share each weight read).  No
+ * reference counterpart (forward_token is batch 1, cpu_lightspark.py:424);
+ * defined as M independent A4 calls and bit-identical to them:
+ *   output[m, n] = ((float)sum_k W[n,k] * x[m,k] * act_scales[m]) * scales[n]
+ * x int8 [m, width]; act_scales fp32 [m]; output fp32 [m, rows];
+ * acc_out (nullable) int32 [m, rows].  The products run on int8 MFMA
+ * (v_mfma_i32_16x16x64_i8) with the K dimension split across blocks; the
+ * split partial sums meet in `workspace` (hq_gemm_workspace_bytes(m, rows,
+ * width) bytes, 16-byte aligned, zero-filled before its first use).  A call
+ * leaves its accumulator and counter regions at zero again, so a workspace
+ * may be reused by later calls of the same (m, rows, width); give calls of
+ * other shapes their own workspace.  width % 32 == 0, weights 16-byte
+ * aligned, 1 <= m. */
+size_t hq_gemm_workspace_bytes(int m, int rows, int width);
+int hq_int4_i8_gemm(const int8_t* x, const float* act_scales, const uint8_t* weights,
+                    const float* scales, float* output, int m, int rows, int width,
+                    int32_t* acc_out, void* workspace, void* stream);
+/* Fused form: per-sequence quantization of fp32 x [m, width] (the A3 spec
+ * applied to each row), then the GEMM.  q_out int8 [m, width] and
+ * act_scales_out fp32 [m] are optional outputs. */
+int hq_quant_int4_gemm(const float* x, const uint8_t* weights, const float* scales,
+                       float* output, int m, int rows, int width, int8_t* q_out,
+                       float* act_scales_out, int32_t* acc_out, void* workspace,
+                       void* stream);
+
+/* ------------------------------------------------------------- A6..A13 --
+ * One decode step of a Qwen3-shaped model, as LiteSparkQwen.forward_token
+ * (cpu_lightspark.py:424-468): embedding row decode, per layer RMSNorm ->
+ * quant -> fused qkv GEMV -> qk-norm -> RoPE -> fp16 KV write -> GQA
+ * attention -> quant -> o GEMV + residual -> RMSNorm -> quant -> fused
+ * gate_up GEMV with SwiGLU -> quant -> down GEMV + residual; final RMSNorm
+ * -> quant -> tied LM head GEMV -> argmax (lowest index on ties, as
+ * np.argmax at cpu_lightspark.py:704-705).
+ * All pointers inside the structs are device pointers except hq_model.layer,
+ * a host array of `layers` entries.  The structs are plain C. */
+typedef struct hq_layer {
+    const uint8_t* qkv;      const float* qkv_scales;      /* [q+2kv, hidden/2], [q+2kv] */
+    const uint8_t* o;        const float* o_scales;        /* [hidden, q/2], [hidden] */
+    const uint8_t* gate_up;  const float* gate_up_scales;  /* [2*inter, hidden/2] */
+    const uint8_t* down;     const float* down_scales;     /* [hidden, inter/2] */
+    const float* input_norm; const float* post_norm;       /* [hidden] */
+    const float* q_norm;     const float* k_norm;          /* [head_dim] */
+} hq_layer;
+
+typedef struct hq_model {
+    int32_t layers, hidden, intermediate, heads, kv_heads, head_dim, vocab, rope_positions;
+    float eps;
+    int32_t reserved;
+    const hq_layer* layer;          /* HOST array [layers] */
+    const uint8_t* embedding;       /* [vocab, hidden/2], tied LM head */
+    const float* embedding_scales;  /* [vocab] */
+    const float* final_norm;        /* [hidden] */
+    const float* rope_cos;          /* [rope_positions, head_dim/2] */
+    const float* rope_sin;
+} hq_model;
+
+typedef struct hq_state {
+    int32_t capacity;     /* KV positions */
+    int32_t reserved;
+    uint16_t* keys;       /* fp16 [layers, capacity, kv_heads, head_dim] */
+    uint16_t* values;
+    int32_t* position;    /* [1] next position; advanced by each step */
+    int32_t* token;       /* [1] input token; replaced by the greedy token */
+    int32_t* status;      /* [1] 0, or HQ_STEP_BAD_TOKEN / HQ_STEP_FULL (sticky) */
+    float* x;             /* [hidden] residual stream */
+    float* qkv;           /* [q+2kv] raw fused projection */
+    float* attended;      /* [q] */
+    float* activated;     /* [inter] SwiGLU output */
+    float* logits;        /* [vocab] */
+    void* workspace;      /* hq_step_workspace_bytes(); zero-filled once */
+} hq_state;
+
+#define HQ_STEP_BAD_TOKEN 1
+#define HQ_STEP_FULL 2
+
+size_t hq_step_workspace_bytes(const hq_model* model, int capacity);
+/* Enqueue one step.  Reads *state->token and *state->position on the device,
+ * so the same launch sequence serves every position (graph-capturable). */
+int hq_decode_step(const hq_model* model, const hq_state* state, void* stream);
+
+/* Launch one body GEMV of the step (the kernel the step launches) for one
+ * layer on the state's buffers, so a kernel can be timed in isolation.
+ * kind: 0 = RMSNorm+qkv, 1 = o + residual, 2 = RMSNorm+gate_up+SwiGLU,
+ * 3 = down + residual.  No reference counterpart (measurement hook). */
+int hq_step_gemv(const hq_model* model, const hq_state* state, int layer, int kind,
+                 void* stream);
+
+/* Capture `steps` consecutive decode steps enqueued on `stream` (which must
+ * not be the default stream) into an executable HIP graph. */
+int hq_graph_capture(const hq_model* model, const hq_state* state, int steps,
+                     void* stream, void** graph_exec);
+int hq_graph_launch(void* graph_exec, void* stream);
+int hq_graph_destroy(void* graph_exec);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,174 @@
+"""GPU parity of the whole decode step (LiteSparkQwen.forward_token,
+cpu_lightspark.py:424-468 in the reference repository) against the CPU
+oracle: logits, KV cache and greedy tokens bit-exact."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.gpu_util import assert_bits_equal, dev, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+KEYS = ("qkv", "qkv_scales", "o", "o_scales", "gate_up", "gate_up_scales", "down",
+        "down_scales", "input_norm", "post_norm", "q_norm", "k_norm")
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[gpu] {request.node.nodeid}", flush=True)
+    yield
+    torch.cuda.synchronize()
+
+
+def golden_model(g):
+    from harsh4b_amd.synthetic import model_from_arrays
+    arrays = {k: [np.ascontiguousarray(a) for a in g[k]] for k in KEYS}
+    for k in ("embedding", "embedding_scales", "final_norm"):
+        arrays[k] = np.ascontiguousarray(g[k])
+    return model_from_arrays(g["config"], arrays)
+
+
+def oracle_of(model):
+    from harsh4b_amd.synthetic import host_arrays
+    return oracle.OracleModel(model.config, host_arrays(model))
+
+
+def test_rope_tables_match_reference_run(forward_golden):
+    from harsh4b_amd.lightspark import rope_tables
+    cos, sin = rope_tables(forward_golden["config"])
+    np.testing.assert_array_equal(cos, forward_golden["rope_cos"])
+    np.testing.assert_array_equal(sin, forward_golden["rope_sin"])
+
+
+def test_tiny_model_step_by_step(forward_golden):
+    g = forward_golden
+    model = golden_model(g)
+    ref = oracle_of(model)
+    cap = len(g["tokens"])
+    st = model.new_state(cap)
+    rs = ref.new_state(cap)
+    for i, t in enumerate(g["tokens"]):
+        logits = model.forward_token(int(t), st)
+        tok = model.greedy_token(st)
+        rtok = ref.forward_token(int(t), rs)
+        assert_bits_equal(to_host(logits), rs.logits, f"logits step {i}")
+        assert tok == rtok == int(g["greedy"][i]), (i, tok, rtok, g["greedy"][i])
+        # the reference run used an fp32 KV cache: fp16 storage stays close
+        assert np.abs(to_host(logits) - g["logits"][i]).max() < 0.1
+    assert_bits_equal(to_host(st.keys).view(np.uint16), rs.keys, "keys")
+    assert_bits_equal(to_host(st.values).view(np.uint16), rs.values, "values")
+    assert_bits_equal(to_host(st.x), rs.x, "residual")
+    st.check_status()
+
+
+def test_tiny_model_graph_replay_matches_eager(forward_golden):
+    g = forward_golden
+    model = golden_model(g)
+    a = model.new_state(12)
+    b = model.new_state(12)
+    first = int(g["tokens"][0])
+    # eager greedy loop
+    toks_a = []
+    model.forward_token(first, a)
+    for _ in range(8):
+        t = model.greedy_token(a)
+        toks_a.append(t)
+        model.forward_token(t, a)
+    toks_a.append(model.greedy_token(a))
+    # device-resident greedy loop through a captured graph, replayed 9 times
+    toks_b = []
+    with torch.cuda.stream(b.stream):
+        b.token.fill_(first)
+    for _ in range(9):
+        model.decode_greedy(b, 1)
+        toks_b.append(model.greedy_token(b))
+    assert toks_a == toks_b
+    assert_bits_equal(to_host(b.logits), to_host(a.logits), "graph logits")
+    assert_bits_equal(to_host(b.keys).view(np.uint16), to_host(a.keys).view(np.uint16), "graph keys")
+    a.check_status()
+    b.check_status()
+
+
+def test_step_errors(forward_golden):
+    g = forward_golden
+    model = golden_model(g)
+    st = model.new_state(1)
+    with pytest.raises(ValueError, match="outside the vocabulary"):
+        model.forward_token(int(g["config"]["vocab_size"]), st)
+    model.forward_token(3, st)
+    with pytest.raises(ValueError, match="capacity exhausted"):
+        model.forward_token(3, st)
+
+
+def test_device_flags_bad_token_without_fault(forward_golden):
+    # force the condition from the host: an out-of-vocabulary id written
+    # straight into the device token slot; the kernel clamps and flags it
+    import ctypes
+    from harsh4b_amd import _native
+    g = forward_golden
+    model = golden_model(g)
+    st = model.new_state(2)
+    with torch.cuda.stream(st.stream):
+        st.token.fill_(10 ** 6)
+    _native.check(_native.lib().hq_decode_step(ctypes.byref(model.struct), ctypes.byref(st.struct),
+                                               st.stream.cuda_stream), "step")
+    with pytest.raises(ValueError, match="outside the vocabulary"):
+        st.check_status()
+
+
+# ------------------------------------------------------------------ full size
+@pytest.fixture(scope="module")
+def qwen():
+    from harsh4b_amd.config import QWEN3_4B
+    from harsh4b_amd.synthetic import random_model
+    model = random_model(QWEN3_4B, seed=11)
+    torch.cuda.synchronize()
+    return model, oracle_of(model)
+
+
+def test_qwen3_4b_first_tokens_bit_exact(qwen):
+    model, ref = qwen
+    cap = 8
+    st = model.new_state(cap)
+    rs = ref.new_state(cap)
+    token = 151643
+    for i in range(4):
+        logits = model.forward_token(token, st)
+        tok = model.greedy_token(st)
+        rtok = ref.forward_token(token, rs)
+        assert_bits_equal(to_host(logits), rs.logits, f"logits step {i}")
+        assert tok == rtok
+        token = tok
+    assert_bits_equal(to_host(st.keys).view(np.uint16)[:, :4], rs.keys[:, :4], "keys")
+    st.check_status()
+
+
+@pytest.mark.parametrize("ctx", [300, 4000])
+def test_qwen3_4b_long_context_bit_exact(qwen, ctx):
+    # an fp16 N(0,1) cache of `ctx` positions on both sides, then two steps
+    model, ref = qwen
+    cap = ctx + 2
+    st = model.new_state(cap)
+    rs = ref.new_state(cap)
+    rng = np.random.default_rng(ctx)
+    shape = st.keys.shape
+    for name in ("keys", "values"):
+        cache = rng.standard_normal((shape[0], ctx) + tuple(shape[2:])).astype(np.float16)
+        getattr(st, name)[:, :ctx] = to_dev(cache)
+        getattr(rs, name)[:, :ctx] = cache.view(np.uint16)
+    st.device_position.fill_(ctx)
+    st.position = ctx
+    rs.position = ctx
+    torch.cuda.synchronize()
+    token = 1234
+    for i in range(2):
+        logits = model.forward_token(token, st)
+        tok = model.greedy_token(st)
+        rtok = ref.forward_token(token, rs)
+        assert_bits_equal(to_host(logits), rs.logits, f"ctx {ctx} step {i}")
+        assert tok == rtok
+        token = tok
+    assert_bits_equal(to_host(st.keys).view(np.uint16)[:, ctx:ctx + 2], rs.keys[:, ctx:ctx + 2], "new keys")
+    st.check_status()
