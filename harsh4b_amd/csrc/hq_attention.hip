@@ -28,45 +28,60 @@
 
 namespace hq {
 
+// K and V of one chunk are staged in LDS: every 16-byte load of a chunk is
+// issued one chunk ahead (two register buffers), so each chunk costs one
+// memory round trip at most.  Rows are padded by 16 bytes to spread banks.
 template <int D>
-__device__ __forceinline__ void load_k_lane(const uint16_t* src, float* k)
+struct ChunkTile {
+    static constexpr int kRowHalves = D + 8;                 // padded row
+    static constexpr int kGroupsPerRow = D / 8;              // 16-byte groups per row
+    static constexpr int kGroups = kAttnChunk * kGroupsPerRow;
+    static constexpr int kPerThread = (kGroups + kBlock - 1) / kBlock;
+};
+
+template <int D>
+__device__ __forceinline__ void load_chunk(const AttnParams& a, int t0, int tn, int skip_t,
+                                           size_t kv_off, uint4* kreg, uint4* vreg)
 {
-    constexpr int DPL = D / 16;
-    if constexpr (DPL == 8) {
-        const uint4 v = *reinterpret_cast<const uint4*>(src);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    using T = ChunkTile<D>;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            k[2 * j] = f16_to_f32(uint16_t(w[j] & 0xFFFFu));
-            k[2 * j + 1] = f16_to_f32(uint16_t(w[j] >> 16));
-        }
-    } else if constexpr (DPL == 4) {
-        const uint2 v = *reinterpret_cast<const uint2*>(src);
-        k[0] = f16_to_f32(uint16_t(v.x & 0xFFFFu));
-        k[1] = f16_to_f32(uint16_t(v.x >> 16));
-        k[2] = f16_to_f32(uint16_t(v.y & 0xFFFFu));
-        k[3] = f16_to_f32(uint16_t(v.y >> 16));
-    } else {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) k[j] = f16_to_f32(src[j]);
+    for (int r = 0; r < T::kPerThread; ++r) {
+        const int id = threadIdx.x + kBlock * r;
+        const int t = id / T::kGroupsPerRow;
+        const int d8 = id % T::kGroupsPerRow;
+        const bool ok = id < T::kGroups && t < tn && t != skip_t;
+        const size_t off = size_t(t0 + t) * a.time_stride + kv_off + size_t(d8) * 8;
+        kreg[r] = ok ? *reinterpret_cast<const uint4*>(a.keys + off) : make_uint4(0, 0, 0, 0);
+        vreg[r] = ok ? *reinterpret_cast<const uint4*>(a.values + off) : make_uint4(0, 0, 0, 0);
     }
 }
 
-template <int D, int GMAX, bool STEP>
+// Block (kv_head, split) walks chunks [split*CPB, split*CPB + CPB) of the
+// context.  With a single split (context <= CPB*64) it combines its chunk
+// partials itself; otherwise the partials go to the workspace and the last
+// split of the kv head to arrive combines all of them.  Either way the
+// combine runs over ascending chunks, so the result is the same bits.
+template <int D, int GMAX, bool STEP, int CPB>
 __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
 {
     constexpr int C = kAttnChunk;
     constexpr int DPL = D / 16;
     constexpr int PAIRS = (GMAX * D + kBlock - 1) / kBlock;   // (head, dim) pairs per thread
     constexpr int HSTEP = kBlock / D;                          // heads between a thread's pairs
+    using T = ChunkTile<D>;
     __shared__ float q_s[GMAX][D];
-    __shared__ float kcur[D];
-    __shared__ float vcur[D];
+    __shared__ __align__(16) uint16_t k_s[C * T::kRowHalves];
+    __shared__ __align__(16) uint16_t v_s[C * T::kRowHalves];
+    __shared__ uint16_t kc_s[D];
+    __shared__ uint16_t vc_s[D];
     __shared__ float e_s[GMAX][C];
+    __shared__ float m_s[GMAX][CPB];
+    __shared__ float l_s[GMAX][CPB];
+    __shared__ float o_s[CPB][GMAX][D];   // per-chunk V partials
     __shared__ int last_flag;
 
     const int g = blockIdx.x;
-    const int c = blockIdx.y;
+    const int split = blockIdx.y;
     const int G = a.groups;
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
@@ -76,7 +91,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     if constexpr (STEP) {
         pos = *a.position;
         if (pos < 0 || pos >= a.capacity) {
-            if (g == 0 && c == 0 && tid == 0) atomicOr(a.status, HQ_STEP_FULL);
+            if (g == 0 && split == 0 && tid == 0) atomicOr(a.status, HQ_STEP_FULL);
             return;
         }
         n = pos + 1;
@@ -85,13 +100,21 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         n = a.context;
     }
     const int nc = (n + C - 1) / C;
-    if (c >= nc) return;
-    const int t0 = c * C;
-    const int tn = min(C, n - t0);          // valid positions in this chunk
-    const bool has_cur = STEP && (c == nc - 1);
+    const int nsplit = (nc + CPB - 1) / CPB;
+    if (split >= nsplit) return;
+    const int c_begin = split * CPB;
+    const int c_end = min(nc, c_begin + CPB);
     const size_t kv_off = size_t(g) * D;
+    const int cur_chunk = STEP ? nc - 1 : -1;     // chunk holding the current position
 
-    // ---- phase 1: query heads (and in STEP mode the current k/v) ----------
+    uint4 kreg[T::kPerThread], vreg[T::kPerThread];
+    {
+        const int t0 = c_begin * C;
+        load_chunk<D>(a, t0, min(C, n - t0), c_begin == cur_chunk ? pos - t0 : -1, kv_off, kreg, vreg);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // the chunk loads go out before the query prologue
+
+    // ---- query heads (and in STEP mode the current k/v) ---------------------
     if constexpr (STEP) {
         static_assert(D == 128, "STEP mode is written for head_dim 128");
         const float* cs = a.rope_cos + size_t(pos) * (D / 2);
@@ -109,7 +132,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
             q_s[h][lane] = y0 * c0 - y1 * s0;
             q_s[h][lane + 64] = y1 * c0 + y0 * s0;
         }
-        if (has_cur) {
+        if (split == nsplit - 1) {
             const int heads = a.kv_heads * G;
             uint16_t* kdst = a.keys + size_t(pos) * a.time_stride + kv_off;
             uint16_t* vdst = a.values + size_t(pos) * a.time_stride + kv_off;
@@ -127,16 +150,16 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                 const uint16_t h1 = f32_to_f16(y1 * c0 + y0 * s0);
                 kdst[lane] = h0;
                 kdst[lane + 64] = h1;
-                kcur[lane] = f16_to_f32(h0);
-                kcur[lane + 64] = f16_to_f32(h1);
+                kc_s[lane] = h0;
+                kc_s[lane + 64] = h1;
             } else if (wave == 1) {
                 const float* src = a.qkv + size_t(heads + a.kv_heads + g) * D;
                 const uint16_t h0 = f32_to_f16(src[lane]);
                 const uint16_t h1 = f32_to_f16(src[lane + 64]);
                 vdst[lane] = h0;
                 vdst[lane + 64] = h1;
-                vcur[lane] = f16_to_f32(h0);
-                vcur[lane + 64] = f16_to_f32(h1);
+                vc_s[lane] = h0;
+                vc_s[lane + 64] = h1;
             }
         }
     } else {
@@ -144,28 +167,59 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     }
     __syncthreads();
 
-    // ---- phase 2: scores, 16 lanes per position ----------------------------
-    {
-        const int grp = tid >> 4;       // 16 groups
-        const int l16 = tid & 15;
-        const float scale = 1.0f / __builtin_sqrtf(float(D));
-        float qr[GMAX][DPL];
+    const int grp = tid >> 4;       // 16 lane groups for the scores
+    const int l16 = tid & 15;
+    const float scale = 1.0f / __builtin_sqrtf(float(D));
+    float qr[GMAX][DPL];
 #pragma unroll
-        for (int h = 0; h < GMAX; ++h)
+    for (int h = 0; h < GMAX; ++h)
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) qr[h][j] = (h < G) ? q_s[h][l16 * DPL + j] : 0.0f;
+        for (int j = 0; j < DPL; ++j) qr[h][j] = (h < G) ? q_s[h][l16 * DPL + j] : 0.0f;
+    const int d = tid % D;
+    const int h0 = tid / D;
+
+    // the chunk loop stays rolled: one copy of its body keeps the kernel's
+    // code small enough to stay resident in the instruction cache
+#pragma unroll 1
+    for (int ci = 0; ci < CPB; ++ci) {
+        const int c = c_begin + ci;
+        if (c >= c_end) break;
+        const int t0 = c * C;
+        const int tn = min(C, n - t0);
+
+        // registers -> LDS (the current position's row comes from kc_s/vc_s)
+#pragma unroll
+        for (int r = 0; r < T::kPerThread; ++r) {
+            const int id = tid + kBlock * r;
+            const int t = id / T::kGroupsPerRow;
+            const int d8 = id % T::kGroupsPerRow;
+            if (id < T::kGroups && t < tn) {
+                uint4 kv = kreg[r], vv = vreg[r];
+                if (c == cur_chunk && t0 + t == pos) {
+                    kv = *reinterpret_cast<const uint4*>(kc_s + d8 * 8);
+                    vv = *reinterpret_cast<const uint4*>(vc_s + d8 * 8);
+                }
+                *reinterpret_cast<uint4*>(k_s + t * T::kRowHalves + d8 * 8) = kv;
+                *reinterpret_cast<uint4*>(v_s + t * T::kRowHalves + d8 * 8) = vv;
+            }
+        }
+        __syncthreads();
+        if (c + 1 < c_end) {
+            const int t1 = t0 + C;
+            load_chunk<D>(a, t1, min(C, n - t1), c + 1 == cur_chunk ? pos - t1 : -1, kv_off, kreg,
+                          vreg);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // scores, 16 lanes per position
 #pragma unroll
         for (int rep = 0; rep < C / 16; ++rep) {
             const int i = grp + 16 * rep;
-            const int t = t0 + i;
             if (i < tn) {
                 float k[DPL];
-                if (has_cur && t == pos) {
+                const uint16_t* kr = k_s + i * T::kRowHalves + l16 * DPL;
 #pragma unroll
-                    for (int j = 0; j < DPL; ++j) k[j] = kcur[l16 * DPL + j];
-                } else {
-                    load_k_lane<D>(a.keys + size_t(t) * a.time_stride + kv_off + l16 * DPL, k);
-                }
+                for (int j = 0; j < DPL; ++j) k[j] = f16_to_f32(kr[j]);
 #pragma unroll
                 for (int h = 0; h < GMAX; ++h) {
                     if (h < G) {
@@ -182,57 +236,97 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                     if (h < G) e_s[h][i] = -__builtin_inff();
             }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // ---- phase 3: chunk softmax statistics, one wave per head --------------
-    const int heads = a.kv_heads * G;
-    const int pstride = D + 2;
-    for (int h = wave; h < G; h += kBlock / kWave) {
-        const float s = e_s[h][lane];
-        const float m = fmax_group<kWave>(s);
-        const float e = (lane < tn) ? spec_expf(s - m) : 0.0f;
-        const float l = tree_sum<kWave>(e);
-        e_s[h][lane] = e;
-        if (lane == 0) {
-            float* pp = a.part + (size_t(g * G + h) * a.max_chunks + c) * pstride;
-            pp[0] = m;
-            pp[1] = l;
+        // chunk softmax statistics, one wave per head
+        for (int h = wave; h < G; h += kBlock / kWave) {
+            const float sc = e_s[h][lane];
+            const float m = fmax_group<kWave>(sc);
+            const float e = (lane < tn) ? spec_expf(sc - m) : 0.0f;
+            const float l = tree_sum<kWave>(e);
+            e_s[h][lane] = e;
+            if (lane == 0) { m_s[h][ci] = m; l_s[h][ci] = l; }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // ---- phase 4: partial V accumulation ------------------------------------
-    const int d = tid % D;
-    const int h0 = tid / D;
-    {
-        float o[PAIRS];
+        // partial V accumulation from LDS: an fmaf chain over ascending
+        // positions; the LDS reads of 8 positions are issued before their
+        // fmas so their latency is paid once per 8 positions
+        float o_acc[PAIRS];
 #pragma unroll
-        for (int r = 0; r < PAIRS; ++r) o[r] = 0.0f;
-        const uint16_t* vsrc = a.values + size_t(t0) * a.time_stride + kv_off + d;
-        for (int i = 0; i < tn; ++i) {
-            float v;
-            if (has_cur && t0 + i == pos) v = vcur[d];
-            else v = f16_to_f32(vsrc[size_t(i) * a.time_stride]);
+        for (int r = 0; r < PAIRS; ++r) o_acc[r] = 0.0f;
+        int i = 0;
+        for (; i + 8 <= tn; i += 8) {
+            float v[8], e[PAIRS][8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                v[j] = f16_to_f32(v_s[(i + j) * T::kRowHalves + d]);
+#pragma unroll
+                for (int r = 0; r < PAIRS; ++r) {
+                    const int h = min(h0 + HSTEP * r, GMAX - 1);
+                    e[r][j] = e_s[h][i + j];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int r = 0; r < PAIRS; ++r)
+                    o_acc[r] = __builtin_fmaf(e[r][j], v[j], o_acc[r]);
+        }
+        for (; i < tn; ++i) {
+            const float v = f16_to_f32(v_s[i * T::kRowHalves + d]);
 #pragma unroll
             for (int r = 0; r < PAIRS; ++r) {
-                const int h = h0 + HSTEP * r;
-                if (h < G) o[r] = __builtin_fmaf(e_s[h][i], v, o[r]);
+                const int h = min(h0 + HSTEP * r, GMAX - 1);
+                o_acc[r] = __builtin_fmaf(e_s[h][i], v, o_acc[r]);
             }
         }
 #pragma unroll
         for (int r = 0; r < PAIRS; ++r) {
             const int h = h0 + HSTEP * r;
-            if (h < G) a.part[(size_t(g * G + h) * a.max_chunks + c) * pstride + 2 + d] = o[r];
+            if (h < G) o_s[ci][h][d] = o_acc[r];
         }
+        __syncthreads();
     }
 
-    // ---- phase 5: last block of this kv head combines ----------------------
+    const int pstride = D + 2;
+    const int nmine = c_end - c_begin;
+    if (nsplit == 1) {
+        // every chunk is in this block: combine in ascending chunk order
+#pragma unroll
+        for (int r = 0; r < PAIRS; ++r) {
+            const int h = h0 + HSTEP * r;
+            if (h >= G) continue;
+            float M = -__builtin_inff();
+            for (int ci = 0; ci < nmine; ++ci) M = fmaxf(M, m_s[h][ci]);
+            float L = 0.0f, O = 0.0f;
+            for (int ci = 0; ci < nmine; ++ci) {
+                const float al = spec_expf(m_s[h][ci] - M);
+                L = __builtin_fmaf(al, l_s[h][ci], L);
+                O = __builtin_fmaf(al, o_s[ci][h][d], O);
+            }
+            a.out[size_t(g * G + h) * D + d] = O * (1.0f / L);
+        }
+        return;
+    }
+
+    // several splits: publish this block's chunk partials
+    for (int ci = 0; ci < nmine; ++ci) {
+        const int c = c_begin + ci;
+#pragma unroll
+        for (int r = 0; r < PAIRS; ++r) {
+            const int h = h0 + HSTEP * r;
+            if (h >= G) continue;
+            float* pp = a.part + (size_t(g * G + h) * a.max_chunks + c) * pstride;
+            pp[2 + d] = o_s[ci][h][d];
+            if (d == 0) { pp[0] = m_s[h][ci]; pp[1] = l_s[h][ci]; }
+        }
+    }
     __threadfence();
     __syncthreads();
     if (tid == 0) {
         const int ticket = atomicAdd(a.counters + g, 1);
-        last_flag = (ticket == nc - 1);
+        last_flag = (ticket == nsplit - 1);
     }
     __syncthreads();
     if (!last_flag) return;
@@ -259,7 +353,6 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         a.out[size_t(g * G + h) * D + d] = O * (1.0f / L);
     }
     if (tid == 0) a.counters[g] = 0;
-    (void)heads;
 }
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim)
@@ -267,10 +360,19 @@ size_t attention_workspace_floats(int heads, int max_chunks, int head_dim)
     return size_t(heads) * size_t(max_chunks) * size_t(head_dim + 2);
 }
 
+constexpr int kChunksPerBlock = 4;
+
+int attention_splits(int context)
+{
+    const int nc = (context + kAttnChunk - 1) / kAttnChunk;
+    return (nc + kChunksPerBlock - 1) / kChunksPerBlock;
+}
+
 template <int D, int GMAX, bool STEP>
 static hipError_t launch_attn(const AttnParams& a, hipStream_t s)
 {
-    hipLaunchKernelGGL((attention_kernel<D, GMAX, STEP>), dim3(a.kv_heads, a.max_chunks),
+    const int splits = (a.max_chunks + kChunksPerBlock - 1) / kChunksPerBlock;
+    hipLaunchKernelGGL((attention_kernel<D, GMAX, STEP, kChunksPerBlock>), dim3(a.kv_heads, splits),
                        dim3(kBlock), 0, s, a);
     return hipGetLastError();
 }
@@ -314,9 +416,8 @@ extern "C" int hq_gqa_decode(const float* query, const uint16_t* keys, const uin
     if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128) return HQ_ERR_ARG;
     if (kv_time_stride < kv_heads * head_dim) return HQ_ERR_ARG;
     if (kv_heads * 256 > 256 * 64) return HQ_ERR_ARG;   // counters fit in 256 bytes
-    const size_t dpl_bytes = size_t(head_dim / 16) * 2;
-    if (((reinterpret_cast<uintptr_t>(keys)) % dpl_bytes) != 0 ||
-        (size_t(kv_time_stride) * 2) % dpl_bytes != 0)
+    if ((reinterpret_cast<uintptr_t>(keys) & 15u) != 0 ||
+        (reinterpret_cast<uintptr_t>(values) & 15u) != 0 || (kv_time_stride % 8) != 0)
         return HQ_ERR_ALIGN;
     const int nc = (context + kAttnChunk - 1) / kAttnChunk;
     AttnParams a{};

@@ -52,45 +52,57 @@ __device__ __forceinline__ int dot_chunk(uint4 w, const uint8_t* xs_chunk, int a
     return acc;
 }
 
-// Activation prologue: fills xs (width bytes, de-interleaved int8) and
-// returns the act scale.  Element i is handled by thread i % 256, which for
-// PRO_RMSNORM is exactly the spec's 256-lane partial sum of squares.
+// Activation registers: element i = tid + 256*j of x (and gamma) is held
+// by thread tid, which for PRO_RMSNORM is exactly the spec's 256-lane
+// partial sum of squares.  Loads are unconditional (clamped index) so the
+// compiler issues them back to back before any use.
 template <int XJ, int PRO>
-__device__ __forceinline__ float activation_prologue(const GemvParams& p, uint8_t* xs,
-                                                     float* red)
+struct ActRegs {
+    float x[XJ];
+    float g[PRO == PRO_RMSNORM ? XJ : 1];
+};
+
+template <int XJ, int PRO>
+__device__ __forceinline__ void load_activation(const GemvParams& p, ActRegs<XJ, PRO>& a)
+{
+    if constexpr (PRO != PRO_I8) {
+        const int K = p.width;
+#pragma unroll
+        for (int j = 0; j < XJ; ++j) {
+            const int i = min(int(threadIdx.x) + kBlock * j, K - 1);
+            a.x[j] = p.xf[i];
+            if constexpr (PRO == PRO_RMSNORM) a.g[j] = p.gamma[i];
+        }
+    }
+}
+
+// Activation prologue: fills xs (width bytes, de-interleaved int8) and
+// returns the act scale.
+template <int XJ, int PRO>
+__device__ __forceinline__ float activation_prologue(const GemvParams& p, ActRegs<XJ, PRO>& a,
+                                                     uint8_t* xs, float* red)
 {
     const int tid = threadIdx.x;
     const int K = p.width;
     if constexpr (PRO == PRO_I8) {
-        for (int i = tid; i < K; i += kBlock) {
-            const int8_t q = p.xq[i];
-            xs[xq_offset(i)] = uint8_t(q);
-        }
+        for (int i = tid; i < K; i += kBlock) xs[xq_offset(i)] = uint8_t(p.xq[i]);
         return p.act_scale;
     } else {
-        float xr[XJ];
-#pragma unroll
-        for (int j = 0; j < XJ; ++j) {
-            const int i = tid + kBlock * j;
-            xr[j] = (i < K) ? p.xf[i] : 0.0f;
-        }
         if constexpr (PRO == PRO_RMSNORM) {
             float ss = 0.0f;
 #pragma unroll
             for (int j = 0; j < XJ; ++j)
-                if (tid + kBlock * j < K) ss = __builtin_fmaf(xr[j], xr[j], ss);
+                if (tid + kBlock * j < K) ss = __builtin_fmaf(a.x[j], a.x[j], ss);
             const float total = block_tree_sum256(ss, red);
             const float ms = total / float(K);
             const float r = __builtin_sqrtf(ms + p.eps);
 #pragma unroll
-            for (int j = 0; j < XJ; ++j) {
-                const int i = tid + kBlock * j;
-                if (i < K) xr[j] = (xr[j] / r) * p.gamma[i];
-            }
+            for (int j = 0; j < XJ; ++j) a.x[j] = (a.x[j] / r) * a.g[j];
         }
         float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < XJ; ++j) amax = fmaxf(amax, fabsf(xr[j]));
+        for (int j = 0; j < XJ; ++j)
+            if (tid + kBlock * j < K) amax = fmaxf(amax, fabsf(a.x[j]));
         amax = block_max_nonneg(amax, red);
         amax = fmaxf(amax, 1e-5f);
         const float inv = 127.0f / amax;
@@ -99,7 +111,7 @@ __device__ __forceinline__ float activation_prologue(const GemvParams& p, uint8_
         for (int j = 0; j < XJ; ++j) {
             const int i = tid + kBlock * j;
             if (i < K) {
-                const int8_t q = quant_i8(xr[j], inv);
+                const int8_t q = quant_i8(a.x[j], inv);
                 xs[xq_offset(i)] = uint8_t(q);
                 if (write_q) p.q_out[i] = q;
             }
@@ -110,7 +122,41 @@ __device__ __forceinline__ float activation_prologue(const GemvParams& p, uint8_
     }
 }
 
-template <int RB, int MAXC, int XJ, int PRO, int EPI>
+// Rows of row-slot `slot` in tile `tile`.
+template <int RB, int EPI>
+__device__ __forceinline__ int tile_row(const GemvParams& p, int tile, int slot, bool& valid)
+{
+    if constexpr (EPI == EPI_SWIGLU) {
+        constexpr int HALF = RB / 2;
+        const int pair = tile * HALF + (slot % HALF);
+        valid = pair < p.half_rows;
+        return (slot < HALF) ? pair : p.half_rows + pair;
+    } else {
+        const int row = tile * RB + slot;
+        valid = row < p.rows;
+        return row;
+    }
+}
+
+// Loads are unconditional (chunk index clamped; rows past the end read row
+// 0) so that no branch separates them and the wait counters stay exact; the
+// dot loop skips chunks past the row and the epilogue drops invalid rows.
+template <int MAXC, int LPR>
+__device__ __forceinline__ void load_tile(const uint8_t* wrow, int lir, int base, int nchunks,
+                                          uint4 (&wv)[MAXC])
+{
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = min(base + lir + j * LPR, nchunks - 1);
+        wv[j] = load_w16(wrow + size_t(c) * 16);
+    }
+}
+
+// Tiles: a tile is RB output rows.  Non-persistent launches give each block
+// one tile; persistent launches (PERSIST) loop over tiles blockIdx.x +
+// k*gridDim.x with the next tile's weights in flight while the current one
+// is reduced (two register buffers), and need width <= MAXC*LPR*32.
+template <int RB, int MAXC, int XJ, int PRO, int EPI, bool PERSIST>
 __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
 {
     constexpr int KP = 32 / RB;
@@ -119,6 +165,8 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     __shared__ float red[kBlock];
     __shared__ int part[32];
     __shared__ int accs[32];
+    __shared__ float bval[kBlock / kWave];
+    __shared__ int bidx[kBlock / kWave];
     __shared__ int last_flag;
 
     const int tid = threadIdx.x;
@@ -129,124 +177,139 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     const int lir = kp * 8 + li;
     const int K = p.width;
     const int nchunks = K >> 5;
+    const int ntiles = (EPI == EPI_SWIGLU) ? (p.half_rows + RB / 2 - 1) / (RB / 2)
+                                           : (p.rows + RB - 1) / RB;
 
-    int row;
+    // 1. activation loads, then the first tile's weight loads
+    ActRegs<XJ, PRO> areg;
+    load_activation<XJ, PRO>(p, areg);
+    int tile = blockIdx.x;
     bool valid;
-    if constexpr (EPI == EPI_SWIGLU) {
-        constexpr int HALF = RB / 2;
-        const int pair = blockIdx.x * HALF + (slot % HALF);
-        valid = pair < p.half_rows;
-        row = (slot < HALF) ? pair : p.half_rows + pair;
-    } else {
-        row = blockIdx.x * RB + slot;
-        valid = row < p.rows;
-    }
+    int row = tile_row<RB, EPI>(p, tile, slot, valid);
     const uint8_t* wrow = p.w + size_t(valid ? row : 0) * size_t(K >> 1);
-
-    // 1. first batch of weight loads (in flight during the prologue)
     uint4 wv[MAXC];
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        const int c = lir + j * LPR;
-        wv[j] = (valid && c < nchunks) ? load_w16(wrow + size_t(c) * 16) : make_uint4(0, 0, 0, 0);
-    }
+    load_tile<MAXC, LPR>(wrow, lir, 0, nchunks, wv);
+    // keep the scheduler from sinking the weight loads below the first use
+    // of the activations: the HBM stream must start before any wait
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 2. activations -> LDS
-    const float act = activation_prologue<XJ, PRO>(p, xs, red);
+    // 2. activations -> LDS (overlaps the weight stream)
+    const float act = activation_prologue<XJ, PRO>(p, areg, xs, red);
     __syncthreads();
 
-    // 3. int4 x int8 dot products
-    int acc16 = 0;
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        const int c = lir + j * LPR;
-        if (c < nchunks) acc16 = dot_chunk(wv[j], xs + c * 32, acc16);
-    }
-    for (int base = MAXC * LPR; base < nchunks; base += MAXC * LPR) {
-#pragma unroll
-        for (int j = 0; j < MAXC; ++j) {
-            const int c = base + lir + j * LPR;
-            wv[j] = (valid && c < nchunks) ? load_w16(wrow + size_t(c) * 16) : make_uint4(0, 0, 0, 0);
+    float best_v = -__builtin_inff();   // EPI_ARGMAX: running best of this block
+    int best_i = 0x7FFFFFFF;
+    while (true) {
+        // 3. prefetch the next tile (persistent), dot products of this one
+        const int next = tile + int(gridDim.x);
+        uint4 wn[PERSIST ? MAXC : 1];
+        bool nvalid = false;
+        int nrow = 0;
+        if constexpr (PERSIST) {
+            if (next < ntiles) {
+                nrow = tile_row<RB, EPI>(p, next, slot, nvalid);
+                load_tile<MAXC, LPR>(p.w + size_t(nvalid ? nrow : 0) * size_t(K >> 1), lir, 0,
+                                     nchunks, wn);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        int acc16 = 0;
 #pragma unroll
         for (int j = 0; j < MAXC; ++j) {
-            const int c = base + lir + j * LPR;
+            const int c = lir + j * LPR;
             if (c < nchunks) acc16 = dot_chunk(wv[j], xs + c * 32, acc16);
         }
-    }
-    acc16 = isum<8>(acc16);
-    if (li == 0) part[grp] = acc16 >> 4;
-    __syncthreads();
-    if (tid < RB) {
-        int a = 0;
+        if constexpr (!PERSIST) {
+            for (int base = MAXC * LPR; base < nchunks; base += MAXC * LPR) {
+                load_tile<MAXC, LPR>(wrow, lir, base, nchunks, wv);
 #pragma unroll
-        for (int k = 0; k < KP; ++k) a += part[tid + RB * k];
-        accs[tid] = a;
-    }
-    __syncthreads();
-
-    // 4. epilogue
-    if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
-        if (tid < RB) {
-            const int r = blockIdx.x * RB + tid;
-            if (r < p.rows) {
-                const int a = accs[tid];
-                const float v = (float(a) * act) * p.ws[r];
-                if (p.acc_out) p.acc_out[r] = a;
-                if constexpr (EPI == EPI_STORE) {
-                    p.out[r] = v;
-                } else {
-                    if (p.out_aux) p.out_aux[r] = v;
-                    p.out[r] = p.out[r] + v;
+                for (int j = 0; j < MAXC; ++j) {
+                    const int c = base + lir + j * LPR;
+                    if (c < nchunks) acc16 = dot_chunk(wv[j], xs + c * 32, acc16);
                 }
             }
         }
-    } else if constexpr (EPI == EPI_SWIGLU) {
-        constexpr int HALF = RB / 2;
-        if (tid < HALF) {
-            const int pair = blockIdx.x * HALF + tid;
-            if (pair < p.half_rows) {
-                const int gr = pair, ur = p.half_rows + pair;
-                const float g = (float(accs[tid]) * act) * p.ws[gr];
-                const float u = (float(accs[tid + HALF]) * act) * p.ws[ur];
-                if (p.acc_out) { p.acc_out[gr] = accs[tid]; p.acc_out[ur] = accs[tid + HALF]; }
-                if (p.out_aux) { p.out_aux[gr] = g; p.out_aux[ur] = u; }
-                const float t = 1.0f + spec_expf(-g);
-                p.out[pair] = (g / t) * u;
-            }
+        acc16 = isum<8>(acc16);
+        if (li == 0) part[grp] = acc16 >> 4;
+        __syncthreads();
+        if (tid < RB) {
+            int a = 0;
+#pragma unroll
+            for (int k = 0; k < KP; ++k) a += part[tid + RB * k];
+            accs[tid] = a;
         }
-    } else {  // EPI_ARGMAX
-        if (tid < kWave) {
-            float v = -__builtin_inff();
-            int idx = 0x7FFFFFFF;
+        __syncthreads();
+
+        // 4. epilogue of this tile
+        if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
             if (tid < RB) {
-                const int r = blockIdx.x * RB + tid;
+                const int r = tile * RB + tid;
                 if (r < p.rows) {
-                    v = (float(accs[tid]) * act) * p.ws[r];
-                    idx = r;
+                    const int a = accs[tid];
+                    const float v = (float(a) * act) * p.ws[r];
+                    if (p.acc_out) p.acc_out[r] = a;
+                    if constexpr (EPI == EPI_STORE) {
+                        p.out[r] = v;
+                    } else {
+                        if (p.out_aux) p.out_aux[r] = v;
+                        p.out[r] = p.out[r] + v;
+                    }
+                }
+            }
+        } else if constexpr (EPI == EPI_SWIGLU) {
+            constexpr int HALF = RB / 2;
+            if (tid < HALF) {
+                const int pair = tile * HALF + tid;
+                if (pair < p.half_rows) {
+                    const int gr = pair, ur = p.half_rows + pair;
+                    const float g = (float(accs[tid]) * act) * p.ws[gr];
+                    const float u = (float(accs[tid + HALF]) * act) * p.ws[ur];
+                    if (p.acc_out) { p.acc_out[gr] = accs[tid]; p.acc_out[ur] = accs[tid + HALF]; }
+                    if (p.out_aux) { p.out_aux[gr] = g; p.out_aux[ur] = u; }
+                    const float t = 1.0f + spec_expf(-g);
+                    p.out[pair] = (g / t) * u;
+                }
+            }
+        } else {  // EPI_ARGMAX: logits out, running block best
+            if (tid < RB) {
+                const int r = tile * RB + tid;
+                if (r < p.rows) {
+                    const float v = (float(accs[tid]) * act) * p.ws[r];
                     p.out[r] = v;
                     if (p.acc_out) p.acc_out[r] = accs[tid];
+                    if (argmax_better(v, r, best_v, best_i)) { best_v = v; best_i = r; }
                 }
             }
+        }
+        if constexpr (!PERSIST) break;
+        if (next >= ntiles) break;
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) {
-                const float ov = __shfl_xor(v, o, kWave);
-                const int oi = __shfl_xor(idx, o, kWave);
-                if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
-            }
-            if (tid == 0) {
-                p.part_val[blockIdx.x] = v;
-                p.part_idx[blockIdx.x] = idx;
-                __threadfence();
-                const int ticket = atomicAdd(p.counter, 1);
-                last_flag = (ticket == int(gridDim.x) - 1);
-            }
+        for (int j = 0; j < MAXC; ++j) wv[j] = wn[j];
+        tile = next;
+    }
+
+    if constexpr (EPI == EPI_ARGMAX) {
+        // block best over the row slots, then the last block to arrive
+        // reduces the per-block partials (no waiting).
+        float v = best_v;
+        int idx = best_i;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(v, o, kWave);
+            const int oi = __shfl_xor(idx, o, kWave);
+            if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
+        }
+        if (tid == 0) {
+            p.part_val[blockIdx.x] = v;
+            p.part_idx[blockIdx.x] = idx;
+            __threadfence();
+            last_flag = (atomicAdd(p.counter, 1) == int(gridDim.x) - 1);
         }
         __syncthreads();
         if (last_flag) {
             __threadfence();
-            float v = -__builtin_inff();
-            int idx = 0x7FFFFFFF;
+            v = -__builtin_inff();
+            idx = 0x7FFFFFFF;
             for (int b = tid; b < int(gridDim.x); b += kBlock) {
                 const float bv = __hip_atomic_load(p.part_val + b, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -260,12 +323,12 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
                 const int oi = __shfl_xor(idx, o, kWave);
                 if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
             }
-            if ((tid & (kWave - 1)) == 0) { red[tid / kWave] = v; part[tid / kWave] = idx; }
+            if ((tid & (kWave - 1)) == 0) { bval[tid / kWave] = v; bidx[tid / kWave] = idx; }
             __syncthreads();
             if (tid == 0) {
 #pragma unroll
                 for (int w = 1; w < kBlock / kWave; ++w)
-                    if (argmax_better(red[w], part[w], v, idx)) { v = red[w]; idx = part[w]; }
+                    if (argmax_better(bval[w], bidx[w], v, idx)) { v = bval[w]; idx = bidx[w]; }
                 *p.token = idx;
                 *p.position = *p.position + 1;
                 *p.counter = 0;
@@ -391,47 +454,60 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* x, int n, f
 // ---------------------------------------------------------------------------
 // host-side dispatch
 // ---------------------------------------------------------------------------
-template <int RB, int MAXC, int XJ, int PRO, int EPI>
+template <int RB, int MAXC, int XJ, int PRO, int EPI, bool PERSIST = false>
 static hipError_t launch(const GemvParams& p, int blocks, hipStream_t s)
 {
-    hipLaunchKernelGGL((gemv_kernel<RB, MAXC, XJ, PRO, EPI>), dim3(blocks), dim3(kBlock),
+    hipLaunchKernelGGL((gemv_kernel<RB, MAXC, XJ, PRO, EPI, PERSIST>), dim3(blocks), dim3(kBlock),
                        size_t(p.width), s, p);
     return hipGetLastError();
 }
 
 // XJ (register-resident activations per thread) is picked from the width.
-template <int RB, int MAXC, int PRO, int EPI>
+template <int RB, int MAXC, int PRO, int EPI, bool PERSIST = false>
 static hipError_t launch_xj(const GemvParams& p, int blocks, hipStream_t s)
 {
-    if (PRO == PRO_I8) return launch<RB, MAXC, 1, PRO, EPI>(p, blocks, s);
-    if (p.width <= 10 * kBlock) return launch<RB, MAXC, 10, PRO, EPI>(p, blocks, s);
-    if (p.width <= 16 * kBlock) return launch<RB, MAXC, 16, PRO, EPI>(p, blocks, s);
-    return launch<RB, MAXC, 40, PRO, EPI>(p, blocks, s);
+    if (PRO == PRO_I8) return launch<RB, MAXC, 1, PRO, EPI, PERSIST>(p, blocks, s);
+    if (p.width <= 10 * kBlock) return launch<RB, MAXC, 10, PRO, EPI, PERSIST>(p, blocks, s);
+    if (p.width <= 16 * kBlock) return launch<RB, MAXC, 16, PRO, EPI, PERSIST>(p, blocks, s);
+    return launch<RB, MAXC, 40, PRO, EPI, PERSIST>(p, blocks, s);
 }
 
 constexpr int kMaxWidth = 40 * kBlock;   // 10240: register-resident activation limit
 
-int step_gemv_blocks(StepGemv kind, int rows, int half_rows)
+// The LM head is a persistent launch: 2 blocks per CU loop over its
+// 4748 tiles with double-buffered weight loads.
+constexpr int kPersistBlocks = 512;
+
+static bool lm_head_persistent(int width) { return width <= 10 * 8 * 32; }
+
+int step_gemv_blocks(StepGemv kind, int rows, int half_rows, int width)
 {
     switch (kind) {
     case StepGemv::Qkv: return (rows + 15) / 16;
     case StepGemv::OResidual: return (rows + 7) / 8;
     case StepGemv::GateUpSwiglu: return (half_rows + 15) / 16;
     case StepGemv::DownResidual: return (rows + 7) / 8;
-    case StepGemv::LmHead: return (rows + 31) / 32;
+    case StepGemv::LmHead: {
+        const int tiles = (rows + 31) / 32;
+        if (!lm_head_persistent(width)) return tiles;
+        return tiles < kPersistBlocks ? tiles : kPersistBlocks;
+    }
     }
     return 0;
 }
 
 hipError_t launch_step_gemv(StepGemv kind, const GemvParams& p, hipStream_t s)
 {
-    const int blocks = step_gemv_blocks(kind, p.rows, p.half_rows);
+    const int blocks = step_gemv_blocks(kind, p.rows, p.half_rows, p.width);
     switch (kind) {
     case StepGemv::Qkv: return launch_xj<16, 5, PRO_RMSNORM, EPI_STORE>(p, blocks, s);
     case StepGemv::OResidual: return launch_xj<8, 4, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
     case StepGemv::GateUpSwiglu: return launch_xj<32, 10, PRO_RMSNORM, EPI_SWIGLU>(p, blocks, s);
     case StepGemv::DownResidual: return launch_xj<8, 10, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
-    case StepGemv::LmHead: return launch_xj<32, 10, PRO_RMSNORM, EPI_ARGMAX>(p, blocks, s);
+    case StepGemv::LmHead:
+        if (lm_head_persistent(p.width))   // one weight batch per tile
+            return launch_xj<32, 10, PRO_RMSNORM, EPI_ARGMAX, true>(p, blocks, s);
+        return launch_xj<32, 10, PRO_RMSNORM, EPI_ARGMAX, false>(p, blocks, s);
     }
     return hipErrorInvalidValue;
 }

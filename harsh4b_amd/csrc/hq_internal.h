@@ -38,7 +38,7 @@ struct GemvParams {
 enum class StepGemv { Qkv, OResidual, GateUpSwiglu, DownResidual, LmHead };
 
 // Number of blocks a step GEMV launches (sizes the argmax partials).
-int step_gemv_blocks(StepGemv kind, int rows, int half_rows);
+int step_gemv_blocks(StepGemv kind, int rows, int half_rows, int width);
 hipError_t launch_step_gemv(StepGemv kind, const GemvParams& p, hipStream_t s);
 
 // ---- attention ---------------------------------------------------------------

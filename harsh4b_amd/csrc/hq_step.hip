@@ -54,7 +54,7 @@ static StepLayout step_layout(const hq_model* m, int capacity)
     L.kv_size = m->kv_heads * m->head_dim;
     L.groups = m->heads / m->kv_heads;
     L.max_chunks = (capacity + kAttnChunk - 1) / kAttnChunk;
-    L.lm_blocks = step_gemv_blocks(StepGemv::LmHead, m->vocab, 0);
+    L.lm_blocks = step_gemv_blocks(StepGemv::LmHead, m->vocab, 0, m->hidden);
     L.attn_part_bytes = align256(attention_workspace_floats(m->heads, L.max_chunks, m->head_dim) * 4);
     L.attn_counter_off = L.attn_part_bytes;
     L.lm_val_off = L.attn_counter_off + align256(size_t(m->kv_heads) * 4);

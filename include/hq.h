@@ -80,8 +80,8 @@ int hq_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps, v
  * hq_gqa_workspace_bytes(context, ...) bytes, 256-byte aligned, zero-filled
  * before its first use; every call leaves its counter words at zero, so one
  * workspace serves any later call whose context needs no more bytes.
- * head_dim in {16, 32, 64, 128}; groups <= 8; context >= 1; keys/values
- * aligned to head_dim/16 halves. */
+ * head_dim in {16, 32, 64, 128}; groups <= 8; context >= 1; keys and
+ * values 16-byte aligned and kv_time_stride a multiple of 8. */
 size_t hq_gqa_workspace_bytes(int context, int kv_heads, int groups, int head_dim);
 int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* values,
                   void* workspace, float* output, int context, int kv_heads, int groups,

@@ -63,9 +63,9 @@ def test_gemv_unaligned_weights_take_generic_path():
     s = rng.random(rows, dtype=np.float32)
     out = torch.empty(rows, dtype=torch.float32, device=dev())
     from harsh4b_amd import _native
-    _native.check(_native.lib().hq_int4_i8_gemv(to_dev(x).data_ptr(), buf.data_ptr() + 1,
-                                                to_dev(s).data_ptr(), 0.5, out.data_ptr(), rows,
-                                                width, None), "gemv")
+    xd, sd = to_dev(x), to_dev(s)      # keep both alive until the kernel has run
+    _native.check(_native.lib().hq_int4_i8_gemv(xd.data_ptr(), buf.data_ptr() + 1, sd.data_ptr(),
+                                                0.5, out.data_ptr(), rows, width, None), "gemv")
     assert_bits_equal(to_host(out), oracle.int4_i8_gemv(x, packed, s, 0.5, rows, width), "unaligned")
 
 
