@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
             const float x0 = src[lane], x1 = src[lane + 64];
             float p = __builtin_fmaf(x0, x0, 0.0f);
             p = __builtin_fmaf(x1, x1, p);
-            const float ss = tree_sum<kWave>(p);
+            const float ss = wave_tree_sum64_all(p);
             const float r = __builtin_sqrtf(ss / float(D) + a.eps);
             const float y0 = (x0 / r) * a.q_norm[lane];
             const float y1 = (x1 / r) * a.q_norm[lane + 64];
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                 const float x0 = src[lane], x1 = src[lane + 64];
                 float p = __builtin_fmaf(x0, x0, 0.0f);
                 p = __builtin_fmaf(x1, x1, p);
-                const float ss = tree_sum<kWave>(p);
+                const float ss = wave_tree_sum64_all(p);
                 const float r = __builtin_sqrtf(ss / float(D) + a.eps);
                 const float y0 = (x0 / r) * a.k_norm[lane];
                 const float y1 = (x1 / r) * a.k_norm[lane + 64];
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                         float pp = 0.0f;
 #pragma unroll
                         for (int j = 0; j < DPL; ++j) pp = __builtin_fmaf(qr[h][j], k[j], pp);
-                        const float dot = tree_sum<16>(pp);
+                        const float dot = row_tree_sum16(pp);
                         if (l16 == 0) e_s[h][i] = dot * scale;
                     }
                 }
@@ -241,9 +241,9 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         // chunk softmax statistics, one wave per head
         for (int h = wave; h < G; h += kBlock / kWave) {
             const float sc = e_s[h][lane];
-            const float m = fmax_group<kWave>(sc);
+            const float m = wave_max64_all(sc);
             const float e = (lane < tn) ? spec_expf(sc - m) : 0.0f;
-            const float l = tree_sum<kWave>(e);
+            const float l = wave_tree_sum64(e);
             e_s[h][lane] = e;
             if (lane == 0) { m_s[h][ci] = m; l_s[h][ci] = l; }
         }
@@ -318,11 +318,11 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
             const int h = h0 + HSTEP * r;
             if (h >= G) continue;
             float* pp = a.part + (size_t(g * G + h) * a.max_chunks + c) * pstride;
-            pp[2 + d] = o_s[ci][h][d];
-            if (d == 0) { pp[0] = m_s[h][ci]; pp[1] = l_s[h][ci]; }
+            publish_f(pp + 2 + d, o_s[ci][h][d]);
+            if (d == 0) { publish_f(pp, m_s[h][ci]); publish_f(pp + 1, l_s[h][ci]); }
         }
     }
-    __threadfence();
+    wait_all_memory();
     __syncthreads();
     if (tid == 0) {
         const int ticket = atomicAdd(a.counters + g, 1);
@@ -330,29 +330,26 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     }
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();
 #pragma unroll
     for (int r = 0; r < PAIRS; ++r) {
         const int h = h0 + HSTEP * r;
         if (h >= G) continue;
         const float* base = a.part + size_t(g * G + h) * a.max_chunks * pstride;
         float M = -__builtin_inff();
-        for (int cc = 0; cc < nc; ++cc)
-            M = fmaxf(M, __hip_atomic_load(base + size_t(cc) * pstride, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT));
+        for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, read_f(base + size_t(cc) * pstride));
         float L = 0.0f, O = 0.0f;
         for (int cc = 0; cc < nc; ++cc) {
             const float* pc = base + size_t(cc) * pstride;
-            const float mc = __hip_atomic_load(pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float lc = __hip_atomic_load(pc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float oc = __hip_atomic_load(pc + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float mc = read_f(pc);
+            const float lc = read_f(pc + 1);
+            const float oc = read_f(pc + 2 + d);
             const float al = spec_expf(mc - M);
             L = __builtin_fmaf(al, lc, L);
             O = __builtin_fmaf(al, oc, O);
         }
         a.out[size_t(g * G + h) * D + d] = O * (1.0f / L);
     }
-    if (tid == 0) a.counters[g] = 0;
+    if (tid == 0) publish_i(a.counters + g, 0);
 }
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim)

@@ -61,39 +61,118 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h)
 }
 
 // ---- wave-level reductions -------------------------------------------------
-// Halving tree across `width` lanes (width a power of two <= 64): after the
-// xor steps width/2 ... 1 every lane of the group holds the tree in which
-// partial i is paired with i + o at each level o -- the order the oracle's
-// tree_sum uses.  fp32 addition is commutative, so lane i and lane i^o form
-// the same sum.
-template <int WIDTH>
-__device__ __forceinline__ float tree_sum(float v)
+// Halving trees: at level o, partial i is paired with partial i + o.  Within
+// a 16-lane row the levels use DPP row_shl (lane i reads lane i + o); across
+// rows gfx950's v_permlane16_swap / v_permlane32_swap pair lane i with lane
+// i + 16 / i + 32.  Every level is one VALU op, no LDS round trip, and the
+// pairing is exactly the oracle's tree_sum order (fp32 addition is
+// commutative, so which lane of a pair adds is irrelevant).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
 {
-#pragma unroll
-    for (int o = WIDTH / 2; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, kWave);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(unsigned, v),
+                                                                  CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
+
+// Cross-row exchanges.  v_permlane32_swap(x, y) swaps the upper 32 lanes of
+// x with the lower 32 lanes of y (v_permlane16_swap: odd 16-lane rows of x
+// with even rows of y); both registers are read and written, so the
+// instructions are written as inline asm with two in/out operands (the
+// compiler's builtin for them folds one of the two results away); the
+// s_nop wait states on either side cover the VALU-write -> swap-read and
+// swap-write -> VALU-read hazards the compiler cannot see through asm.  With
+// y = 0 on entry, lane i < 32 ends with x = v[i], y = v[i + 32]
+// (v[i + 16] for the 16-lane form, lanes i < 16 of each 32-lane half).
+__device__ __forceinline__ void swap32(unsigned& x, unsigned& y)
+{
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ void swap16(unsigned& x, unsigned& y)
+{
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+
+// Levels 32 and 16 of a 64-lane tree, valid in lanes 0..15.
+__device__ __forceinline__ float levels_32_16(float v)
+{
+    unsigned x = __builtin_bit_cast(unsigned, v), y = 0u;
+    swap32(x, y);
+    v = __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+    x = __builtin_bit_cast(unsigned, v);
+    y = 0u;
+    swap16(x, y);
+    return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+}
+
+// 16-lane tree within each DPP row; the total is valid in lane 0 of the row.
+__device__ __forceinline__ float row_tree_sum16(float v)
+{
+    v = v + dpp_f<kRowShl8>(v);
+    v = v + dpp_f<kRowShl4>(v);
+    v = v + dpp_f<kRowShl2>(v);
+    v = v + dpp_f<kRowShl1>(v);
     return v;
 }
 
-template <int WIDTH>
-__device__ __forceinline__ int isum(int v)
+// 64-lane tree; the total is valid in lane 0.
+__device__ __forceinline__ float wave_tree_sum64(float v) { return row_tree_sum16(levels_32_16(v)); }
+
+// 64-lane tree, total broadcast to every lane.
+__device__ __forceinline__ float wave_tree_sum64_all(float v)
 {
-#pragma unroll
-    for (int o = WIDTH / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                         __builtin_bit_cast(unsigned, wave_tree_sum64(v)), 0));
+}
+
+// Integer sum over aligned groups of 8 lanes; valid in the group's first lane.
+__device__ __forceinline__ int group8_isum(int v)
+{
+    v += dpp_i<kRowShl4>(v);
+    v += dpp_i<kRowShl2>(v);
+    v += dpp_i<kRowShl1>(v);
     return v;
 }
 
-template <int WIDTH>
-__device__ __forceinline__ float fmax_group(float v)
+// Integer sum over the wave (order-free); valid in lane 0.
+__device__ __forceinline__ int wave_isum64(int v)
 {
-#pragma unroll
-    for (int o = WIDTH / 2; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    unsigned x = unsigned(v), y = 0u;
+    swap32(x, y);
+    x = unsigned(int(x) + int(y));
+    y = 0u;
+    swap16(x, y);
+    v = int(x) + int(y);
+    v += dpp_i<kRowShl8>(v);
+    return group8_isum(v);
+}
+
+// Max over the wave (order-free), read from lane 0 and broadcast to every lane.
+__device__ __forceinline__ float wave_max64_all(float v)
+{
+    unsigned x = __builtin_bit_cast(unsigned, v), y = x;
+    swap32(x, y);
+    v = fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
+    x = __builtin_bit_cast(unsigned, v);
+    y = x;
+    swap16(x, y);
+    v = fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
+    v = fmaxf(v, dpp_f<kRowShl8>(v));
+    v = fmaxf(v, dpp_f<kRowShl4>(v));
+    v = fmaxf(v, dpp_f<kRowShl2>(v));
+    v = fmaxf(v, dpp_f<kRowShl1>(v));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(unsigned, v), 0));
 }
 
 // Block-wide (256 threads) max of non-negative values; `red` is 4 floats of LDS.
 __device__ __forceinline__ float block_max_nonneg(float v, float* red)
 {
-    v = fmax_group<kWave>(v);
+    v = wave_max64_all(v);
     const int wave = threadIdx.x / kWave;
     if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
     __syncthreads();
@@ -113,16 +192,63 @@ __device__ __forceinline__ float block_tree_sum256(float v, float* red)
     __syncthreads();
     if (t < 128) red[t] = red[t] + red[t + 128];
     __syncthreads();
-    float r = 0.0f;
     if (t < 64) {
-        r = red[t] + red[t + 64];
-        r = tree_sum<kWave>(r);
+        const float r = wave_tree_sum64(red[t] + red[t + 64]);
         if (t == 0) red[0] = r;
     }
     __syncthreads();
-    r = red[0];
+    const float r = red[0];
     __syncthreads();
     return r;
+}
+
+// ---- cross-block hand-off without fences ------------------------------------
+// A full fence (__threadfence) writes back the XCD's L2 and costs tens of
+// microseconds when hundreds of blocks issue it, and same-address atomics
+// serialise at ~20 ns each.  Blocks therefore publish data with agent-scope
+// atomic stores (written through to the coherence point), wait for them to
+// complete, and only then take a ticket; readers use agent-scope atomic
+// loads.  publish_f/i, read_f/i are those accesses.
+__device__ __forceinline__ void publish_f(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_i(int* p, int v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float read_f(const float* p)
+{
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int read_i(const int* p)
+{
+    return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this thread issued has completed.
+__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+constexpr int kTicketGroup = 32;   // blocks per first-level ticket counter
+
+// Two-level arrival ticket for `nblocks` blocks, called by one thread per
+// block after __syncthreads() has ordered the block's published writes.
+// counters: [ceil(nblocks / 32) group counters][1 top counter], zero between
+// uses; the function leaves them zero again.  Returns true in exactly one
+// block, the last to arrive, after all others have published.
+__device__ __forceinline__ bool last_block_ticket(int* counters, int block, int nblocks)
+{
+    const int groups = (nblocks + kTicketGroup - 1) / kTicketGroup;
+    const int g = block / kTicketGroup;
+    const int gsize = min(kTicketGroup, nblocks - g * kTicketGroup);
+    if (atomicAdd(counters + g, 1) != gsize - 1) return false;
+    publish_i(counters + g, 0);
+    if (atomicAdd(counters + groups, 1) != groups - 1) return false;
+    publish_i(counters + groups, 0);
+    return true;
+}
+__host__ __device__ constexpr int ticket_words(int nblocks)
+{
+    return (nblocks + kTicketGroup - 1) / kTicketGroup + 1;
 }
 
 // Argmax order of np.argmax: a NaN beats any number, the lowest index wins

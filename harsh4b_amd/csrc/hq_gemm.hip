@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmParams p)
             if (mm < p.m && n < p.n) atomicAdd(p.acc + size_t(mm) * p.n + n, acc[b][r] >> 4);
         }
     }
-    __threadfence();
+    wait_all_memory();   // this thread's atomic adds have been performed
     __syncthreads();
     if (tid == 0) {
         const int ticket = atomicAdd(p.counters + tile, 1);
@@ -151,18 +151,17 @@ __global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmParams p)
     }
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();
     const int trows = min(kTileRows, p.n - tile * kTileRows);
     for (int e = tid; e < p.m * trows; e += kBlock) {
         const int mm = e / trows;
         const int n = tile * kTileRows + e % trows;
         int32_t* cell = p.acc + size_t(mm) * p.n + n;
-        const int a = __hip_atomic_load(cell, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int a = read_i(cell);
         p.out[size_t(mm) * p.n + n] = (float(a) * p.act[mm]) * p.ws[n];
         if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
-        __hip_atomic_store(cell, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        publish_i(cell, 0);
     }
-    if (tid == 0) p.counters[tile] = 0;
+    if (tid == 0) publish_i(p.counters + tile, 0);
 }
 
 // Per-sequence spec quantization: block m quantizes row m.

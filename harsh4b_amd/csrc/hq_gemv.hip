@@ -36,20 +36,21 @@ __device__ __forceinline__ uint4 load_w16(const uint8_t* p)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ int dot_chunk(uint4 w, const uint8_t* xs_chunk, int acc)
+// 16 * sum(w * x) over one 16-byte weight chunk, accumulated into two
+// independent integer chains (integer addition is exact in any order).
+__device__ __forceinline__ void dot_chunk(uint4 w, const uint8_t* xs_chunk, int& a0, int& a1)
 {
     const uint4 xa = *reinterpret_cast<const uint4*>(xs_chunk);
     const uint4 xb = *reinterpret_cast<const uint4*>(xs_chunk + 16);
     const int m = int(0xF0F0F0F0u);
-    acc = __builtin_amdgcn_sdot4(int(w.x << 4) & m, int(xa.x), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.x) & m, int(xa.y), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.y << 4) & m, int(xa.z), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.y) & m, int(xa.w), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.z << 4) & m, int(xb.x), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.z) & m, int(xb.y), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.w << 4) & m, int(xb.z), acc, false);
-    acc = __builtin_amdgcn_sdot4(int(w.w) & m, int(xb.w), acc, false);
-    return acc;
+    a0 = __builtin_amdgcn_sdot4(int(w.x << 4) & m, int(xa.x), a0, false);
+    a1 = __builtin_amdgcn_sdot4(int(w.x) & m, int(xa.y), a1, false);
+    a0 = __builtin_amdgcn_sdot4(int(w.y << 4) & m, int(xa.z), a0, false);
+    a1 = __builtin_amdgcn_sdot4(int(w.y) & m, int(xa.w), a1, false);
+    a0 = __builtin_amdgcn_sdot4(int(w.z << 4) & m, int(xb.x), a0, false);
+    a1 = __builtin_amdgcn_sdot4(int(w.z) & m, int(xb.y), a1, false);
+    a0 = __builtin_amdgcn_sdot4(int(w.w << 4) & m, int(xb.z), a0, false);
+    a1 = __builtin_amdgcn_sdot4(int(w.w) & m, int(xb.w), a1, false);
 }
 
 // Activation registers: element i = tid + 256*j of x (and gamma) is held
@@ -122,59 +123,81 @@ __device__ __forceinline__ float activation_prologue(const GemvParams& p, ActReg
     }
 }
 
-// Rows of row-slot `slot` in tile `tile`.
-template <int RB, int EPI>
-__device__ __forceinline__ int tile_row(const GemvParams& p, int tile, int slot, bool& valid)
+// ---------------------------------------------------------------------------
+// Kernel shape: a wave owns whole rows.  LPR lanes (8, 16, 32 or 64) read one
+// row, RPW = 64 / LPR rows per wave, RB = 4 * RPW rows per 256-thread block
+// (a "tile").  Lane l of a row loads chunks l, l + LPR, ... (16 bytes = 32
+// int4 values each), so a row's lanes read LPR*16 contiguous bytes per load.
+// Row sums leave the wave through DPP and readlane: no LDS and no barrier
+// between the dot products and the epilogue.  With EPI_SWIGLU, RPW = 2 and
+// a wave's rows are gate rows followed by the matching up rows.
+template <int LPR>
+__device__ __forceinline__ int row_isum(int v, int r)
 {
-    if constexpr (EPI == EPI_SWIGLU) {
-        constexpr int HALF = RB / 2;
-        const int pair = tile * HALF + (slot % HALF);
-        valid = pair < p.half_rows;
-        return (slot < HALF) ? pair : p.half_rows + pair;
+    // v: per-lane partial; returns the total of row r of the wave (uniform)
+    if constexpr (LPR == 8) {
+        v = group8_isum(v);
+        return __builtin_amdgcn_readlane(v, 8 * r);
     } else {
-        const int row = tile * RB + slot;
+        v += dpp_i<kRowShl8>(v);
+        v = group8_isum(v);
+        if constexpr (LPR == 16) return __builtin_amdgcn_readlane(v, 16 * r);
+        if constexpr (LPR == 32)
+            return __builtin_amdgcn_readlane(v, 32 * r) + __builtin_amdgcn_readlane(v, 32 * r + 16);
+        return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+               __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+    }
+}
+
+template <int LPR, int EPI>
+__device__ __forceinline__ int wave_row(const GemvParams& p, int tile, int wave, int r, bool& valid)
+{
+    constexpr int RPW = kWave / LPR;
+    if constexpr (EPI == EPI_SWIGLU) {
+        // the wave's rows 0..RPW/2-1 are gate rows, the next RPW/2 the
+        // matching up rows
+        constexpr int PPW = RPW / 2;
+        static_assert(PPW >= 1, "SwiGLU tiles need at least two rows per wave");
+        const int pair = (tile * 4 + wave) * PPW + (r % PPW);
+        valid = pair < p.half_rows;
+        return r < PPW ? pair : p.half_rows + pair;
+    } else {
+        const int row = (tile * 4 + wave) * RPW + r;
         valid = row < p.rows;
         return row;
     }
 }
 
-// Loads are unconditional (chunk index clamped; rows past the end read row
-// 0) so that no branch separates them and the wait counters stay exact; the
-// dot loop skips chunks past the row and the epilogue drops invalid rows.
 template <int MAXC, int LPR>
-__device__ __forceinline__ void load_tile(const uint8_t* wrow, int lir, int base, int nchunks,
-                                          uint4 (&wv)[MAXC])
+__device__ __forceinline__ void load_tile(const uint8_t* wrow, int li, int nchunks, uint4 (&wv)[MAXC])
 {
+    // unconditional (clamped) loads: no branch separates them, so the wait
+    // counters stay exact; chunks past the row are skipped in the dot loop
 #pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        const int c = min(base + lir + j * LPR, nchunks - 1);
-        wv[j] = load_w16(wrow + size_t(c) * 16);
-    }
+    for (int j = 0; j < MAXC; ++j) wv[j] = load_w16(wrow + size_t(min(li + j * LPR, nchunks - 1)) * 16);
 }
 
-// Tiles: a tile is RB output rows.  Non-persistent launches give each block
-// one tile; persistent launches (PERSIST) loop over tiles blockIdx.x +
-// k*gridDim.x with the next tile's weights in flight while the current one
-// is reduced (two register buffers), and need width <= MAXC*LPR*32.
-template <int RB, int MAXC, int XJ, int PRO, int EPI, bool PERSIST>
+// Tiles: non-persistent launches give each block one tile (and walk wide
+// rows in batches of MAXC chunks per lane); persistent launches (PERSIST)
+// loop over tiles blockIdx.x + k*gridDim.x with the next tile's weights in
+// flight during the current tile's dot products, and need
+// width <= MAXC*LPR*32.
+template <int LPR, int MAXC, int XJ, int PRO, int EPI, bool PERSIST>
 __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
 {
-    constexpr int KP = 32 / RB;
-    constexpr int LPR = 8 * KP;
+    constexpr int RPW = kWave / LPR;
+    constexpr int RB = 4 * RPW;
     extern __shared__ __align__(16) uint8_t xs[];
     __shared__ float red[kBlock];
-    __shared__ int part[32];
-    __shared__ int accs[32];
     __shared__ float bval[kBlock / kWave];
     __shared__ int bidx[kBlock / kWave];
     __shared__ int last_flag;
 
     const int tid = threadIdx.x;
-    const int grp = tid >> 3;
-    const int li = tid & 7;
-    const int slot = grp % RB;
-    const int kp = grp / RB;
-    const int lir = kp * 8 + li;
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
+    const int rsel = lane / LPR;          // row of the wave this lane reads
+    const int li = lane % LPR;            // lane within the row
     const int K = p.width;
     const int nchunks = K >> 5;
     const int ntiles = (EPI == EPI_SWIGLU) ? (p.half_rows + RB / 2 - 1) / (RB / 2)
@@ -185,10 +208,10 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     load_activation<XJ, PRO>(p, areg);
     int tile = blockIdx.x;
     bool valid;
-    int row = tile_row<RB, EPI>(p, tile, slot, valid);
+    int row = wave_row<LPR, EPI>(p, tile, wave, rsel, valid);
     const uint8_t* wrow = p.w + size_t(valid ? row : 0) * size_t(K >> 1);
     uint4 wv[MAXC];
-    load_tile<MAXC, LPR>(wrow, lir, 0, nchunks, wv);
+    load_tile<MAXC, LPR>(wrow, li, nchunks, wv);
     // keep the scheduler from sinking the weight loads below the first use
     // of the activations: the HBM stream must start before any wait
     __builtin_amdgcn_sched_barrier(0);
@@ -197,86 +220,87 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     const float act = activation_prologue<XJ, PRO>(p, areg, xs, red);
     __syncthreads();
 
-    float best_v = -__builtin_inff();   // EPI_ARGMAX: running best of this block
+    float best_v = -__builtin_inff();   // EPI_ARGMAX: running best of this lane's rows
     int best_i = 0x7FFFFFFF;
     while (true) {
         // 3. prefetch the next tile (persistent), dot products of this one
         const int next = tile + int(gridDim.x);
         uint4 wn[PERSIST ? MAXC : 1];
-        bool nvalid = false;
-        int nrow = 0;
         if constexpr (PERSIST) {
             if (next < ntiles) {
-                nrow = tile_row<RB, EPI>(p, next, slot, nvalid);
-                load_tile<MAXC, LPR>(p.w + size_t(nvalid ? nrow : 0) * size_t(K >> 1), lir, 0,
-                                     nchunks, wn);
+                bool nvalid;
+                const int nrow = wave_row<LPR, EPI>(p, next, wave, rsel, nvalid);
+                load_tile<MAXC, LPR>(p.w + size_t(nvalid ? nrow : 0) * size_t(K >> 1), li, nchunks, wn);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        int acc16 = 0;
+        int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
 #pragma unroll
         for (int j = 0; j < MAXC; ++j) {
-            const int c = lir + j * LPR;
-            if (c < nchunks) acc16 = dot_chunk(wv[j], xs + c * 32, acc16);
+            const int c = li + j * LPR;
+            if (c < nchunks) {
+                if (j & 1) dot_chunk(wv[j], xs + c * 32, a2, a3);
+                else dot_chunk(wv[j], xs + c * 32, a0, a1);
+            }
         }
         if constexpr (!PERSIST) {
             for (int base = MAXC * LPR; base < nchunks; base += MAXC * LPR) {
-                load_tile<MAXC, LPR>(wrow, lir, base, nchunks, wv);
+#pragma unroll
+                for (int j = 0; j < MAXC; ++j)
+                    wv[j] = load_w16(wrow + size_t(min(base + li + j * LPR, nchunks - 1)) * 16);
 #pragma unroll
                 for (int j = 0; j < MAXC; ++j) {
-                    const int c = base + lir + j * LPR;
-                    if (c < nchunks) acc16 = dot_chunk(wv[j], xs + c * 32, acc16);
-                }
-            }
-        }
-        acc16 = isum<8>(acc16);
-        if (li == 0) part[grp] = acc16 >> 4;
-        __syncthreads();
-        if (tid < RB) {
-            int a = 0;
-#pragma unroll
-            for (int k = 0; k < KP; ++k) a += part[tid + RB * k];
-            accs[tid] = a;
-        }
-        __syncthreads();
-
-        // 4. epilogue of this tile
-        if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
-            if (tid < RB) {
-                const int r = tile * RB + tid;
-                if (r < p.rows) {
-                    const int a = accs[tid];
-                    const float v = (float(a) * act) * p.ws[r];
-                    if (p.acc_out) p.acc_out[r] = a;
-                    if constexpr (EPI == EPI_STORE) {
-                        p.out[r] = v;
-                    } else {
-                        if (p.out_aux) p.out_aux[r] = v;
-                        p.out[r] = p.out[r] + v;
+                    const int c = base + li + j * LPR;
+                    if (c < nchunks) {
+                        if (j & 1) dot_chunk(wv[j], xs + c * 32, a2, a3);
+                        else dot_chunk(wv[j], xs + c * 32, a0, a1);
                     }
                 }
             }
-        } else if constexpr (EPI == EPI_SWIGLU) {
-            constexpr int HALF = RB / 2;
-            if (tid < HALF) {
-                const int pair = tile * HALF + tid;
-                if (pair < p.half_rows) {
-                    const int gr = pair, ur = p.half_rows + pair;
-                    const float g = (float(accs[tid]) * act) * p.ws[gr];
-                    const float u = (float(accs[tid + HALF]) * act) * p.ws[ur];
-                    if (p.acc_out) { p.acc_out[gr] = accs[tid]; p.acc_out[ur] = accs[tid + HALF]; }
+        }
+        const int part = (a0 + a1) + (a2 + a3);
+
+        // 4. epilogue of this tile: lane r < RPW finishes row r of the wave
+        int acc = 0;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int t = row_isum<LPR>(part, r) >> 4;
+            if (lane == r) acc = t;
+        }
+        if constexpr (EPI == EPI_SWIGLU) {
+            constexpr int PPW = RPW / 2;
+            int acc_up = 0;
+#pragma unroll
+            for (int r = 0; r < PPW; ++r) {
+                const int t = row_isum<LPR>(part, r + PPW) >> 4;
+                if (lane == r) acc_up = t;
+            }
+            if (lane < PPW) {
+                bool ok;
+                const int gr = wave_row<LPR, EPI>(p, tile, wave, lane, ok);
+                if (ok) {
+                    const int ur = p.half_rows + gr;
+                    const float g = (float(acc) * act) * p.ws[gr];
+                    const float u = (float(acc_up) * act) * p.ws[ur];
+                    if (p.acc_out) { p.acc_out[gr] = acc; p.acc_out[ur] = acc_up; }
                     if (p.out_aux) { p.out_aux[gr] = g; p.out_aux[ur] = u; }
                     const float t = 1.0f + spec_expf(-g);
-                    p.out[pair] = (g / t) * u;
+                    p.out[gr] = (g / t) * u;
                 }
             }
-        } else {  // EPI_ARGMAX: logits out, running block best
-            if (tid < RB) {
-                const int r = tile * RB + tid;
-                if (r < p.rows) {
-                    const float v = (float(accs[tid]) * act) * p.ws[r];
+        } else if (lane < RPW) {
+            bool ok;
+            const int r = wave_row<LPR, EPI>(p, tile, wave, lane, ok);
+            if (ok) {
+                const float v = (float(acc) * act) * p.ws[r];
+                if (p.acc_out) p.acc_out[r] = acc;
+                if constexpr (EPI == EPI_STORE) {
                     p.out[r] = v;
-                    if (p.acc_out) p.acc_out[r] = accs[tid];
+                } else if constexpr (EPI == EPI_RESIDUAL) {
+                    if (p.out_aux) p.out_aux[r] = v;
+                    p.out[r] = p.out[r] + v;
+                } else {   // EPI_ARGMAX
+                    p.out[r] = v;
                     if (argmax_better(v, r, best_v, best_i)) { best_v = v; best_i = r; }
                 }
             }
@@ -289,8 +313,8 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     }
 
     if constexpr (EPI == EPI_ARGMAX) {
-        // block best over the row slots, then the last block to arrive
-        // reduces the per-block partials (no waiting).
+        // block best, then the last block to arrive reduces the per-block
+        // partials (no waiting)
         float v = best_v;
         int idx = best_i;
 #pragma unroll
@@ -299,22 +323,24 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
             const int oi = __shfl_xor(idx, o, kWave);
             if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
         }
+        if (lane == 0) { bval[wave] = v; bidx[wave] = idx; }
+        __syncthreads();
         if (tid == 0) {
-            p.part_val[blockIdx.x] = v;
-            p.part_idx[blockIdx.x] = idx;
-            __threadfence();
-            last_flag = (atomicAdd(p.counter, 1) == int(gridDim.x) - 1);
+#pragma unroll
+            for (int w = 1; w < kBlock / kWave; ++w)
+                if (argmax_better(bval[w], bidx[w], v, idx)) { v = bval[w]; idx = bidx[w]; }
+            publish_f(p.part_val + blockIdx.x, v);
+            publish_i(p.part_idx + blockIdx.x, idx);
+            wait_all_memory();
+            last_flag = last_block_ticket(p.counter, blockIdx.x, gridDim.x);
         }
         __syncthreads();
         if (last_flag) {
-            __threadfence();
             v = -__builtin_inff();
             idx = 0x7FFFFFFF;
             for (int b = tid; b < int(gridDim.x); b += kBlock) {
-                const float bv = __hip_atomic_load(p.part_val + b, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-                const int bi = __hip_atomic_load(p.part_idx + b, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+                const float bv = read_f(p.part_val + b);
+                const int bi = read_i(p.part_idx + b);
                 if (argmax_better(bv, bi, v, idx)) { v = bv; idx = bi; }
             }
 #pragma unroll
@@ -323,7 +349,8 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
                 const int oi = __shfl_xor(idx, o, kWave);
                 if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
             }
-            if ((tid & (kWave - 1)) == 0) { bval[tid / kWave] = v; bidx[tid / kWave] = idx; }
+            __syncthreads();
+            if (lane == 0) { bval[wave] = v; bidx[wave] = idx; }
             __syncthreads();
             if (tid == 0) {
 #pragma unroll
@@ -331,7 +358,6 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
                     if (argmax_better(bval[w], bidx[w], v, idx)) { v = bval[w]; idx = bidx[w]; }
                 *p.token = idx;
                 *p.position = *p.position + 1;
-                *p.counter = 0;
             }
         }
     }
@@ -357,7 +383,7 @@ __global__ __launch_bounds__(kBlock) void gemv_generic_kernel(
         const int hi = int(int8_t(b)) >> 4;
         acc += lo * int(x[2 * j]) + hi * int(x[2 * j + 1]);
     }
-    acc = isum<kWave>(acc);
+    acc = wave_isum64(acc);
     if (lane == 0) {
         out[row] = (float(acc) * act) * ws[row];
         if (acc_out) acc_out[row] = acc;
@@ -419,19 +445,18 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* x, int n, f
     if (tid == 0) {
         for (int w = 1; w < kBlock / kWave; ++w)
             if (argmax_better(sv[w], si[w], v, idx)) { v = sv[w]; idx = si[w]; }
-        pval[blockIdx.x] = v;
-        pidx[blockIdx.x] = idx;
-        __threadfence();
-        last_flag = (atomicAdd(counter, 1) == int(gridDim.x) - 1);
+        publish_f(pval + blockIdx.x, v);
+        publish_i(pidx + blockIdx.x, idx);
+        wait_all_memory();
+        last_flag = last_block_ticket(counter, blockIdx.x, gridDim.x);
     }
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();
     v = -__builtin_inff();
     idx = 0x7FFFFFFF;
     for (int b = tid; b < int(gridDim.x); b += kBlock) {
-        const float bv = __hip_atomic_load(pval + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int bi = __hip_atomic_load(pidx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float bv = read_f(pval + b);
+        const int bi = read_i(pidx + b);
         if (argmax_better(bv, bi, v, idx)) { v = bv; idx = bi; }
     }
 #pragma unroll
@@ -447,50 +472,60 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* x, int n, f
         for (int w = 1; w < kBlock / kWave; ++w)
             if (argmax_better(sv[w], si[w], v, idx)) { v = sv[w]; idx = si[w]; }
         *out = idx;
-        *counter = 0;
     }
 }
 
 // ---------------------------------------------------------------------------
 // host-side dispatch
 // ---------------------------------------------------------------------------
-template <int RB, int MAXC, int XJ, int PRO, int EPI, bool PERSIST = false>
+template <int LPR, int MAXC, int XJ, int PRO, int EPI, bool PERSIST = false>
 static hipError_t launch(const GemvParams& p, int blocks, hipStream_t s)
 {
-    hipLaunchKernelGGL((gemv_kernel<RB, MAXC, XJ, PRO, EPI, PERSIST>), dim3(blocks), dim3(kBlock),
+    hipLaunchKernelGGL((gemv_kernel<LPR, MAXC, XJ, PRO, EPI, PERSIST>), dim3(blocks), dim3(kBlock),
                        size_t(p.width), s, p);
     return hipGetLastError();
 }
 
 // XJ (register-resident activations per thread) is picked from the width.
-template <int RB, int MAXC, int PRO, int EPI, bool PERSIST = false>
+template <int LPR, int MAXC, int PRO, int EPI, bool PERSIST = false>
 static hipError_t launch_xj(const GemvParams& p, int blocks, hipStream_t s)
 {
-    if (PRO == PRO_I8) return launch<RB, MAXC, 1, PRO, EPI, PERSIST>(p, blocks, s);
-    if (p.width <= 10 * kBlock) return launch<RB, MAXC, 10, PRO, EPI, PERSIST>(p, blocks, s);
-    if (p.width <= 16 * kBlock) return launch<RB, MAXC, 16, PRO, EPI, PERSIST>(p, blocks, s);
-    return launch<RB, MAXC, 40, PRO, EPI, PERSIST>(p, blocks, s);
+    if (PRO == PRO_I8) return launch<LPR, MAXC, 1, PRO, EPI, PERSIST>(p, blocks, s);
+    if (p.width <= 10 * kBlock) return launch<LPR, MAXC, 10, PRO, EPI, PERSIST>(p, blocks, s);
+    if (p.width <= 16 * kBlock) return launch<LPR, MAXC, 16, PRO, EPI, PERSIST>(p, blocks, s);
+    return launch<LPR, MAXC, 40, PRO, EPI, PERSIST>(p, blocks, s);
 }
 
 constexpr int kMaxWidth = 40 * kBlock;   // 10240: register-resident activation limit
 
-// The LM head is a persistent launch: 2 blocks per CU loop over its
-// 4748 tiles with double-buffered weight loads.
+// Lanes per row of each step GEMV (rows per 256-thread tile = 4 * 64 / LPR),
+// chosen so every lane streams 3..10 chunks and the launch fills the chip:
+//   qkv      K 2560  16 lanes/row  5 chunks/lane  384 tiles
+//   o        K 4096  32 lanes/row  4 chunks/lane  320 tiles
+//   gate_up  K 2560   8 lanes/row 10 chunks/lane  608 tiles (16 gate/up pairs)
+//   down     K 9728  32 lanes/row 10 chunks/lane  320 tiles
+//   LM head  K 2560   8 lanes/row 10 chunks/lane 4748 tiles, persistent:
+//            2 blocks per CU loop over the tiles
+constexpr int kQkvLPR = 16, kOLPR = 32, kGateLPR = 8, kDownLPR = 32, kHeadLPR = 8;
 constexpr int kPersistBlocks = 512;
+constexpr int kDefaultLPR = 32;
+constexpr int kDefaultRB = 4 * (kWave / kDefaultLPR);
 
-static bool lm_head_persistent(int width) { return width <= 10 * 8 * 32; }
+static int rows_per_tile(int lpr) { return 4 * (kWave / lpr); }
+static bool lm_head_persistent(int width) { return width <= 10 * kHeadLPR * 32; }
 
 int step_gemv_blocks(StepGemv kind, int rows, int half_rows, int width)
 {
+    auto tiles = [](int n, int per) { return (n + per - 1) / per; };
     switch (kind) {
-    case StepGemv::Qkv: return (rows + 15) / 16;
-    case StepGemv::OResidual: return (rows + 7) / 8;
-    case StepGemv::GateUpSwiglu: return (half_rows + 15) / 16;
-    case StepGemv::DownResidual: return (rows + 7) / 8;
+    case StepGemv::Qkv: return tiles(rows, rows_per_tile(kQkvLPR));
+    case StepGemv::OResidual: return tiles(rows, rows_per_tile(kOLPR));
+    case StepGemv::GateUpSwiglu: return tiles(half_rows, rows_per_tile(kGateLPR) / 2);
+    case StepGemv::DownResidual: return tiles(rows, rows_per_tile(kDownLPR));
     case StepGemv::LmHead: {
-        const int tiles = (rows + 31) / 32;
-        if (!lm_head_persistent(width)) return tiles;
-        return tiles < kPersistBlocks ? tiles : kPersistBlocks;
+        const int t = tiles(rows, rows_per_tile(kHeadLPR));
+        if (!lm_head_persistent(width)) return t;
+        return t < kPersistBlocks ? t : kPersistBlocks;
     }
     }
     return 0;
@@ -500,14 +535,14 @@ hipError_t launch_step_gemv(StepGemv kind, const GemvParams& p, hipStream_t s)
 {
     const int blocks = step_gemv_blocks(kind, p.rows, p.half_rows, p.width);
     switch (kind) {
-    case StepGemv::Qkv: return launch_xj<16, 5, PRO_RMSNORM, EPI_STORE>(p, blocks, s);
-    case StepGemv::OResidual: return launch_xj<8, 4, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
-    case StepGemv::GateUpSwiglu: return launch_xj<32, 10, PRO_RMSNORM, EPI_SWIGLU>(p, blocks, s);
-    case StepGemv::DownResidual: return launch_xj<8, 10, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
+    case StepGemv::Qkv: return launch_xj<kQkvLPR, 5, PRO_RMSNORM, EPI_STORE>(p, blocks, s);
+    case StepGemv::OResidual: return launch_xj<kOLPR, 4, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
+    case StepGemv::GateUpSwiglu: return launch_xj<kGateLPR, 10, PRO_RMSNORM, EPI_SWIGLU>(p, blocks, s);
+    case StepGemv::DownResidual: return launch_xj<kDownLPR, 10, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
     case StepGemv::LmHead:
         if (lm_head_persistent(p.width))   // one weight batch per tile
-            return launch_xj<32, 10, PRO_RMSNORM, EPI_ARGMAX, true>(p, blocks, s);
-        return launch_xj<32, 10, PRO_RMSNORM, EPI_ARGMAX, false>(p, blocks, s);
+            return launch_xj<kHeadLPR, 10, PRO_RMSNORM, EPI_ARGMAX, true>(p, blocks, s);
+        return launch_xj<kHeadLPR, 10, PRO_RMSNORM, EPI_ARGMAX, false>(p, blocks, s);
     }
     return hipErrorInvalidValue;
 }
@@ -532,9 +567,7 @@ extern "C" int hq_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const fl
         GemvParams p{};
         p.w = weights; p.ws = scales; p.rows = rows; p.width = width;
         p.xq = x; p.act_scale = activation_scale; p.out = output;
-        const int rb = rows >= 4096 ? 32 : 8;
-        e = rb == 32 ? launch<32, 8, 1, PRO_I8, EPI_STORE>(p, (rows + 31) / 32, s)
-                     : launch<8, 8, 1, PRO_I8, EPI_STORE>(p, (rows + 7) / 8, s);
+        e = launch<kDefaultLPR, 8, 1, PRO_I8, EPI_STORE>(p, (rows + kDefaultRB - 1) / kDefaultRB, s);
     } else {
         const int per = kBlock / kWave;
         hipLaunchKernelGGL(gemv_generic_kernel, dim3((rows + per - 1) / per), dim3(kBlock), 0, s,
@@ -559,12 +592,7 @@ extern "C" int hq_quant_int4_gemv(const float* x, const uint8_t* weights, const 
     p.xf = x; p.out = output; p.q_out = q_out; p.act_out = act_scale_out; p.acc_out = acc_out;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (rows >= 8192)
-        e = launch_xj<32, 10, PRO_QUANT, EPI_STORE>(p, (rows + 31) / 32, s);
-    else if (rows >= 4096)
-        e = launch_xj<16, 10, PRO_QUANT, EPI_STORE>(p, (rows + 15) / 16, s);
-    else
-        e = launch_xj<8, 10, PRO_QUANT, EPI_STORE>(p, (rows + 7) / 8, s);
+    e = launch_xj<kDefaultLPR, 10, PRO_QUANT, EPI_STORE>(p, (rows + kDefaultRB - 1) / kDefaultRB, s);
     return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }
 
@@ -590,7 +618,8 @@ extern "C" size_t hq_argmax_workspace_bytes(int n)
 {
     if (n <= 0) return 0;
     const size_t blocks = (size_t(n) + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
-    return 256 + blocks * 8;   // counter first (fixed place), then the partials
+    // arrival counters first, then the partials
+    return ((size_t(ticket_words(int(blocks))) * 4 + 255) & ~size_t(255)) + blocks * 8;
 }
 
 extern "C" int hq_argmax(const float* x, int n, int32_t* out_index, void* workspace, void* stream)
@@ -599,9 +628,10 @@ extern "C" int hq_argmax(const float* x, int n, int32_t* out_index, void* worksp
     if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return HQ_ERR_ALIGN;
     const int blocks = (n + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
     char* ws = static_cast<char*>(workspace);
+    const size_t off = (size_t(ticket_words(blocks)) * 4 + 255) & ~size_t(255);
     int32_t* counter = reinterpret_cast<int32_t*>(ws);
-    float* pval = reinterpret_cast<float*>(ws + 256);
-    int32_t* pidx = reinterpret_cast<int32_t*>(ws + 256 + size_t(blocks) * 4);
+    float* pval = reinterpret_cast<float*>(ws + off);
+    int32_t* pidx = reinterpret_cast<int32_t*>(ws + off + size_t(blocks) * 4);
     hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), x, n, pval, pidx, counter, out_index);
     return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;

@@ -60,7 +60,7 @@ static StepLayout step_layout(const hq_model* m, int capacity)
     L.lm_val_off = L.attn_counter_off + align256(size_t(m->kv_heads) * 4);
     L.lm_idx_off = L.lm_val_off + align256(size_t(L.lm_blocks) * 4);
     L.lm_counter_off = L.lm_idx_off + align256(size_t(L.lm_blocks) * 4);
-    L.total = L.lm_counter_off + 256;
+    L.total = L.lm_counter_off + align256(size_t(ticket_words(L.lm_blocks)) * 4);
     return L;
 }
 
