@@ -8,10 +8,15 @@ after a 64-token random prompt.  A "step" is one decode token: 144 body
 GEMVs + 36 attentions + LM head + argmax, replayed from a HIP graph with the
 greedy token fed back on the device.
 
-Printed as one JSON line: tok/s (value), the body-GEMV roofline of the
-dominant kernel measured live with HIP events, the aggregate body-GEMV
-bandwidth, and the CPU oracle's tok/s on this host's cores for the same
-model and context (cpu_baseline, a bounded sample).
+Printed as one JSON line: tok/s (value), the HBM roofline of the dominant
+kernel (the fused RMSNorm + quant + gate/up GEMV + SwiGLU, the largest body
+stream per launch and the largest share of the step) measured live with HIP
+events on the launch stream, the aggregate body-GEMV bandwidth, and the CPU
+oracle's tok/s on this host's cores for the same model and context
+(cpu_baseline, a bounded sample).  `roofline.traffic` is the HBM bytes per
+launch of that kernel from the committed PMC profile
+(profiles/decode_traffic_pmc.json: FETCH_SIZE and WRITE_SIZE scaled by a copy
+kernel's reading), or null when the profile is absent.
 """
 from __future__ import annotations
 
@@ -27,6 +32,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+DOMINANT = "gate_up"
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_traffic_pmc.json"
 METRIC = "decode tok/s @ Qwen3-4B batch 1; body-GEMV HBM GB/s as % of peak"
 
 
@@ -64,6 +71,15 @@ def algorithmic_bytes(config):
     r, w = sh["down"]
     out["down"] = r * w // 2 + 4 * r + 4 * i + 4 * h + 4 * h          # W, scales, act, x r+w
     return out
+
+
+def measured_traffic(kind):
+    """HBM bytes per launch of one step GEMV kind from the PMC profile."""
+    try:
+        prof = json.loads(TRAFFIC_PROFILE.read_text())
+        return int(prof["kernels"][kind]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def time_graph(lib, model, state, launches, reps, torch):
@@ -240,7 +256,7 @@ def main():
                          args.gemv_reps, torch)
     state.check_status()
     alg = algorithmic_bytes(cfg)
-    dominant = max(per_kind_ms, key=lambda k: per_kind_ms[k])
+    dominant = DOMINANT
     achieved = alg[dominant] / (per_kind_ms[dominant] * 1e-3) / 1e9
     body_gbs = body_bytes(cfg) / (body_ms * 1e-3) / 1e9
     for k in kinds:
@@ -266,7 +282,9 @@ def main():
                    "global_batch": 1, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": f"gemv_kernel ({dominant})", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dominant),
+                     "algorithmic_bytes": alg[dominant],
+                     "us_per_launch": round(per_kind_ms[dominant] * 1e3, 3)},
         "body_gemv": {"bytes_per_token": body_bytes(cfg), "us_per_token": round(body_ms * 1e3, 2),
                       "achieved": round(body_gbs, 1), "unit": "GB/s",
                       "frac": round(body_gbs / HBM_PEAK_GBS, 4)},
