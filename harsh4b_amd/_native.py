@@ -31,10 +31,11 @@ class HqModel(ctypes.Structure):
         ("intermediate", ctypes.c_int32), ("heads", ctypes.c_int32),
         ("kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("vocab", ctypes.c_int32), ("rope_positions", ctypes.c_int32),
-        ("eps", ctypes.c_float), ("reserved", ctypes.c_int32),
+        ("eps", ctypes.c_float), ("flags", ctypes.c_int32),
         ("layer", ctypes.POINTER(HqLayer)),
         ("embedding", vp), ("embedding_scales", vp), ("final_norm", vp),
         ("rope_cos", vp), ("rope_sin", vp),
+        ("device_layer", vp),
     ]
 
 
@@ -49,6 +50,8 @@ class HqState(ctypes.Structure):
 
 HQ_STEP_BAD_TOKEN = 1
 HQ_STEP_FULL = 2
+HQ_STEP_SYNC = 4
+HQ_MODEL_PER_LAYER_KERNELS = 1
 
 _SIGNATURES = {
     "hq_status_string": ([c_int], ctypes.c_char_p),
@@ -64,6 +67,7 @@ _SIGNATURES = {
     "hq_gemm_workspace_bytes": ([c_int, c_int, c_int], c_size),
     "hq_int4_i8_gemm": ([vp, vp, vp, vp, vp, c_int, c_int, c_int, vp, vp, vp], c_int),
     "hq_quant_int4_gemm": ([vp, vp, vp, vp, c_int, c_int, c_int, vp, vp, vp, vp, vp], c_int),
+    "hq_step_layer_blocks": ([ctypes.POINTER(HqModel)], c_int),
     "hq_step_workspace_bytes": ([ctypes.POINTER(HqModel), c_int], c_size),
     "hq_decode_step": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), vp], c_int),
     "hq_step_gemv": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), c_int, c_int, vp], c_int),

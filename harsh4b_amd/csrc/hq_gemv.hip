@@ -23,35 +23,10 @@
 //     and a shift by 4 give the int32 accumulator (|16*acc| < 2^31 for
 //     K <= 9728*2 with |w| <= 7, |x| <= 127).
 #include "hq_device.h"
+#include "hq_int4.h"
 #include "hq_internal.h"
 
 namespace hq {
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// Weights are read exactly once per step: stream them past the caches.
-__device__ __forceinline__ uint4 load_w16(const uint8_t* p)
-{
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// 16 * sum(w * x) over one 16-byte weight chunk, accumulated into two
-// independent integer chains (integer addition is exact in any order).
-__device__ __forceinline__ void dot_chunk(uint4 w, const uint8_t* xs_chunk, int& a0, int& a1)
-{
-    const uint4 xa = *reinterpret_cast<const uint4*>(xs_chunk);
-    const uint4 xb = *reinterpret_cast<const uint4*>(xs_chunk + 16);
-    const int m = int(0xF0F0F0F0u);
-    a0 = __builtin_amdgcn_sdot4(int(w.x << 4) & m, int(xa.x), a0, false);
-    a1 = __builtin_amdgcn_sdot4(int(w.x) & m, int(xa.y), a1, false);
-    a0 = __builtin_amdgcn_sdot4(int(w.y << 4) & m, int(xa.z), a0, false);
-    a1 = __builtin_amdgcn_sdot4(int(w.y) & m, int(xa.w), a1, false);
-    a0 = __builtin_amdgcn_sdot4(int(w.z << 4) & m, int(xb.x), a0, false);
-    a1 = __builtin_amdgcn_sdot4(int(w.z) & m, int(xb.y), a1, false);
-    a0 = __builtin_amdgcn_sdot4(int(w.w << 4) & m, int(xb.z), a0, false);
-    a1 = __builtin_amdgcn_sdot4(int(w.w) & m, int(xb.w), a1, false);
-}
 
 // Activation registers: element i = tid + 256*j of x (and gamma) is held
 // by thread tid, which for PRO_RMSNORM is exactly the spec's 256-lane
@@ -131,24 +106,6 @@ __device__ __forceinline__ float activation_prologue(const GemvParams& p, ActReg
 // Row sums leave the wave through DPP and readlane: no LDS and no barrier
 // between the dot products and the epilogue.  With EPI_SWIGLU, RPW = 2 and
 // a wave's rows are gate rows followed by the matching up rows.
-template <int LPR>
-__device__ __forceinline__ int row_isum(int v, int r)
-{
-    // v: per-lane partial; returns the total of row r of the wave (uniform)
-    if constexpr (LPR == 8) {
-        v = group8_isum(v);
-        return __builtin_amdgcn_readlane(v, 8 * r);
-    } else {
-        v += dpp_i<kRowShl8>(v);
-        v = group8_isum(v);
-        if constexpr (LPR == 16) return __builtin_amdgcn_readlane(v, 16 * r);
-        if constexpr (LPR == 32)
-            return __builtin_amdgcn_readlane(v, 32 * r) + __builtin_amdgcn_readlane(v, 32 * r + 16);
-        return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
-               __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
-    }
-}
-
 template <int LPR, int EPI>
 __device__ __forceinline__ int wave_row(const GemvParams& p, int tile, int wave, int r, bool& valid)
 {

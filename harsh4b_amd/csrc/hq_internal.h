@@ -70,4 +70,19 @@ struct AttnParams {
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);
 hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s);
 
+// ---- persistent layer kernel ---------------------------------------------------
+// Shapes the kernel is compiled for (head_dim 128, <= 4 query heads per kv
+// head, hidden <= 2560, ...).
+bool engine_fits(const hq_model* m);
+// Grid size on the current device (0: the kernel cannot run there).
+int engine_blocks(const hq_model* m);
+// 64-bit hand-off entries the kernel needs in the workspace.
+size_t engine_ll_entries(const hq_model* m);
+hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, uint32_t* epoch,
+                         float* part, int32_t* counters, int max_chunks, int nb, uint32_t* trace,
+                         hipStream_t s);
+// HQ_ENGINE_TRACE builds: bytes of phase timestamps kept after the step
+// workspace proper (0 otherwise).
+size_t engine_trace_bytes(const hq_model* m);
+
 }  // namespace hq

@@ -2,8 +2,9 @@
 // library's status helpers and HIP-graph capture of whole steps.
 //
 // The launch sequence follows LiteSparkQwen.forward_token
-// (cpu_lightspark.py:424-468 in the reference repository), fused into five
-// kernels per layer:
+// (cpu_lightspark.py:424-468 in the reference repository).  The decoder
+// layers run either as one persistent kernel (hq_engine.hip) or as five
+// kernels per layer, with the same arithmetic:
 //   1. RMSNorm(input) -> int8 quant -> qkv GEMV              (:431-434)
 //   2. qk-norm -> RoPE -> fp16 KV write -> GQA attention     (:435-441)
 //   3. int8 quant -> o GEMV -> residual add                  (:442-445)
@@ -42,7 +43,8 @@ __global__ __launch_bounds__(kBlock) void embedding_kernel(
 
 struct StepLayout {
     int q_size, kv_size, groups, max_chunks, lm_blocks;
-    size_t attn_part_bytes, attn_counter_off, lm_val_off, lm_idx_off, lm_counter_off, total;
+    size_t attn_part_bytes, attn_counter_off, lm_val_off, lm_idx_off, lm_counter_off;
+    size_t epoch_off, ll_off, trace_off, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -60,7 +62,10 @@ static StepLayout step_layout(const hq_model* m, int capacity)
     L.lm_val_off = L.attn_counter_off + align256(size_t(m->kv_heads) * 4);
     L.lm_idx_off = L.lm_val_off + align256(size_t(L.lm_blocks) * 4);
     L.lm_counter_off = L.lm_idx_off + align256(size_t(L.lm_blocks) * 4);
-    L.total = L.lm_counter_off + align256(size_t(ticket_words(L.lm_blocks)) * 4);
+    L.epoch_off = L.lm_counter_off + align256(size_t(ticket_words(L.lm_blocks)) * 4);
+    L.ll_off = L.epoch_off + 256;
+    L.trace_off = L.ll_off + align256(engine_ll_entries(m) * 8);
+    L.total = L.trace_off + engine_trace_bytes(m);
     return L;
 }
 
@@ -83,6 +88,7 @@ static int validate(const hq_model* m, const hq_state* st)
         !st->qkv || !st->attended || !st->activated || !st->logits || !st->workspace)
         return HQ_ERR_ARG;
     if (!a16(m->embedding) || !a16(st->workspace)) return HQ_ERR_ALIGN;
+    if (m->device_layer && !a16(m->device_layer)) return HQ_ERR_ALIGN;
     for (int l = 0; l < m->layers; ++l) {
         const hq_layer& L = m->layer[l];
         if (!L.qkv || !L.o || !L.gate_up || !L.down || !L.qkv_scales || !L.o_scales ||
@@ -136,7 +142,16 @@ static hipError_t enqueue_step(const hq_model* m, const hq_state* st, hipStream_
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
 
-    for (int l = 0; l < m->layers; ++l) {
+    const int nb = (m->device_layer && !(m->flags & HQ_MODEL_PER_LAYER_KERNELS) && engine_fits(m))
+                       ? engine_blocks(m) : 0;
+    if (nb > 0) {
+        e = launch_engine(m, st, reinterpret_cast<uint64_t*>(ws + Ly.ll_off),
+                          reinterpret_cast<uint32_t*>(ws + Ly.epoch_off), reinterpret_cast<float*>(ws),
+                          reinterpret_cast<int32_t*>(ws + Ly.attn_counter_off), Ly.max_chunks, nb,
+                          engine_trace_bytes(m) ? reinterpret_cast<uint32_t*>(ws + Ly.trace_off) : nullptr, s);
+        if (e != hipSuccess) return e;
+    }
+    for (int l = 0; nb == 0 && l < m->layers; ++l) {
         const hq_layer& L = m->layer[l];
         if ((e = layer_gemv(m, st, l, StepGemv::Qkv, s)) != hipSuccess) return e;
 
@@ -185,12 +200,20 @@ extern "C" const char* hq_status_string(int status)
     }
 }
 
-extern "C" int hq_abi_version(void) { return 100; }
+extern "C" int hq_abi_version(void) { return 101; }
 
 extern "C" size_t hq_step_workspace_bytes(const hq_model* model, int capacity)
 {
     if (!model || capacity <= 0 || model->head_dim <= 0 || model->kv_heads <= 0) return 0;
     return step_layout(model, capacity).total;
+}
+
+extern "C" int hq_step_layer_blocks(const hq_model* model)
+{
+    if (!model || !model->device_layer || (model->flags & HQ_MODEL_PER_LAYER_KERNELS) ||
+        model->kv_heads <= 0 || model->heads <= 0 || !engine_fits(model))
+        return 0;
+    return engine_blocks(model);
 }
 
 extern "C" int hq_decode_step(const hq_model* model, const hq_state* state, void* stream)

@@ -187,6 +187,8 @@ class QwenDecodeState:
             raise ValueError("a token ID outside the vocabulary reached the device")
         if code & _native.HQ_STEP_FULL:
             raise ValueError("decode state capacity exhausted")
+        if code & _native.HQ_STEP_SYNC:
+            raise RuntimeError("a phase wait of the persistent layer kernel gave up")
 
     def close(self) -> None:
         if self._graph is not None:
@@ -249,7 +251,32 @@ class LiteSparkQwen:
         m.final_norm = final_norm.data_ptr()
         m.rope_cos = self.rope_cos.data_ptr()
         m.rope_sin = self.rope_sin.data_ptr()
+        # device copy of the layer table: lets a step run its decoder layers
+        # as one persistent kernel
+        table = bytes(self._layer_structs)
+        self._layer_table = torch.frombuffer(bytearray(table), dtype=torch.uint8).to(self.device)
+        m.device_layer = self._layer_table.data_ptr()
+        m.flags = 0
         self.struct = m
+
+    @property
+    def layer_kernel_blocks(self) -> int:
+        """Blocks of the persistent layer kernel a step launches (0: the
+        step runs five kernels per decoder layer)."""
+        return int(_native.lib().hq_step_layer_blocks(ctypes.byref(self.struct)))
+
+    @property
+    def per_layer_kernels(self) -> bool:
+        """True when steps run five kernels per decoder layer instead of the
+        persistent layer kernel (same results)."""
+        return bool(self.struct.flags & _native.HQ_MODEL_PER_LAYER_KERNELS)
+
+    @per_layer_kernels.setter
+    def per_layer_kernels(self, value: bool) -> None:
+        if value:
+            self.struct.flags |= _native.HQ_MODEL_PER_LAYER_KERNELS
+        else:
+            self.struct.flags &= ~_native.HQ_MODEL_PER_LAYER_KERNELS
 
     def new_state(self, capacity: int) -> QwenDecodeState:
         return QwenDecodeState(self, capacity)

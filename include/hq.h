@@ -131,7 +131,11 @@ int hq_quant_int4_gemm(const float* x, const uint8_t* weights, const float* scal
  * -> quant -> tied LM head GEMV -> argmax (lowest index on ties, as
  * np.argmax at cpu_lightspark.py:704-705).
  * All pointers inside the structs are device pointers except hq_model.layer,
- * a host array of `layers` entries.  The structs are plain C. */
+ * a host array of `layers` entries.  The structs are plain C.
+ * When hq_model.device_layer holds a device copy of that array (and the
+ * shapes fit its limits), the decoder layers of a step run as one persistent
+ * kernel; otherwise as five kernels per layer.  Both give the same bits.
+ * HQ_MODEL_PER_LAYER_KERNELS in hq_model.flags selects the five-kernel form. */
 typedef struct hq_layer {
     const uint8_t* qkv;      const float* qkv_scales;      /* [q+2kv, hidden/2], [q+2kv] */
     const uint8_t* o;        const float* o_scales;        /* [hidden, q/2], [hidden] */
@@ -144,14 +148,17 @@ typedef struct hq_layer {
 typedef struct hq_model {
     int32_t layers, hidden, intermediate, heads, kv_heads, head_dim, vocab, rope_positions;
     float eps;
-    int32_t reserved;
+    int32_t flags;                  /* HQ_MODEL_* bits */
     const hq_layer* layer;          /* HOST array [layers] */
     const uint8_t* embedding;       /* [vocab, hidden/2], tied LM head */
     const float* embedding_scales;  /* [vocab] */
     const float* final_norm;        /* [hidden] */
     const float* rope_cos;          /* [rope_positions, head_dim/2] */
     const float* rope_sin;
+    const hq_layer* device_layer;   /* optional DEVICE copy of layer[] */
 } hq_model;
+
+#define HQ_MODEL_PER_LAYER_KERNELS 1
 
 typedef struct hq_state {
     int32_t capacity;     /* KV positions */
@@ -160,7 +167,7 @@ typedef struct hq_state {
     uint16_t* values;
     int32_t* position;    /* [1] next position; advanced by each step */
     int32_t* token;       /* [1] input token; replaced by the greedy token */
-    int32_t* status;      /* [1] 0, or HQ_STEP_BAD_TOKEN / HQ_STEP_FULL (sticky) */
+    int32_t* status;      /* [1] 0, or HQ_STEP_* bits (sticky) */
     float* x;             /* [hidden] residual stream */
     float* qkv;           /* [q+2kv] raw fused projection */
     float* attended;      /* [q] */
@@ -171,8 +178,13 @@ typedef struct hq_state {
 
 #define HQ_STEP_BAD_TOKEN 1
 #define HQ_STEP_FULL 2
+#define HQ_STEP_SYNC 4   /* a phase wait of the persistent layer kernel gave up */
 
 size_t hq_step_workspace_bytes(const hq_model* model, int capacity);
+/* Blocks of the persistent layer kernel a step of this model launches on the
+ * current device (one per CU at most), or 0 when the step runs five kernels
+ * per layer.  No reference counterpart (introspection). */
+int hq_step_layer_blocks(const hq_model* model);
 /* Enqueue one step.  Reads *state->token and *state->position on the device,
  * so the same launch sequence serves every position (graph-capturable). */
 int hq_decode_step(const hq_model* model, const hq_state* state, void* stream);

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 def test_status_strings_and_version():
     from harsh4b_amd import _native
     lib = _native.lib()
-    assert lib.hq_abi_version() == 100
+    assert lib.hq_abi_version() == 101
     assert lib.hq_status_string(0) == b"ok"
     assert b"invalid" in lib.hq_status_string(1)
 

@@ -172,3 +172,97 @@ def test_qwen3_4b_long_context_bit_exact(qwen, ctx):
         token = tok
     assert_bits_equal(to_host(st.keys).view(np.uint16)[:, ctx:ctx + 2], rs.keys[:, ctx:ctx + 2], "new keys")
     st.check_status()
+
+
+# ------------------------------------------- persistent layer kernel vs per-layer
+def _run_tokens(model, st, tokens):
+    out = []
+    for t in tokens:
+        out.append(to_host(model.forward_token(int(t), st)).copy())
+    return out
+
+
+def test_tiny_model_layer_kernel_matches_per_layer_kernels(forward_golden):
+    g = forward_golden
+    model = golden_model(g)
+    assert model.layer_kernel_blocks > 0, "the tiny model fits the persistent layer kernel"
+    cap = len(g["tokens"])
+    a = model.new_state(cap)
+    la = _run_tokens(model, a, g["tokens"])
+    model.per_layer_kernels = True
+    assert model.layer_kernel_blocks == 0
+    b = model.new_state(cap)
+    lb = _run_tokens(model, b, g["tokens"])
+    model.per_layer_kernels = False
+    for i, (x, y) in enumerate(zip(la, lb)):
+        assert_bits_equal(x, y, f"logits step {i}")
+    assert_bits_equal(to_host(a.keys).view(np.uint16), to_host(b.keys).view(np.uint16), "keys")
+    assert_bits_equal(to_host(a.x), to_host(b.x), "residual")
+    a.check_status()
+    b.check_status()
+
+
+@pytest.mark.parametrize("ctx", [0, 300])
+def test_qwen3_4b_layer_kernel_matches_per_layer_kernels(qwen, ctx):
+    model, _ = qwen
+    assert model.layer_kernel_blocks > 0, "Qwen3-4B fits the persistent layer kernel"
+    cap = ctx + 4
+    states = []
+    rng = np.random.default_rng(ctx + 7)
+    cache = {}
+    for name in ("keys", "values"):
+        cache[name] = rng.standard_normal((36, ctx, 8, 128)).astype(np.float16)
+    results = []
+    for per_layer in (False, True):
+        model.per_layer_kernels = per_layer
+        st = model.new_state(cap)
+        if ctx:
+            for name in ("keys", "values"):
+                getattr(st, name)[:, :ctx] = to_dev(cache[name])
+            st.device_position.fill_(ctx)
+            st.position = ctx
+            torch.cuda.synchronize()
+        toks, logits = [], []
+        token = 4242
+        for _ in range(3):
+            logits.append(to_host(model.forward_token(token, st)).copy())
+            token = model.greedy_token(st)
+            toks.append(token)
+        st.check_status()
+        results.append((toks, logits, to_host(st.keys).view(np.uint16)[:, ctx:ctx + 3].copy()))
+        states.append(st)
+    model.per_layer_kernels = False
+    (ta, la, ka), (tb, lb, kb) = results
+    assert ta == tb
+    for i in range(3):
+        assert_bits_equal(la[i], lb[i], f"ctx {ctx} logits step {i}")
+    assert_bits_equal(ka, kb, f"ctx {ctx} new keys")
+
+
+def test_layer_kernel_graph_replays_continue_epochs(forward_golden):
+    # the hand-off epochs live in the workspace: many replays of one captured
+    # step stay in step with eager steps of the per-layer path
+    g = forward_golden
+    model = golden_model(g)
+    first = int(g["tokens"][0])
+    a = model.new_state(40)
+    with torch.cuda.stream(a.stream):
+        a.token.fill_(first)
+    toks_a = []
+    for _ in range(30):
+        model.decode_greedy(a, 1)
+        toks_a.append(model.greedy_token(a))
+    model.per_layer_kernels = True
+    b = model.new_state(40)
+    toks_b = []
+    model.forward_token(first, b)
+    for _ in range(29):
+        t = model.greedy_token(b)
+        toks_b.append(t)
+        model.forward_token(t, b)
+    toks_b.append(model.greedy_token(b))
+    model.per_layer_kernels = False
+    assert toks_a == toks_b
+    assert_bits_equal(to_host(a.logits), to_host(b.logits), "logits after 30 steps")
+    a.check_status()
+    b.check_status()
