@@ -105,7 +105,8 @@ struct EngineParams {
 // the 100 MHz wall clock at fixed points of layers kTraceL0 .. kTraceL0+3,
 // from lane 0 of every wave, kept in LDS (a global store would join the
 // wave's vector-memory queue and shift the waits being measured) and copied
-// at the end to trace[((block*4 + layer-kTraceL0)*16 + point)*16 + wave].
+// at the end to trace[((block*4 + layer-kTraceL0)*16 + point)*16 + wave]; the
+// attention's own points follow for blocks gridDim.x + block.
 #ifdef HQ_ENGINE_TRACE
 constexpr int kTraceL0 = 16;
 #define ENG_MARK(point)                                                                          \
@@ -269,6 +270,17 @@ __device__ __forceinline__ float block_max16(float v, float* bmax)
     return r;
 }
 
+// Norm weights of this input thread's elements t + 256*j, loaded into
+// registers a phase before the RMSNorm that uses them (a load just before
+// the poll would delay the poll: a wave's loads complete in order).
+template <int NPT>
+__device__ __forceinline__ void load_gamma(const float* g, int n, float (&out)[NPT])
+{
+    const int t = opaque_tid();
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) out[j] = t + 256 * j < n ? gmem(g)[t + 256 * j] : 0.0f;
+}
+
 // Activation prologues.  The phase input is held in registers, element
 // t + T*j in out[j] of thread t < T; the int8 result goes to xq in the
 // de-interleaved layout, followed by zeros up to npad (the GEMV layouts read
@@ -277,7 +289,7 @@ __device__ __forceinline__ float block_max16(float v, float* bmax)
 
 // RMSNorm (the spec's 256 strided fmaf partials: T = 256) then quantization.
 template <int NPT>
-__device__ __forceinline__ float rmsnorm_quant(float (&x)[NPT], int n, const float* gam, float eps,
+__device__ __forceinline__ float rmsnorm_quant(float (&x)[NPT], int n, const float (&gam)[NPT], float eps,
                                                uint8_t* xq, int npad, float* red, float* bmax)
 {
     const int t = opaque_tid();
@@ -296,7 +308,7 @@ __device__ __forceinline__ float rmsnorm_quant(float (&x)[NPT], int n, const flo
 #pragma unroll
         for (int j = 0; j < NPT; ++j)
             if (t + 256 * j < n) {
-                x[j] = (x[j] / r) * gam[t + 256 * j];
+                x[j] = (x[j] / r) * gam[j];
                 amax = fmaxf(amax, fabsf(x[j]));
             }
     }
@@ -474,9 +486,10 @@ struct AttnLds {
     uint16_t k[kAttnChunk * kRow];
     uint16_t v[kAttnChunk * kRow];
     uint16_t kc[kD], vc[kD];
-    float e[kG][kAttnChunk];
+    alignas(16) float e[kG][kAttnChunk];
     float m[kG][kCPB], l[kG][kCPB];
-    float o[kCPB][kG][kD];
+    float alpha[kG][kCPB], inv_l[kG];
+    alignas(16) float o[kCPB][kG][kD];
 };
 
 // K/V of chunk rows [t0, t0 + tn) into registers: 64 rows x 16 groups of
@@ -500,11 +513,22 @@ __device__ __forceinline__ void load_kv_chunk(const uint16_t* keys, const uint16
 // STEP mode (hq_attention.hip).
 __device__ void attention_item(const EngineParams& p, const float* q_norm, const float* k_norm, int l, int item, int nsplit,
                                int n, int nc, int pos, uint32_t epoch_qkv, uint32_t epoch_att,
-                               AttnLds& A, int& last, unsigned& budget)
+                               AttnLds& A, int& last, unsigned& budget, uint32_t* atr)
 {
+#ifdef HQ_ENGINE_TRACE
+#define ATT_MARK(k)                                                                                 \
+    do {                                                                                            \
+        const int t_ = opaque_tid();                                                                \
+        if ((t_ & (kWave - 1)) == 0 && l >= kTraceL0 && l < kTraceL0 + 4)                           \
+            atr[((l - kTraceL0) * 16 + (k)) * 16 + t_ / kWave] = uint32_t(wall_clock64());          \
+    } while (0)
+#else
+#define ATT_MARK(k) do { (void)atr; } while (0)
+#endif
     // A aliases the weight waves' stage buffer: wait until every wave is
     // done with its staged qkv weights
     block_sync();
+    ATT_MARK(0);
     const int tid = opaque_tid();
     const int wave = tid / kWave;
     const int lane = tid & (kWave - 1);
@@ -573,6 +597,7 @@ __device__ void attention_item(const EngineParams& p, const float* q_norm, const
     }
     block_sync();
 
+    ATT_MARK(2);
     // per-head RMSNorm + RoPE of q; k (norm + RoPE) and v appended as fp16
     if (wave < G) {
         const float x0 = A.raw[wave * kD + lane], x1 = A.raw[wave * kD + lane + 64];
@@ -608,6 +633,7 @@ __device__ void attention_item(const EngineParams& p, const float* q_norm, const
         else vals[size_t(pos) * size_t(p.kv_stride) + kv_off + (tid - kD)] = A.vc[tid - kD];
     }
 
+    ATT_MARK(3);
     const int grp = tid >> 4;        // position of the chunk this lane group scores
     const int l16 = tid & 15;
     const float scale = 1.0f / __builtin_sqrtf(float(kD));
@@ -634,6 +660,7 @@ __device__ void attention_item(const EngineParams& p, const float* q_norm, const
             }
         }
         block_sync();
+        if (ci == 0) ATT_MARK(4);
         if (c + 1 < c_end) {
             const int t1 = t0 + C;
             load_kv_chunk(keys, vals, p.kv_stride, kv_off, t1, min(C, n - t1),
@@ -668,6 +695,7 @@ __device__ void attention_item(const EngineParams& p, const float* q_norm, const
                 if (h < G) A.e[h][grp] = -__builtin_inff();
         }
         block_sync();
+        if (ci == 0) ATT_MARK(5);
 
         if (wave < G) {
             const float sc = A.e[wave][lane];
@@ -678,45 +706,77 @@ __device__ void attention_item(const EngineParams& p, const float* q_norm, const
             if (lane == 0) { A.m[wave][ci] = m; A.l[wave][ci] = ls; }
         }
         block_sync();
+        if (ci == 0) ATT_MARK(6);
 
         if (vh < G) {
+            // o = fmaf chain over ascending positions; a full chunk reads 16
+            // positions ahead of their fmas, so the chain waits on LDS once
+            // per 16 positions instead of once per 8
             float o = 0.0f;
-            int i = 0;
-#pragma unroll 1
-            for (; i + 8 <= tn; i += 8) {
-                float vv[8], ee[8];
+            if (tn == C) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    vv[j] = f16_to_f32(A.v[(i + j) * kRow + vd]);
-                    ee[j] = A.e[vh][i + j];
+                for (int i0 = 0; i0 < C; i0 += 16) {
+                    float vv[16], ee[16];
+#pragma unroll
+                    for (int j = 0; j < 16; j += 4) {
+                        const float4 e4 = *reinterpret_cast<const float4*>(&A.e[vh][i0 + j]);
+                        ee[j] = e4.x; ee[j + 1] = e4.y; ee[j + 2] = e4.z; ee[j + 3] = e4.w;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) vv[j] = f16_to_f32(A.v[(i0 + j) * kRow + vd]);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) o = __builtin_fmaf(ee[j], vv[j], o);
                 }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o = __builtin_fmaf(ee[j], vv[j], o);
-            }
+            } else {
+                int i = 0;
 #pragma unroll 1
-            for (; i < tn; ++i) o = __builtin_fmaf(A.e[vh][i], f16_to_f32(A.v[i * kRow + vd]), o);
+                for (; i + 8 <= tn; i += 8) {
+                    float vv[8], ee[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        vv[j] = f16_to_f32(A.v[(i + j) * kRow + vd]);
+                        ee[j] = A.e[vh][i + j];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o = __builtin_fmaf(ee[j], vv[j], o);
+                }
+#pragma unroll 1
+                for (; i < tn; ++i) o = __builtin_fmaf(A.e[vh][i], f16_to_f32(A.v[i * kRow + vd]), o);
+            }
             A.o[ci][vh][vd] = o;
         }
         block_sync();
+        if (ci == 0) ATT_MARK(7);
     }
+    ATT_MARK(8);
 
     const int nmine = c_end - c_begin;
     if (nsplit == 1) {
+        // the combine weights a_c = exp(m_c - M) and 1/L depend on the head
+        // only: one lane per head computes them (same operations, same bits)
+        if (tid < G) {
+            float M = -__builtin_inff();
+            for (int ci = 0; ci < nmine; ++ci) M = fmaxf(M, A.m[tid][ci]);
+            float L = 0.0f;
+            for (int ci = 0; ci < nmine; ++ci) {
+                const float al = spec_expf(A.m[tid][ci] - M);
+                A.alpha[tid][ci] = al;
+                L = __builtin_fmaf(al, A.l[tid][ci], L);
+            }
+            A.inv_l[tid] = 1.0f / L;
+        }
+        block_sync();
+        ATT_MARK(9);
         if (tid < kIThreads) {
             for (int pr = tid; pr < G * kD; pr += kIThreads) {
                 const int h = pr >> 7, d = pr & (kD - 1);
-                float M = -__builtin_inff();
-                for (int ci = 0; ci < nmine; ++ci) M = fmaxf(M, A.m[h][ci]);
-                float L = 0.0f, O = 0.0f;
-                for (int ci = 0; ci < nmine; ++ci) {
-                    const float al = spec_expf(A.m[h][ci] - M);
-                    L = __builtin_fmaf(al, A.l[h][ci], L);
-                    O = __builtin_fmaf(al, A.o[ci][h][d], O);
-                }
-                ll_store(p.ll_att + size_t(kvh * G + h) * kD + d, O * (1.0f / L), epoch_att);
+                float O = 0.0f;
+                for (int ci = 0; ci < nmine; ++ci) O = __builtin_fmaf(A.alpha[h][ci], A.o[ci][h][d], O);
+                ll_store(p.ll_att + size_t(kvh * G + h) * kD + d, O * A.inv_l[h], epoch_att);
             }
         }
         block_sync();
+        ATT_MARK(10);
         return;
     }
 
@@ -768,7 +828,6 @@ __device__ void attention_item(const EngineParams& p, const float* q_norm, const
 
 __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
 {
-    __shared__ float gam_s[kMaxHidden];
     __shared__ __align__(16) uint8_t xq_s[kMaxVec];
     __shared__ float red[260];
     __shared__ float bmax[kWaves];
@@ -787,6 +846,10 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     __shared__ hq_layer lay_s[kMaxLayers];
 #ifdef HQ_ENGINE_TRACE
     __shared__ uint32_t trace_s[4 * 16 * 16];
+    __shared__ uint32_t atr_s[4 * 16 * 16];
+    for (int i = threadIdx.x; i < 4 * 16 * 16; i += kThreads) atr_s[i] = 0;
+#else
+    uint32_t* const atr_s = nullptr;
 #endif
 
     const int tid = threadIdx.x;
@@ -828,6 +891,8 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     //   gate_up  slots 0-4   end of P2,  slots 5-9 at the end of P3
     //   down     slots 0-4   end of P4
     stage_rows<kQkvLPR, kQkvMAXC>(stage_s, !iw, lay_s[0].qkv, q0, q1, H, ww);
+    float gin[kHidNPT] = {};   // input_norm of the coming P1 (input waves)
+    if (iw) load_gamma(lay_s[0].input_norm, H, gin);
 
 #pragma unroll 1
     for (int l = 0; l < p.L; ++l) {
@@ -845,7 +910,6 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         // stays live into the next phase on any path
         float xin[kHidNPT] = {};
         if (iw) {
-            for (int i = tid; i < H; i += kIThreads) gam_s[i] = gmem(Ly.input_norm)[i];
             if (l == 0) {
 #pragma unroll
                 for (int j = 0; j < kHidNPT; ++j)
@@ -857,7 +921,7 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         ENG_MARK(1);
         block_sync();
         ENG_MARK(2);
-        float act = rmsnorm_quant(xin, H, gam_s, p.eps, xq_s, kQkvLPR * kQkvMAXC * 32, red, bmax);
+        float act = rmsnorm_quant(xin, H, gin, p.eps, xq_s, kQkvLPR * kQkvMAXC * 32, red, bmax);
         ENG_MARK(3);
         if (!iw && q0 + ww * 2 < q1) {
             const float sq = row_scale<kQkvLPR>(Ly.qkv_scales, q0, q1, ww);
@@ -874,7 +938,7 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         // ---- P2: attention --------------------------------------------------
         for (int it = b; it < items; it += NB)
             attention_item(p, uniform_ptr(Ly.q_norm), uniform_ptr(Ly.k_norm), l, it, nsplit, n, nc, pos,
-                           E + 1, E + 2, A, last_s, budget);
+                           E + 1, E + 2, A, last_s, budget, atr_s);
         // everything the attention loaded has been consumed; saying so keeps
         // the compiler's waits for those loads from landing after the weight
         // prefetch below, where they would wait for it too
@@ -885,7 +949,11 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
 
         // ---- P3: quant -> o -> residual ----------------------------------------
         float att[kAttNPT] = {};
-        if (iw) poll_into<kIThreads, kAttNPT>(p.ll_att, qd, E + 2, att, budget, p.status);
+        float gpost[kHidNPT] = {};   // post_norm for P4, loaded once the poll is done
+        if (iw) {
+            poll_into<kIThreads, kAttNPT>(p.ll_att, qd, E + 2, att, budget, p.status);
+            load_gamma(Ly.post_norm, H, gpost);
+        }
         ENG_MARK(6);
         block_sync();
         ENG_MARK(7);
@@ -908,14 +976,11 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
 
         // ---- P4: RMSNorm(post) -> quant -> gate_up -> SwiGLU -----------------------
         float xpost[kHidNPT] = {};
-        if (iw) {
-            for (int i = tid; i < H; i += kIThreads) gam_s[i] = gmem(Ly.post_norm)[i];
-            poll_into<kIThreads, kHidNPT>(p.ll_x3, H, E + 3, xpost, budget, p.status);
-        }
+        if (iw) poll_into<kIThreads, kHidNPT>(p.ll_x3, H, E + 3, xpost, budget, p.status);
         ENG_MARK(9);
         block_sync();
         ENG_MARK(10);
-        act = rmsnorm_quant(xpost, H, gam_s, p.eps, xq_s, kGuLPR * 2 * kGuHalf * 32, red, bmax);
+        act = rmsnorm_quant(xpost, H, gpost, p.eps, xq_s, kGuLPR * 2 * kGuHalf * 32, red, bmax);
         if (!iw && g0 + ww * 4 < g1) {
             const int er = min(g0 + ww * 4 + min(lane_id(), 3), g1 - 1);
             const float sg = gmem(Ly.gate_up_scales)[er];
@@ -942,6 +1007,7 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         // lands well within the hand-off time
         float av[kActNPT] = {};
         poll_into<kThreads, kActNPT>(p.ll_act, I, E + 4, av, budget, p.status);
+        if (iw && !final_layer) load_gamma(lay_s[l + 1].input_norm, H, gin);
         ENG_MARK(12);
         block_sync();
         ENG_MARK(13);
@@ -969,7 +1035,10 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     }
 #ifdef HQ_ENGINE_TRACE
     block_sync();
-    for (int i = tid; i < 4 * 16 * 16; i += kThreads) p.trace[size_t(b) * 4 * 16 * 16 + i] = trace_s[i];
+    for (int i = tid; i < 4 * 16 * 16; i += kThreads) {
+        p.trace[size_t(b) * 4 * 16 * 16 + i] = trace_s[i];
+        p.trace[size_t(gridDim.x + b) * 4 * 16 * 16 + i] = atr_s[i];
+    }
 #endif
     if (b == 0 && tid == 0) *p.epoch = base + 5u * uint32_t(p.L);
 }
@@ -1021,7 +1090,7 @@ int engine_blocks(const hq_model* m)
 size_t engine_trace_bytes(const hq_model* m)
 {
 #ifdef HQ_ENGINE_TRACE
-    return size_t(256) * 4 * 16 * 16 * sizeof(uint32_t);
+    return size_t(2 * 256) * 4 * 16 * 16 * sizeof(uint32_t);
 #else
     (void)m;
     return 0;
