@@ -115,8 +115,16 @@ constexpr int kTraceL0 = 16;
         if ((t_ & (kWave - 1)) == 0 && l >= kTraceL0 && l < kTraceL0 + 4)                        \
             trace_s[((l - kTraceL0) * 16 + (point)) * 16 + t_ / kWave] = uint32_t(wall_clock64()); \
     } while (0)
+// sub-phase points: mk points at the 16x16 block of the layer (or nullptr)
+#define SUB_MARK(mk, point)                                                                      \
+    do {                                                                                         \
+        const int t_ = opaque_tid();                                                             \
+        if ((mk) != nullptr && (t_ & (kWave - 1)) == 0)                                          \
+            (mk)[(point) * 16 + t_ / kWave] = uint32_t(wall_clock64());                          \
+    } while (0)
 #else
 #define ENG_MARK(point) do { } while (0)
+#define SUB_MARK(mk, point) do { (void)(mk); } while (0)
 #endif
 
 namespace {
@@ -139,16 +147,6 @@ __device__ __forceinline__ bool ll_ready(uint64_t v, uint32_t epoch)
 
 __device__ __forceinline__ int split_begin(int n, int b, int nb);
 
-// The input waves publish a phase's outputs res[0, n) to dst[0, n).  Weight
-// waves issue no global stores: on gfx9 a store's data registers are read
-// after issue, and the compiler's wait before reusing them would, behind the
-// weight wave's untracked prefetch loads (dma16), wait for those as well.
-__device__ __forceinline__ void publish_rows(const float* res, uint64_t* dst, int n, uint32_t epoch)
-{
-    const int t = threadIdx.x;
-    if (t < kIThreads)
-        for (int i = t; i < n; i += kIThreads) ll_store(dst + i, res[i], epoch);
-}
 
 __device__ __forceinline__ int split_begin(int n, int b, int nb)
 {
@@ -166,6 +164,17 @@ __device__ __forceinline__ int opaque_tid()
 }
 
 __device__ __forceinline__ int lane_id() { return opaque_tid() & (kWave - 1); }
+
+// The input waves publish a phase's outputs res[0, n) to dst[0, n).  Weight
+// waves issue no global stores: on gfx9 a store's data registers are read
+// after issue, and the compiler's wait before reusing them would, behind the
+// weight wave's untracked prefetch loads (dma16), wait for those as well.
+__device__ __forceinline__ void publish_rows(const float* res, uint64_t* dst, int n, uint32_t epoch)
+{
+    const int t = opaque_tid();
+    if (t < kIThreads)
+        for (int i = t; i < n; i += kIThreads) ll_store(dst + i, res[i], epoch);
+}
 
 // Block barrier for this kernel: the wave's LDS operations complete, then
 // s_barrier.  __syncthreads() also carries a workgroup release fence, which
@@ -198,6 +207,30 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p)
     return reinterpret_cast<const T*>((uint64_t(hi) << 32) | lo);
 }
 
+
+// Wave 0 of the block waits until 64 entries spread evenly over src[0, n)
+// are current (lane i watches entry (i+1)*n/64 - 1); the block then reads
+// the whole vector in one burst (poll_into) after a barrier.  Spinning with
+// one wave instead of the readers of all n entries keeps the fabric quiet
+// while the producers' stores travel: a single watching wave on spread
+// entries made a 2560-entry hand-off between 256 blocks 1.0 us shorter than
+// every reader spinning on its own entries.
+__device__ __forceinline__ void watch_spread(const uint64_t* src, int n, uint32_t epoch, unsigned& budget,
+                                             int32_t* status)
+{
+    const int t = opaque_tid();
+    if (t < kWave) {
+        const int e = ((t + 1) * n) / kWave - 1;
+        if (e >= 0) {
+            uint64_t w = ll_load(src + e);
+            while (!ll_ready(w, epoch) && budget != 0) {
+                __builtin_amdgcn_s_sleep(1);
+                if (--budget == 0) atomicOr(status, HQ_STEP_SYNC);
+                w = ll_load(src + e);
+            }
+        }
+    }
+}
 
 // Polls entries t, t+T, ... of src[0, n) (threads t < T) until their epoch
 // is current and returns their values in out[] (0 past n).
@@ -286,40 +319,49 @@ __device__ __forceinline__ void load_gamma(const float* g, int n, float (&out)[N
 // de-interleaved layout, followed by zeros up to npad (the GEMV layouts read
 // whole chunk spans: a zero activation makes a padded chunk contribute 0).
 // Both end with a barrier; every thread gets the act scale.
+// Inputs and norm weights are 0 past n (poll_into, load_gamma), so the
+// element loops run unguarded: a zero element adds fmaf(0, 0, ss) = ss to
+// the sum of squares, leaves the max unchanged and quantizes to the 0 that
+// its xq byte must hold (T*NPT <= kMaxVec keeps those stores inside xq).
+// Straight-line code lets the compiler interleave the elements' division
+// and rounding chains instead of branching around each one.
 
 // RMSNorm (the spec's 256 strided fmaf partials: T = 256) then quantization.
 template <int NPT>
 __device__ __forceinline__ float rmsnorm_quant(float (&x)[NPT], int n, const float (&gam)[NPT], float eps,
-                                               uint8_t* xq, int npad, float* red, float* bmax)
+                                               uint8_t* xq, int npad, float* red, float* bmax,
+                                               uint32_t* mk = nullptr)
 {
     const int t = opaque_tid();
     const bool mine = t < 256;
     asm volatile("" : "+s"(n));   // keep float(n) from being hoisted out of the layer loop
+    static_assert(256 * NPT <= kMaxVec, "xq stores past the buffer");
     float ss = 0.0f;
     if (mine) {
 #pragma unroll
-        for (int j = 0; j < NPT; ++j)
-            if (t + 256 * j < n) ss = __builtin_fmaf(x[j], x[j], ss);
+        for (int j = 0; j < NPT; ++j) ss = __builtin_fmaf(x[j], x[j], ss);
     }
+    SUB_MARK(mk, 0);
     const float total = tree_sum256(ss, red);
+    SUB_MARK(mk, 1);
     const float r = __builtin_sqrtf(total / float(n) + eps);
     float amax = 0.0f;
     if (mine) {
 #pragma unroll
-        for (int j = 0; j < NPT; ++j)
-            if (t + 256 * j < n) {
-                x[j] = (x[j] / r) * gam[j];
-                amax = fmaxf(amax, fabsf(x[j]));
-            }
+        for (int j = 0; j < NPT; ++j) x[j] = (x[j] / r) * gam[j];
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) amax = fmaxf(amax, fabsf(x[j]));
     }
+    SUB_MARK(mk, 2);
     amax = fmaxf(block_max16(amax, bmax), 1e-5f);
+    SUB_MARK(mk, 3);
     const float inv = 127.0f / amax;
     if (mine) {
 #pragma unroll
-        for (int j = 0; j < NPT; ++j)
-            if (t + 256 * j < n) xq[xq_offset(t + 256 * j)] = uint8_t(quant_i8(x[j], inv));
+        for (int j = 0; j < NPT; ++j) xq[xq_offset(t + 256 * j)] = uint8_t(quant_i8(x[j], inv));
     }
     for (int i = n + t; i < npad; i += kThreads) xq[i] = 0;
+    SUB_MARK(mk, 4);
     block_sync();
     return amax / 127.0f;
 }
@@ -329,20 +371,19 @@ template <int T, int NPT>
 __device__ __forceinline__ float quantize(const float (&x)[NPT], int n, uint8_t* xq, int npad,
                                           float* bmax)
 {
+    static_assert(T * NPT <= kMaxVec, "xq stores past the buffer");
     const int t = opaque_tid();
     const bool mine = t < T;
     float amax = 0.0f;
     if (mine) {
 #pragma unroll
-        for (int j = 0; j < NPT; ++j)
-            if (t + T * j < n) amax = fmaxf(amax, fabsf(x[j]));
+        for (int j = 0; j < NPT; ++j) amax = fmaxf(amax, fabsf(x[j]));
     }
     amax = fmaxf(block_max16(amax, bmax), 1e-5f);
     const float inv = 127.0f / amax;
     if (mine) {
 #pragma unroll
-        for (int j = 0; j < NPT; ++j)
-            if (t + T * j < n) xq[xq_offset(t + T * j)] = uint8_t(quant_i8(x[j], inv));
+        for (int j = 0; j < NPT; ++j) xq[xq_offset(t + T * j)] = uint8_t(quant_i8(x[j], inv));
     }
     for (int i = n + t; i < npad; i += kThreads) xq[i] = 0;
     block_sync();
@@ -406,14 +447,53 @@ __device__ __forceinline__ void stage_rows(uint8_t* stage, bool active, const ui
         dma16(W, rowoff + uint32_t(min(li + j * LPR, nch - 1)) * 16, sub + (SLOT0 + j) * 1024);
 }
 
-// Scale of the wave's row `lane` (lanes < RPW), read right before the dot
-// waits for its staged weights, so the load overlaps that wait and the value
-// lives only through the epilogue.
+// Waits until at most N of the wave's memory operations are outstanding
+// (they complete in issue order): a dot waits for its own weights but not
+// for the prefetch issued after them.  Only weight waves use it, and they
+// issue no other memory operations after the prefetch they skip.
+template <int N>
+__device__ __forceinline__ void wait_memory_but()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One 4-byte global->LDS load per lane from S + off into lds + 4*lane.
+__device__ __forceinline__ void dma4(const float* S, uint32_t off, float* lds)
+{
+    const uint32_t m = __builtin_amdgcn_readfirstlane(
+        uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float*)lds)));
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dword %2, %3\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(m), "v"(off), "s"(uniform_ptr(S))
+                 : "memory");
+}
+
+// Row scales travel with their weights: lane i of weight wave ww copies the
+// scale of the wave's row min(i, RPW-1) into scl[ww][i] (read after the
+// dot's wait for the wave's global->LDS loads).
 template <int LPR>
-__device__ __forceinline__ float row_scale(const float* S, int r0, int r1, int ww)
+__device__ __forceinline__ void stage_scales(float (*scl)[kWave], bool active, const float* S, int r0, int r1,
+                                             int ww)
 {
     constexpr int RPW = kWave / LPR;
-    return gmem(S)[min(r0 + ww * RPW + min(lane_id(), RPW - 1), r1 - 1)];
+    if (!active || r0 + ww * RPW >= r1) return;
+    const int row = min(r0 + ww * RPW + min(lane_id(), RPW - 1), r1 - 1);
+    dma4(S, uint32_t(row) * 4u, scl[__builtin_amdgcn_readfirstlane(ww)]);
+}
+
+// SwiGLU scales: lanes 0-3 the gate rows of the wave's four pairs, lanes 4-7
+// the matching up rows (I + pair); the others repeat them.
+__device__ __forceinline__ void stage_pair_scales(float (*scl)[kWave], bool active, const float* S, int p0,
+                                                  int p1, int I, int ww)
+{
+    if (!active || p0 + ww * 4 >= p1) return;
+    const int lane = lane_id();
+    const int pair = min(p0 + ww * 4 + (lane & 3), p1 - 1);
+    const int row = (lane & 4) ? I + pair : pair;
+    dma4(S, uint32_t(row) * 4u, scl[__builtin_amdgcn_readfirstlane(ww)]);
 }
 
 // LDS prefetch of SwiGLU rows: pairs [p0, p1) of the I gate rows; weight
@@ -460,6 +540,42 @@ __device__ __forceinline__ int staged_dot(const uint8_t* stage, const uint8_t* x
         __builtin_amdgcn_sched_barrier(0);
     }
     return (a0 + a1) + (a2 + a3);
+}
+
+// Register prefetch of SwiGLU chunks J0 .. J0+NR-1 (same lane mapping as
+// stage_pairs).  Ordinary loads: the compiler waits for them at their use.
+template <int NR, int J0>
+__device__ __forceinline__ void load_pairs(uint4 (&w)[NR], bool active, const uint8_t* W, int p0, int p1, int I,
+                                           int K, int ww)
+{
+    if (!active || p0 + ww * 4 >= p1) return;
+    const int lane = lane_id();
+    const int nch = K >> 5;
+    const int rsel = lane >> 3;
+    const int pair = min(p0 + ww * 4 + (rsel & 3), p1 - 1);
+    const int row = rsel < 4 ? pair : I + pair;
+    const int li = lane & 7;
+    const uint8_t* base = W + size_t(row) * size_t(K >> 1);
+#pragma unroll
+    for (int j = 0; j < NR; ++j) w[j] = load_w16(base + size_t(min(li + (J0 + j) * 8, nch - 1)) * 16);
+}
+
+// staged_dot over NS staged chunks (slots 0..NS-1) followed by NR chunks
+// held in registers (chunk indices NS..NS+NR-1).
+template <int LPR, int NS, int NR>
+__device__ __forceinline__ int staged_reg_dot(const uint8_t* stage, const uint4 (&w)[NR], const uint8_t* xq,
+                                              int ww)
+{
+    const int lane = lane_id();
+    const int li = lane % LPR;
+    int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+#pragma unroll
+    for (int j = 0; j < NR; j += 2) {
+        dot_chunk(w[j], xq + (li + (NS + j) * LPR) * 32, a2, a3);
+        if (j + 1 < NR) dot_chunk(w[j + 1], xq + (li + (NS + j + 1) * LPR) * 32, a0, a1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return staged_dot<LPR, NS>(stage, xq, ww) + ((a0 + a1) + (a2 + a3));
 }
 
 // Lane r < COUNT receives the accumulator of the wave's row FIRST + r
@@ -561,18 +677,32 @@ __device__ void attention_item(const EngineParams& p, const float* q_norm, const
             if (i < kD / 2) A.cs[i] = p.rope_cos[size_t(pos) * (kD / 2) + i];
             else A.sn[i - kD / 2] = p.rope_sin[size_t(pos) * (kD / 2) + (i - kD / 2)];
         }
-        // q rows of the G heads, then k and v of this kv head
-        const int nq = G * kD;
-        const int ne = nq + 2 * kD;
-        const int qd = p.heads * kD;
+    }
+    // q rows of the G heads, then k and v of this kv head: entry e of the
+    // item's ne inputs sits at ll_qkv[qkv_src(e)]
+    const int nq = G * kD;
+    const int ne = nq + 2 * kD;
+    const int qd = p.heads * kD;
+    auto qkv_src = [&](int e) {
+        return e < nq ? kvh * nq + e
+                      : (e < nq + kD ? qd + kvh * kD + (e - nq) : qd + p.kv_heads * kD + kvh * kD + (e - nq - kD));
+    };
+    if (tid < kWave) {   // wave 0 watches 64 spread entries (see watch_spread)
+        const int src = qkv_src(((tid + 1) * ne) / kWave - 1);
+        uint64_t w = ll_load(p.ll_qkv + src);
+        while (!ll_ready(w, epoch_qkv) && budget != 0) {
+            __builtin_amdgcn_s_sleep(1);
+            if (--budget == 0) atomicOr(p.status, HQ_STEP_SYNC);
+            w = ll_load(p.ll_qkv + src);
+        }
+    }
+    block_sync();
+    if (tid < kIThreads) {
         uint64_t v[3];
         int src[3];
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-            const int e = min(tid + kIThreads * j, ne - 1);
-            src[j] = e < nq ? kvh * nq + e
-                            : (e < nq + kD ? qd + kvh * kD + (e - nq)
-                                           : qd + p.kv_heads * kD + kvh * kD + (e - nq - kD));
+            src[j] = qkv_src(min(tid + kIThreads * j, ne - 1));
             v[j] = ll_load(p.ll_qkv + src[j]);
         }
         int spin = -1;   // as in poll_into: spin on one entry, then refresh the rest
@@ -837,6 +967,8 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     // weight stage (kWaveStage bytes per weight wave); the attention work
     // area of P2 aliases it
     __shared__ __align__(16) uint8_t stage_s[kWWaves * kWaveStage];
+    // row scales staged with the weights: [0] qkv then o, [1] gate_up then down
+    __shared__ float scl_s[3][kWWaves][kWave];   // qkv then o | gate_up | down
     static_assert(sizeof(AttnLds) <= sizeof(stage_s), "attention area larger than the stage");
     AttnLds& A = *reinterpret_cast<AttnLds*>(stage_s);
     // The layer table, copied once.  Read from global memory inside the
@@ -847,7 +979,8 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
 #ifdef HQ_ENGINE_TRACE
     __shared__ uint32_t trace_s[4 * 16 * 16];
     __shared__ uint32_t atr_s[4 * 16 * 16];
-    for (int i = threadIdx.x; i < 4 * 16 * 16; i += kThreads) atr_s[i] = 0;
+    __shared__ uint32_t sub_s[4 * 16 * 16];
+    for (int i = threadIdx.x; i < 4 * 16 * 16; i += kThreads) atr_s[i] = sub_s[i] = 0;
 #else
     uint32_t* const atr_s = nullptr;
 #endif
@@ -885,12 +1018,17 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     const int items = p.kv_heads * nsplit;
 
     // Weight prefetch schedule (the phases in between are its lead time);
-    // a wave overwrites stage slots only after its own dot has read them:
-    //   qkv      slots 0-2   issued at the end of P5 of the previous layer
+    // a wave overwrites stage slots only after its own dot has read them.
+    // Loads issued just before a hand-off would sit in the CU's memory queue
+    // ahead of the poll, so the gate_up and down halves wait until their
+    // phase's input has been read:
+    //   qkv      slots 0-2   after the P5 input read of the previous layer
     //   o        slots 5-6   end of P2
-    //   gate_up  slots 0-4   end of P2,  slots 5-9 at the end of P3
-    //   down     slots 0-4   end of P4
+    //   gate_up  slots 0-4   end of P2, its second half in registers (also
+    //            loaded at the end of P2, used at P4)
+    //   down     slots 5-9   after the P4 input read
     stage_rows<kQkvLPR, kQkvMAXC>(stage_s, !iw, lay_s[0].qkv, q0, q1, H, ww);
+    stage_scales<kQkvLPR>(scl_s[0], !iw, lay_s[0].qkv_scales, q0, q1, ww);
     float gin[kHidNPT] = {};   // input_norm of the coming P1 (input waves)
     if (iw) load_gamma(lay_s[0].input_norm, H, gin);
 
@@ -909,6 +1047,8 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         // each phase input is a fresh, fully initialised array: nothing of it
         // stays live into the next phase on any path
         float xin[kHidNPT] = {};
+        if (l > 0) watch_spread(p.ll_x5, H, E, budget, p.status);
+        block_sync();
         if (iw) {
             if (l == 0) {
 #pragma unroll
@@ -921,15 +1061,19 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         ENG_MARK(1);
         block_sync();
         ENG_MARK(2);
+#ifdef HQ_ENGINE_TRACE
+        uint32_t* const mk = l >= kTraceL0 && l < kTraceL0 + 4 ? sub_s + (l - kTraceL0) * 256 : nullptr;
+#else
+        uint32_t* const mk = nullptr;
+#endif
         float act = rmsnorm_quant(xin, H, gin, p.eps, xq_s, kQkvLPR * kQkvMAXC * 32, red, bmax);
         ENG_MARK(3);
         if (!iw && q0 + ww * 2 < q1) {
-            const float sq = row_scale<kQkvLPR>(Ly.qkv_scales, q0, q1, ww);
-            wait_all_memory();   // the staged qkv weights
+            wait_all_memory();   // the staged qkv weights and scales
             const int part = staged_dot<kQkvLPR, kQkvMAXC>(stage_s, xq_s, ww);
             const int acc = rows_acc<kQkvLPR, 0, 2>(part, lane_id());
             const int row = q0 + ww * 2 + lane_id();
-            if (lane_id() < 2 && row < q1) res_s[row - q0] = (float(acc) * act) * sq;
+            if (lane_id() < 2 && row < q1) res_s[row - q0] = (float(acc) * act) * scl_s[0][ww][lane_id()];
         }
         block_sync();
         publish_rows(res_s, p.ll_qkv + q0, q1 - q0, E + 1);
@@ -945,11 +1089,21 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         wait_all_memory();
         ENG_MARK(5);
         stage_rows<kOLPR, kOMAXC, 5>(stage_s, !iw, Ly.o, h0, h1, qd, ww);
+        stage_scales<kOLPR>(scl_s[0], !iw, Ly.o_scales, h0, h1, ww);
         stage_pairs<kGuHalf, 0>(stage_s, !iw, Ly.gate_up, g0, g1, I, H, ww);
+        stage_pair_scales(scl_s[1], !iw, Ly.gate_up_scales, g0, g1, I, ww);
+        uint4 gub[kGuHalf];   // second gate_up half (weight waves), used at P4
+#pragma unroll
+        for (int j = 0; j < kGuHalf; ++j) gub[j] = make_uint4(0, 0, 0, 0);
+        load_pairs<kGuHalf, kGuHalf>(gub, !iw, Ly.gate_up, g0, g1, I, H, ww);
 
         // ---- P3: quant -> o -> residual ----------------------------------------
         float att[kAttNPT] = {};
         float gpost[kHidNPT] = {};   // post_norm for P4, loaded once the poll is done
+        watch_spread(p.ll_att, qd, E + 2, budget, p.status);
+        SUB_MARK(mk, 9);
+        block_sync();
+        SUB_MARK(mk, 10);
         if (iw) {
             poll_into<kIThreads, kAttNPT>(p.ll_att, qd, E + 2, att, budget, p.status);
             load_gamma(Ly.post_norm, H, gpost);
@@ -959,12 +1113,15 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         ENG_MARK(7);
         act = quantize<kIThreads, kAttNPT>(att, qd, xq_s, kOLPR * kOMAXC * 32, bmax);
         if (!iw && h0 + ww < h1) {
-            const float so = row_scale<kOLPR>(Ly.o_scales, h0, h1, ww);
-            wait_all_memory();   // the staged o weights (and the first gate_up half)
+            // the staged o weights and scale, not the gate_up loads behind
+            // them (kGuHalf staged + 1 scale + kGuHalf register loads when the
+            // wave has pairs)
+            if (g0 + ww * 4 < g1) wait_memory_but<2 * kGuHalf + 1>();
+            else wait_all_memory();
             const int part = staged_dot<kOLPR, kOMAXC, 5>(stage_s, xq_s, ww);
             const int acc = rows_acc<kOLPR, 0, 1>(part, lane_id());
             if (lane_id() == 0) {
-                const float xn = xown_s[ww] + (float(acc) * act) * so;
+                const float xn = xown_s[ww] + (float(acc) * act) * scl_s[0][ww][0];
                 xown_s[ww] = xn;
                 res_s[ww] = xn;
             }
@@ -972,21 +1129,35 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         block_sync();
         publish_rows(res_s, p.ll_x3 + h0, h1 - h0, E + 3);
         ENG_MARK(8);
-        stage_pairs<kGuHalf, kGuHalf>(stage_s, !iw, Ly.gate_up, g0, g1, I, H, ww);
 
         // ---- P4: RMSNorm(post) -> quant -> gate_up -> SwiGLU -----------------------
         float xpost[kHidNPT] = {};
+        watch_spread(p.ll_x3, H, E + 3, budget, p.status);
+        SUB_MARK(mk, 11);
+        block_sync();
+        SUB_MARK(mk, 12);
         if (iw) poll_into<kIThreads, kHidNPT>(p.ll_x3, H, E + 3, xpost, budget, p.status);
         ENG_MARK(9);
         block_sync();
         ENG_MARK(10);
-        act = rmsnorm_quant(xpost, H, gpost, p.eps, xq_s, kGuLPR * 2 * kGuHalf * 32, red, bmax);
+        // The register half of gate_up landed during P3; waiting for it here,
+        // before the down prefetch is issued, settles the compiler's own wait
+        // for those registers (otherwise placed at their use, where it would
+        // also wait for the down prefetch, which the compiler cannot see).
+        if (!iw) wait_all_memory();
+        stage_rows<kDownLPR, kDownMAXC, 5>(stage_s, !iw, Ly.down, h0, h1, I, ww);
+        stage_scales<kDownLPR>(scl_s[2], !iw, Ly.down_scales, h0, h1, ww);
+        act = rmsnorm_quant(xpost, H, gpost, p.eps, xq_s, kGuLPR * 2 * kGuHalf * 32, red, bmax, mk);
         if (!iw && g0 + ww * 4 < g1) {
-            const int er = min(g0 + ww * 4 + min(lane_id(), 3), g1 - 1);
-            const float sg = gmem(Ly.gate_up_scales)[er];
-            const float su = gmem(Ly.gate_up_scales)[I + er];
-            wait_all_memory();   // the staged gate_up weights
-            const int part = staged_dot<kGuLPR, 2 * kGuHalf>(stage_s, xq_s, ww);
+            // the staged gate_up half, its scales and the register half, not
+            // the down prefetch behind them (kDownMAXC + 1 loads)
+            SUB_MARK(mk, 5);
+            if (h0 + ww < h1) wait_memory_but<kDownMAXC + 1>();
+            else wait_all_memory();
+            SUB_MARK(mk, 6);
+            const float sg = scl_s[1][ww][lane_id() & 3];
+            const float su = scl_s[1][ww][4 + (lane_id() & 3)];
+            const int part = staged_reg_dot<kGuLPR, kGuHalf, kGuHalf>(stage_s, gub, xq_s, ww);
             const int acc = rows_acc<kGuLPR, 0, 4>(part, lane_id());
             const int acc_up = rows_acc<kGuLPR, 4, 4>(part, lane_id());
             const int pair = g0 + ww * 4 + lane_id();
@@ -996,29 +1167,41 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
                 const float t = 1.0f + spec_expf(-g);
                 res_s[pair - g0] = (g / t) * u;
             }
+            SUB_MARK(mk, 7);
         }
         block_sync();
+        SUB_MARK(mk, 8);
         publish_rows(res_s, p.ll_act + g0, g1 - g0, E + 4);
         ENG_MARK(11);
-        stage_rows<kDownLPR, kDownMAXC>(stage_s, !iw, Ly.down, h0, h1, I, ww);
 
         // ---- P5: quant -> down -> residual -------------------------------------
         // all waves poll: the weight waves' down prefetch (issued just now)
         // lands well within the hand-off time
         float av[kActNPT] = {};
+        watch_spread(p.ll_act, I, E + 4, budget, p.status);
+        SUB_MARK(mk, 13);
+        block_sync();
+        SUB_MARK(mk, 14);
         poll_into<kThreads, kActNPT>(p.ll_act, I, E + 4, av, budget, p.status);
         if (iw && !final_layer) load_gamma(lay_s[l + 1].input_norm, H, gin);
         ENG_MARK(12);
         block_sync();
         ENG_MARK(13);
+        {
+            const hq_layer& Ln = lay_s[final_layer ? l : l + 1];
+            stage_rows<kQkvLPR, kQkvMAXC>(stage_s, !iw && !final_layer, Ln.qkv, q0, q1, H, ww);
+            stage_scales<kQkvLPR>(scl_s[0], !iw && !final_layer, Ln.qkv_scales, q0, q1, ww);
+        }
         act = quantize<kThreads, kActNPT>(av, I, xq_s, kDownLPR * kDownMAXC * 32, bmax);
         if (!iw && h0 + ww < h1) {
-            const float sd = row_scale<kDownLPR>(Ly.down_scales, h0, h1, ww);
-            wait_all_memory();   // the staged down weights
-            const int part = staged_dot<kDownLPR, kDownMAXC>(stage_s, xq_s, ww);
+            // the staged down weights and scale, not the next layer's qkv
+            // behind them (kQkvMAXC weight loads + 1 scale load)
+            if (!final_layer && q0 + ww * (kWave / kQkvLPR) < q1) wait_memory_but<kQkvMAXC + 1>();
+            else wait_all_memory();
+            const int part = staged_dot<kDownLPR, kDownMAXC, 5>(stage_s, xq_s, ww);
             const int acc = rows_acc<kDownLPR, 0, 1>(part, lane_id());
             if (lane_id() == 0) {
-                const float xn = xown_s[ww] + (float(acc) * act) * sd;
+                const float xn = xown_s[ww] + (float(acc) * act) * scl_s[2][ww][0];
                 xown_s[ww] = xn;
                 res_s[ww] = xn;
             }
@@ -1027,10 +1210,6 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         publish_rows(res_s, p.ll_x5 + h0, h1 - h0, E + 5);
         if (final_layer && tid < h1 - h0) p.x[h0 + tid] = res_s[tid];
         ENG_MARK(14);
-        {
-            const hq_layer& Ln = lay_s[final_layer ? l : l + 1];
-            stage_rows<kQkvLPR, kQkvMAXC>(stage_s, !iw && !final_layer, Ln.qkv, q0, q1, H, ww);
-        }
         ENG_MARK(15);
     }
 #ifdef HQ_ENGINE_TRACE
@@ -1038,6 +1217,7 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     for (int i = tid; i < 4 * 16 * 16; i += kThreads) {
         p.trace[size_t(b) * 4 * 16 * 16 + i] = trace_s[i];
         p.trace[size_t(gridDim.x + b) * 4 * 16 * 16 + i] = atr_s[i];
+        p.trace[size_t(2 * gridDim.x + b) * 4 * 16 * 16 + i] = sub_s[i];
     }
 #endif
     if (b == 0 && tid == 0) *p.epoch = base + 5u * uint32_t(p.L);
@@ -1090,7 +1270,7 @@ int engine_blocks(const hq_model* m)
 size_t engine_trace_bytes(const hq_model* m)
 {
 #ifdef HQ_ENGINE_TRACE
-    return size_t(2 * 256) * 4 * 16 * 16 * sizeof(uint32_t);
+    return size_t(3 * 256) * 4 * 16 * 16 * sizeof(uint32_t);
 #else
     (void)m;
     return 0;
