@@ -130,18 +130,15 @@ static hipError_t layer_gemv(const hq_model* m, const hq_state* st, int l, StepG
     return launch_step_gemv(kind, p, s);
 }
 
-static hipError_t enqueue_step(const hq_model* m, const hq_state* st, hipStream_t s)
+// The decoder layers of a step: the persistent layer kernel when the model
+// carries a device layer table and fits its limits, else five kernels per
+// layer.
+static hipError_t enqueue_layers(const hq_model* m, const hq_state* st, hipStream_t s)
 {
     const StepLayout Ly = step_layout(m, st->capacity);
     char* ws = static_cast<char*>(st->workspace);
-    const int H = m->hidden;
     const size_t kv_layer = size_t(st->capacity) * size_t(Ly.kv_size);
-
-    hipLaunchKernelGGL(embedding_kernel, dim3(1), dim3(kBlock), 0, s, m->embedding,
-                       m->embedding_scales, m->vocab, H, st->token, st->status, st->x);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-
+    hipError_t e = hipSuccess;
     const int nb = (m->device_layer && !(m->flags & HQ_MODEL_PER_LAYER_KERNELS) && engine_fits(m))
                        ? engine_blocks(m) : 0;
     if (nb > 0) {
@@ -173,6 +170,20 @@ static hipError_t enqueue_step(const hq_model* m, const hq_state* st, hipStream_
         if ((e = layer_gemv(m, st, l, StepGemv::GateUpSwiglu, s)) != hipSuccess) return e;
         if ((e = layer_gemv(m, st, l, StepGemv::DownResidual, s)) != hipSuccess) return e;
     }
+    return hipSuccess;
+}
+
+static hipError_t enqueue_step(const hq_model* m, const hq_state* st, hipStream_t s)
+{
+    const StepLayout Ly = step_layout(m, st->capacity);
+    char* ws = static_cast<char*>(st->workspace);
+    const int H = m->hidden;
+
+    hipLaunchKernelGGL(embedding_kernel, dim3(1), dim3(kBlock), 0, s, m->embedding,
+                       m->embedding_scales, m->vocab, H, st->token, st->status, st->x);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if ((e = enqueue_layers(m, st, s)) != hipSuccess) return e;
 
     GemvParams p{};
     p.w = m->embedding; p.ws = m->embedding_scales; p.rows = m->vocab; p.width = H;
@@ -233,6 +244,14 @@ extern "C" int hq_step_gemv(const hq_model* model, const hq_state* state, int la
     const StepGemv kinds[4] = {StepGemv::Qkv, StepGemv::OResidual, StepGemv::GateUpSwiglu,
                                StepGemv::DownResidual};
     return layer_gemv(model, state, layer, kinds[kind], static_cast<hipStream_t>(stream)) == hipSuccess
+               ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+extern "C" int hq_step_layers(const hq_model* model, const hq_state* state, void* stream)
+{
+    const int rc = validate(model, state);
+    if (rc != HQ_OK) return rc;
+    return enqueue_layers(model, state, static_cast<hipStream_t>(stream)) == hipSuccess
                ? HQ_OK : HQ_ERR_LAUNCH;
 }
 

@@ -196,6 +196,12 @@ int hq_decode_step(const hq_model* model, const hq_state* state, void* stream);
 int hq_step_gemv(const hq_model* model, const hq_state* state, int layer, int kind,
                  void* stream);
 
+/* Launch only the decoder layers of a step (the persistent layer kernel, or
+ * the five kernels per layer) on the state's buffers, at the state's current
+ * position, without the embedding, LM head or position advance, so their
+ * time can be measured alone.  No reference counterpart (measurement hook). */
+int hq_step_layers(const hq_model* model, const hq_state* state, void* stream);
+
 /* Capture `steps` consecutive decode steps enqueued on `stream` (which must
  * not be the default stream) into an executable HIP graph. */
 int hq_graph_capture(const hq_model* model, const hq_state* state, int steps,
