@@ -16,9 +16,11 @@ namespace hq {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Weights are read exactly once per step: stream them past the caches.
+// The pointer is global memory: a global (not flat) load waits on the
+// vector-memory counter only, never on the LDS counter.
 __device__ __forceinline__ uint4 load_w16(const uint8_t* p)
 {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    const u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 

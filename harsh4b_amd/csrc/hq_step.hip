@@ -59,7 +59,7 @@ static StepLayout step_layout(const hq_model* m, int capacity)
     L.lm_blocks = step_gemv_blocks(StepGemv::LmHead, m->vocab, 0, m->hidden);
     L.attn_part_bytes = align256(attention_workspace_floats(m->heads, L.max_chunks, m->head_dim) * 4);
     L.attn_counter_off = L.attn_part_bytes;
-    L.lm_val_off = L.attn_counter_off + align256(size_t(m->kv_heads) * 4);
+    L.lm_val_off = L.attn_counter_off + align256(size_t(m->heads > m->kv_heads ? m->heads : m->kv_heads) * 4);
     L.lm_idx_off = L.lm_val_off + align256(size_t(L.lm_blocks) * 4);
     L.lm_counter_off = L.lm_idx_off + align256(size_t(L.lm_blocks) * 4);
     L.epoch_off = L.lm_counter_off + align256(size_t(ticket_words(L.lm_blocks)) * 4);
