@@ -102,8 +102,7 @@ struct EngineParams {
     uint64_t* ll_amax;        // [gridDim.x] max |act| of each block's rows
     uint64_t* ll_pk;          // [I / 4] quantized act, 4 int8 per entry in S.xq's byte order
     uint32_t* epoch;
-    float* part;              // attention chunk partials [heads, max_chunks, D + 2]
-    int32_t* counters;        // [heads] chunk tickets, zero between launches
+    uint64_t* ll_part;        // attention chunk partials [heads, max_chunks, D + 2] (m, l, o)
     int max_chunks;
     uint32_t* trace;          // HQ_ENGINE_TRACE builds: timestamps
 };
@@ -133,10 +132,6 @@ struct KvBuf {
     uint16_t v[kAttnChunk * kD];
 };
 
-struct WaveScratch {               // per input wave (attention)
-    alignas(16) float q[kD];       // normalized, rotated query head
-    alignas(16) float s[kAttnChunk];
-};
 
 struct Shared {
     alignas(16) uint8_t xq[kMaxVec];    // quantized phase input, de-interleaved per 8
@@ -148,7 +143,8 @@ struct Shared {
     int done;                           // weight-wave completions (weight -> input)
     int ibar;                           // input-wave barrier arrivals
     KvBuf kv[kKvBufs];                  // K/V chunks of the attention items
-    WaveScratch ws[kIWaves];
+    alignas(16) float aq[kD];           // attention: the normalized, rotated query head
+    alignas(16) float as[kAttnChunk];   // attention: the chunk's scores
     hq_layer lay[kMaxLayers];
 #ifdef HQ_ENGINE_TRACE
     uint32_t trace[kTraceWords];
@@ -666,214 +662,235 @@ __device__ __forceinline__ void prefetch_kv(const EngineParams& p, int l, int kv
     }
 }
 
-// Attention item of input wave w: query head kvh*G + w of chunk c.
-__device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly, int l,
-                               int kvh, int c, int nc, int n, int pos, uint32_t epoch_qkv,
-                               uint32_t epoch_att, int& bseq, unsigned& budget)
+// Attention item (query head h, chunk c) of one block.  The four input waves
+// split the chunk's scores (16 positions each) and its V accumulation (32
+// dims each); each wave computes the softmax of the 64 scores itself (same
+// operations on the same values, same bits).  With several chunks, every
+// item publishes its partial (m, l, o) and the item of the last chunk
+// combines them in ascending chunk order as they arrive.  Same arithmetic as
+// attention_kernel's STEP mode (hq_attention.hip).
+__device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly, int l, int h, int c, int nc,
+                               int n, int pos, uint32_t epoch_qkv, uint32_t epoch_att, int& bseq,
+                               unsigned& budget)
 {
     const int w = threadIdx.x / kWave;
     const int lane = lane_id();
     const int G = p.G;
+    const int kvh = h / G;
     const int qd = p.heads * kD;
-    const bool active = w < G;
-    const int h = __builtin_amdgcn_readfirstlane(kvh * G + min(w, G - 1));
     const int t0 = c * kAttnChunk;
     const int tn = min(kAttnChunk, n - t0);
     const bool cur = c == nc - 1;            // the chunk holding the current position
-    WaveScratch& WS = S.ws[w];
     KvBuf& buf = S.kv[kb];
 
-    // norm weights and the RoPE row of this position
-    const float qn0 = gmem(Ly.q_norm)[lane], qn1 = gmem(Ly.q_norm)[lane + 64];
-    const float kn0 = gmem(Ly.k_norm)[lane], kn1 = gmem(Ly.k_norm)[lane + 64];
-    const float c0 = gmem(p.rope_cos)[size_t(pos) * (kD / 2) + lane];
-    const float s0 = gmem(p.rope_sin)[size_t(pos) * (kD / 2) + lane];
-
-    // q of head h (dims lane, lane+64), k and v of the kv head
-    // entries: q (dims lane, lane+64) of head h, then k and v of the kv head;
-    // the three row bases are scalar offsets, the lane is the vector offset
-    const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(p.ll_qkv);
-    const uint32_t vo = uint32_t(lane) * 8u;
-    const int sq_ = h * kD * 8;
-    const int sk_ = (qd + kvh * kD) * 8;
-    const int sv_ = (qd + (p.kv_heads + kvh) * kD) * 8;
-    uint64_t eq0 = ll_load(rq, vo, sq_), eq1 = ll_load(rq, vo, sq_ + 512);
-    uint64_t ek0 = ll_load(rq, vo, sk_), ek1 = ll_load(rq, vo, sk_ + 512);
-    uint64_t ev0 = ll_load(rq, vo, sv_), ev1 = ll_load(rq, vo, sv_ + 512);
-    unsigned spins = 0;
-    while (budget != 0) {
-        const int ready = int(ll_ready(eq0, epoch_qkv)) & int(ll_ready(eq1, epoch_qkv)) &
-                          int(ll_ready(ek0, epoch_qkv)) & int(ll_ready(ek1, epoch_qkv)) &
-                          int(ll_ready(ev0, epoch_qkv)) & int(ll_ready(ev1, epoch_qkv));
-        if (ready) break;
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
-        compiler_fence();
-        if (!ll_ready(eq0, epoch_qkv)) eq0 = ll_load(rq, vo, sq_);
-        if (!ll_ready(eq1, epoch_qkv)) eq1 = ll_load(rq, vo, sq_ + 512);
-        if (!ll_ready(ek0, epoch_qkv)) ek0 = ll_load(rq, vo, sk_);
-        if (!ll_ready(ek1, epoch_qkv)) ek1 = ll_load(rq, vo, sk_ + 512);
-        if (!ll_ready(ev0, epoch_qkv)) ev0 = ll_load(rq, vo, sv_);
-        if (!ll_ready(ev1, epoch_qkv)) ev1 = ll_load(rq, vo, sv_ + 512);
-    }
-    if (w == 0) TRACE(l, 25);
-    const float raw[6] = {bits_f32(uint32_t(eq0)), bits_f32(uint32_t(eq1)), bits_f32(uint32_t(ek0)),
-                          bits_f32(uint32_t(ek1)), bits_f32(uint32_t(ev0)), bits_f32(uint32_t(ev1))};
-
-    // per-head RMSNorm + RoPE of q (as attention_kernel's STEP prologue)
-    {
-        const float x0 = raw[0], x1 = raw[1];
-        float s = __builtin_fmaf(x0, x0, 0.0f);
-        s = __builtin_fmaf(x1, x1, s);
-        const float ss = wave_tree_sum64_all(s);
-        const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
-        const float y0 = (x0 / r) * qn0;
-        const float y1 = (x1 / r) * qn1;
-        WS.q[lane] = y0 * c0 - y1 * s0;
-        WS.q[lane + 64] = y1 * c0 + y0 * s0;
-    }
-    if (cur) {
-        // k (norm + RoPE) and v of this position as fp16; wave 0 keeps them
-        // for every wave of the item and writes the cache row
-        const float x0 = raw[2], x1 = raw[3];
-        float s = __builtin_fmaf(x0, x0, 0.0f);
-        s = __builtin_fmaf(x1, x1, s);
-        const float ss = wave_tree_sum64_all(s);
-        const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
-        const float y0 = (x0 / r) * kn0;
-        const float y1 = (x1 / r) * kn1;
-        const uint16_t k0 = f32_to_f16(y0 * c0 - y1 * s0), k1 = f32_to_f16(y1 * c0 + y0 * s0);
-        const uint16_t v0 = f32_to_f16(raw[4]), v1 = f32_to_f16(raw[5]);
-        if (w == 0) {
+    if (w == 0) {
+        // q of head h (dims lane, lane+64); for the current chunk also k and
+        // v of the kv head
+        const float qn0 = gmem(Ly.q_norm)[lane], qn1 = gmem(Ly.q_norm)[lane + 64];
+        const float kn0 = gmem(Ly.k_norm)[lane], kn1 = gmem(Ly.k_norm)[lane + 64];
+        const float c0 = gmem(p.rope_cos)[size_t(pos) * (kD / 2) + lane];
+        const float s0 = gmem(p.rope_sin)[size_t(pos) * (kD / 2) + lane];
+        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(p.ll_qkv);
+        const uint32_t vo = uint32_t(lane) * 8u;
+        const int sq_ = h * kD * 8;
+        const int sk_ = (qd + kvh * kD) * 8;
+        const int sv_ = (qd + (p.kv_heads + kvh) * kD) * 8;
+        const uint64_t done = uint64_t(epoch_qkv) << 32;
+        uint64_t eq0 = ll_load(rq, vo, sq_), eq1 = ll_load(rq, vo, sq_ + 512);
+        uint64_t ek0 = done, ek1 = done, ev0 = done, ev1 = done;
+        if (cur) {
+            ek0 = ll_load(rq, vo, sk_);
+            ek1 = ll_load(rq, vo, sk_ + 512);
+            ev0 = ll_load(rq, vo, sv_);
+            ev1 = ll_load(rq, vo, sv_ + 512);
+        }
+        unsigned spins = 0;
+        while (budget != 0) {
+            const int ready = int(ll_ready(eq0, epoch_qkv)) & int(ll_ready(eq1, epoch_qkv)) &
+                              int(ll_ready(ek0, epoch_qkv)) & int(ll_ready(ek1, epoch_qkv)) &
+                              int(ll_ready(ev0, epoch_qkv)) & int(ll_ready(ev1, epoch_qkv));
+            if (ready) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
+            compiler_fence();
+            if (!ll_ready(eq0, epoch_qkv)) eq0 = ll_load(rq, vo, sq_);
+            if (!ll_ready(eq1, epoch_qkv)) eq1 = ll_load(rq, vo, sq_ + 512);
+            if (!ll_ready(ek0, epoch_qkv)) ek0 = ll_load(rq, vo, sk_);
+            if (!ll_ready(ek1, epoch_qkv)) ek1 = ll_load(rq, vo, sk_ + 512);
+            if (!ll_ready(ev0, epoch_qkv)) ev0 = ll_load(rq, vo, sv_);
+            if (!ll_ready(ev1, epoch_qkv)) ev1 = ll_load(rq, vo, sv_ + 512);
+        }
+        TRACE(l, 25);
+        {
+            // per-head RMSNorm + RoPE of q (as attention_kernel's STEP prologue)
+            const float x0 = bits_f32(uint32_t(eq0)), x1 = bits_f32(uint32_t(eq1));
+            float s = __builtin_fmaf(x0, x0, 0.0f);
+            s = __builtin_fmaf(x1, x1, s);
+            const float ss = wave_tree_sum64_all(s);
+            const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
+            const float y0 = (x0 / r) * qn0;
+            const float y1 = (x1 / r) * qn1;
+            S.aq[lane] = y0 * c0 - y1 * s0;
+            S.aq[lane + 64] = y1 * c0 + y0 * s0;
+        }
+        if (cur) {
+            // k (norm + RoPE) and v of this position, as fp16, into the
+            // chunk's row; one query head of the group writes the cache row
+            const float x0 = bits_f32(uint32_t(ek0)), x1 = bits_f32(uint32_t(ek1));
+            float s = __builtin_fmaf(x0, x0, 0.0f);
+            s = __builtin_fmaf(x1, x1, s);
+            const float ss = wave_tree_sum64_all(s);
+            const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
+            const float y0 = (x0 / r) * kn0;
+            const float y1 = (x1 / r) * kn1;
+            const uint16_t k0 = f32_to_f16(y0 * c0 - y1 * s0), k1 = f32_to_f16(y1 * c0 + y0 * s0);
+            const uint16_t v0 = f32_to_f16(bits_f32(uint32_t(ev0))), v1 = f32_to_f16(bits_f32(uint32_t(ev1)));
             const int rr = pos - t0;
             buf.k[rr * kD + lane] = k0;
             buf.k[rr * kD + lane + 64] = k1;
             buf.v[rr * kD + lane] = v0;
             buf.v[rr * kD + lane + 64] = v1;
-            uint16_t* kl = p.keys + size_t(l) * size_t(p.kv_layer) + size_t(pos) * size_t(p.kv_stride) +
-                           size_t(kvh) * kD;
-            uint16_t* vl = p.values + size_t(l) * size_t(p.kv_layer) + size_t(pos) * size_t(p.kv_stride) +
-                           size_t(kvh) * kD;
-            kl[lane] = k0;
-            kl[lane + 64] = k1;
-            vl[lane] = v0;
-            vl[lane + 64] = v1;
+            if (h % G == 0) {
+                uint16_t* kl = p.keys + size_t(l) * size_t(p.kv_layer) + size_t(pos) * size_t(p.kv_stride) +
+                               size_t(kvh) * kD;
+                uint16_t* vl = p.values + size_t(l) * size_t(p.kv_layer) + size_t(pos) * size_t(p.kv_stride) +
+                               size_t(kvh) * kD;
+                kl[lane] = k0;
+                kl[lane + 64] = k1;
+                vl[lane] = v0;
+                vl[lane + 64] = v1;
+            }
         }
     }
-    // every wave's K/V copies have landed (the loads above were issued after
-    // them and have completed, in order), then the current row is in place
+    // every wave's K/V copies have landed, q and the current row are in place
     wait_all_memory();
     ibar(bseq, budget, p.status);
-    if (w == 0) TRACE(l, 26);
+    TRACE(l, 26);
 
-    // scores: 16 lanes per position (8 dims each), 4 positions per pass
+    // scores of positions 16w .. 16w+15: 16 lanes per position, 8 dims each
     const float scale = 1.0f / __builtin_sqrtf(float(kD));
     const int l16 = lane & 15;
     const int grp = lane >> 4;
-    float qv[8];
     {
-        const float4 qa = *reinterpret_cast<const float4*>(&WS.q[l16 * 8]);
-        const float4 qb = *reinterpret_cast<const float4*>(&WS.q[l16 * 8 + 4]);
+        float qv[8];
+        const float4 qa = *reinterpret_cast<const float4*>(&S.aq[l16 * 8]);
+        const float4 qb = *reinterpret_cast<const float4*>(&S.aq[l16 * 8 + 4]);
         qv[0] = qa.x; qv[1] = qa.y; qv[2] = qa.z; qv[3] = qa.w;
         qv[4] = qb.x; qv[5] = qb.y; qv[6] = qb.z; qv[7] = qb.w;
-    }
-#pragma unroll 4
-    for (int pass = 0; pass < kAttnChunk / 4; ++pass) {
-        const int t = pass * 4 + grp;
-        const uint4 kw = *reinterpret_cast<const uint4*>(&buf.k[t * kD + l16 * 8]);
-        const uint32_t kk[4] = {kw.x, kw.y, kw.z, kw.w};
-        float pp = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            pp = __builtin_fmaf(qv[2 * j], f16_to_f32(uint16_t(kk[j])), pp);
-            pp = __builtin_fmaf(qv[2 * j + 1], f16_to_f32(uint16_t(kk[j] >> 16)), pp);
+        for (int pass = 0; pass < 4; ++pass) {
+            const int t = 16 * w + 4 * pass + grp;
+            const uint4 kw = *reinterpret_cast<const uint4*>(&buf.k[t * kD + l16 * 8]);
+            const uint32_t kk[4] = {kw.x, kw.y, kw.z, kw.w};
+            float pp = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pp = __builtin_fmaf(qv[2 * j], f16_to_f32(uint16_t(kk[j])), pp);
+                pp = __builtin_fmaf(qv[2 * j + 1], f16_to_f32(uint16_t(kk[j] >> 16)), pp);
+            }
+            const float dot = row_tree_sum16(pp);
+            if (l16 == 0) S.as[t] = t < tn ? dot * scale : -__builtin_inff();
         }
-        const float dot = row_tree_sum16(pp);
-        if (l16 == 0) WS.s[t] = t < tn ? dot * scale : -__builtin_inff();
     }
-    lds_drain();
-    if (w == 0) TRACE(l, 27);
-    const float sc = WS.s[lane];
+    ibar(bseq, budget, p.status);
+    TRACE(l, 27);
+    const float sc = S.as[lane];
     const float m = wave_max64_all(sc);
     const float ex = (lane < tn) ? spec_expf(sc - m) : 0.0f;
     const float ls = wave_tree_sum64_all(ex);
-    WS.s[lane] = ex;
-    lds_drain();
 
-    // o[d] = fmaf chain of e_t * v_t[d] over ascending t; lane owns dims
-    // 2*lane, 2*lane+1
+    // o[d] = fmaf chain of e_t * v_t[d] over ascending t, dims 32w .. 32w+31
     // (positions past the context have e_t = 0 and zero V rows: their fmaf
     // returns the accumulator unchanged, bit for bit)
-    float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll 16
-    for (int t = 0; t < kAttnChunk; ++t) {
-        const float et = WS.s[t];
-        const uint32_t vv = *reinterpret_cast<const uint32_t*>(&buf.v[t * kD + 2 * lane]);
-        o0 = __builtin_fmaf(et, f16_to_f32(uint16_t(vv)), o0);
-        o1 = __builtin_fmaf(et, f16_to_f32(uint16_t(vv >> 16)), o1);
+    const int d = 32 * w + (lane & 31);
+    // V rows are read eight positions ahead of the chain that consumes them
+    float o = 0.0f;
+    {
+        constexpr int kB = 8;
+        uint16_t va[kB], vb[kB];
+        static_for<kB>([&](auto j) { va[j] = buf.v[j * kD + d]; });
+        static_for<kAttnChunk / kB>([&](auto bt) {
+            constexpr int t0 = bt * kB;
+            uint16_t* cur = (bt & 1) ? vb : va;
+            uint16_t* nxt = (bt & 1) ? va : vb;
+            if constexpr (t0 + kB < kAttnChunk)
+                static_for<kB>([&](auto j) { nxt[j] = buf.v[(t0 + kB + j) * kD + d]; });
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<kB>([&](auto j) { o = __builtin_fmaf(lane_f(ex, t0 + j), f16_to_f32(cur[j]), o); });
+        });
     }
+    TRACE(l, 28);
 
-    if (w == 0) TRACE(l, 28);
     if (nc == 1) {
         // combine over the single chunk: a = exp(m - M) with M = m
         const float al = spec_expf(m - m);
         const float L = __builtin_fmaf(al, ls, 0.0f);
-        const float inv = 1.0f / L;
-        const float O0 = __builtin_fmaf(al, o0, 0.0f), O1 = __builtin_fmaf(al, o1, 0.0f);
-        if (active) {
-            ll_store(p.ll_att + size_t(h) * kD + 2 * lane, O0 * inv, epoch_att);
-            ll_store(p.ll_att + size_t(h) * kD + 2 * lane + 1, O1 * inv, epoch_att);
-        }
-    } else if (active) {
-        // publish this chunk's partial, take the head's ticket; the last
-        // chunk to arrive combines all of them in ascending chunk order
+        const float O = __builtin_fmaf(al, o, 0.0f);
+        if (lane < 32) ll_store(p.ll_att + size_t(h) * kD + d, O * (1.0f / L), epoch_att);
+    } else {
         constexpr int pstride = kD + 2;
-        float* pp = p.part + (size_t(h) * p.max_chunks + c) * pstride;
-        if (lane == 0) { publish_f(pp, m); publish_f(pp + 1, ls); }
-        publish_f(pp + 2 + 2 * lane, o0);
-        publish_f(pp + 3 + 2 * lane, o1);
-        wait_all_memory();
-        int ticket = 0;
-        if (lane == 0) ticket = atomicAdd(p.counters + h, 1);
-        ticket = __builtin_amdgcn_readfirstlane(ticket);
-        if (ticket == nc - 1) {
-            if (lane == 0) publish_i(p.counters + h, 0);
-            wait_all_memory();
-            const float* base = p.part + size_t(h) * p.max_chunks * pstride;
-            // chunk maxima: lane i reads chunk i (and i + 64, ...) at once
+        uint64_t* hp = p.ll_part + size_t(h) * size_t(p.max_chunks) * pstride;
+        uint64_t* cp = hp + size_t(c) * pstride;
+        if (w == 0 && lane == 0) {
+            ll_store(cp, m, epoch_att);
+            ll_store(cp + 1, ls, epoch_att);
+        }
+        if (lane < 32) ll_store(cp + 2 + d, o, epoch_att);
+        if (cur) {
+            // M over all chunks: lane i watches chunk c0 + i of each group of 64
+            const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(hp, nc * pstride * 8);
+            unsigned spins = 0;
             float M = -__builtin_inff();
-            for (int c0 = 0; c0 < nc; c0 += kWave)
-                if (c0 + lane < nc) M = fmaxf(M, read_f(base + size_t(c0 + lane) * pstride));
-            M = wave_max64_all(M);
-            // the chunks in ascending order, eight chunks' loads in flight
-            float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
-            for (int c0 = 0; c0 < nc; c0 += 8) {
-                float pm[8], pl[8], po0[8], po1[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float* pc = base + size_t(min(c0 + j, nc - 1)) * pstride;
-                    pm[j] = read_f(pc);
-                    pl[j] = read_f(pc + 1);
-                    po0[j] = read_f(pc + 2 + 2 * lane);
-                    po1[j] = read_f(pc + 3 + 2 * lane);
+            for (int c0 = 0; c0 < nc; c0 += kWave) {
+                const int cc = min(c0 + lane, nc - 1);
+                uint64_t em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
+                while (budget != 0) {
+                    if (ll_ready(em, epoch_att)) break;
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
+                    compiler_fence();
+                    if (!ll_ready(em, epoch_att)) em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
                 }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    if (c0 + j < nc) {
-                        const float al = spec_expf(pm[j] - M);
-                        L = __builtin_fmaf(al, pl[j], L);
-                        O0 = __builtin_fmaf(al, po0[j], O0);
-                        O1 = __builtin_fmaf(al, po1[j], O1);
-                    }
-                }
+                M = fmaxf(M, bits_f32(uint32_t(em)));
             }
-            const float inv = 1.0f / L;
-            ll_store(p.ll_att + size_t(h) * kD + 2 * lane, O0 * inv, epoch_att);
-            ll_store(p.ll_att + size_t(h) * kD + 2 * lane + 1, O1 * inv, epoch_att);
+            M = wave_max64_all(M);
+            // L and O over ascending chunks, eight chunks' entries in flight
+            // (their m entries have all arrived above)
+            float L = 0.0f, O = 0.0f;
+            for (int c0 = 0; c0 < nc; c0 += 8) {
+                uint64_t em[8], el[8], eo[8];
+                static_for<8>([&](auto j) {
+                    const int cc = min(c0 + j, nc - 1);
+                    em[j] = ll_load(rp, 0u, (cc * pstride) * 8);
+                    el[j] = ll_load(rp, 0u, (cc * pstride + 1) * 8);
+                    eo[j] = ll_load(rp, uint32_t(d) * 8u, (cc * pstride + 2) * 8);
+                });
+                while (budget != 0) {
+                    int ready = 1;
+                    static_for<8>([&](auto j) { ready &= int(ll_ready(el[j], epoch_att)) & int(ll_ready(eo[j], epoch_att)); });
+                    if (ready) break;
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
+                    compiler_fence();
+                    static_for<8>([&](auto j) {
+                        const int cc = min(c0 + j, nc - 1);
+                        if (!ll_ready(el[j], epoch_att)) el[j] = ll_load(rp, 0u, (cc * pstride + 1) * 8);
+                        if (!ll_ready(eo[j], epoch_att)) eo[j] = ll_load(rp, uint32_t(d) * 8u, (cc * pstride + 2) * 8);
+                    });
+                }
+                static_for<8>([&](auto j) {
+                    if (c0 + j < nc) {
+                        const float al = spec_expf(bits_f32(uint32_t(em[j])) - M);
+                        L = __builtin_fmaf(al, bits_f32(uint32_t(el[j])), L);
+                        O = __builtin_fmaf(al, bits_f32(uint32_t(eo[j])), O);
+                    }
+                });
+            }
+            if (lane < 32) ll_store(p.ll_att + size_t(h) * kD + d, O * (1.0f / L), epoch_att);
         }
     }
-    if (w == 0) TRACE(l, 29);
-    // the item's LDS (buf, scratch) may be reused only after every wave is done
+    TRACE(l, 29);
+    // the item's LDS (K/V chunk, q, scores) may be reused once every wave is done
     ibar(bseq, budget, p.status);
 }
 
@@ -893,7 +910,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
     const int nown = R.h1 - R.h0;
     const int n = pos + 1;
     const int nc = (n + kAttnChunk - 1) / kAttnChunk;
-    const int items = p.kv_heads * nc;
+    const int items = p.heads * nc;   // attention items: (query head, chunk)
     const int NB = gridDim.x;
     const int b = blockIdx.x;
     int bseq = 0;   // input-barrier count
@@ -929,7 +946,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         // this layer's attention K/V: copies start now and land while the
         // qkv hand-off travels
         for (int it = b, k = 0; it < items && k < kKvBufs; it += NB, ++k)
-            prefetch_kv(p, l, it / nc, (it % nc) * kAttnChunk, n, pos, k);
+            prefetch_kv(p, l, (it / nc) / p.G, (it % nc) * kAttnChunk, n, pos, k);
         wait_lds_geq(&S.done, kWWaves * (g + 1), budget, p.status);
         TRACE(l, 4);
         publish_rows(p.ll_qkv + R.q0, R.q1 - R.q0, E + 1);
@@ -937,7 +954,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         // ---- P2: attention ------------------------------------------------------------
         for (int it = b, k = 0; it < items; it += NB, ++k) {
             const int kb = k < kKvBufs ? k : (k & 1);
-            if (k >= kKvBufs) prefetch_kv(p, l, it / nc, (it % nc) * kAttnChunk, n, pos, kb);
+            if (k >= kKvBufs) prefetch_kv(p, l, (it / nc) / p.G, (it % nc) * kAttnChunk, n, pos, kb);
             attention_item(p, kb, Ly, l, it / nc, it % nc, nc, n, pos, E + 1, E + 2, bseq, budget);
         }
 
@@ -1151,8 +1168,7 @@ size_t engine_ll_entries(const hq_model* m)
 }
 
 hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, uint32_t* epoch,
-                         float* part, int32_t* counters, int max_chunks, int nb, uint32_t* trace,
-                         hipStream_t s)
+                         uint64_t* part, int max_chunks, int nb, uint32_t* trace, hipStream_t s)
 {
     EngineParams p{};
     p.layers = m->device_layer;
@@ -1183,8 +1199,7 @@ hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, ui
     p.ll_amax = p.ll_act + m->intermediate;
     p.ll_pk = p.ll_amax + eng::kIThreads;
     p.epoch = epoch;
-    p.part = part;
-    p.counters = counters;
+    p.ll_part = part;
     p.max_chunks = max_chunks;
     p.trace = trace;
     hipLaunchKernelGGL(engine_kernel, dim3(nb), dim3(eng::kThreads), 0, s, p);

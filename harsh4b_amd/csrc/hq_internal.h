@@ -79,8 +79,7 @@ int engine_blocks(const hq_model* m);
 // 64-bit hand-off entries the kernel needs in the workspace.
 size_t engine_ll_entries(const hq_model* m);
 hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, uint32_t* epoch,
-                         float* part, int32_t* counters, int max_chunks, int nb, uint32_t* trace,
-                         hipStream_t s);
+                         uint64_t* part, int max_chunks, int nb, uint32_t* trace, hipStream_t s);
 // HQ_ENGINE_TRACE builds: bytes of phase timestamps kept after the step
 // workspace proper (0 otherwise).
 size_t engine_trace_bytes(const hq_model* m);

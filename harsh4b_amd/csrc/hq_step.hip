@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kBlock) void embedding_kernel(
 struct StepLayout {
     int q_size, kv_size, groups, max_chunks, lm_blocks;
     size_t attn_part_bytes, attn_counter_off, lm_val_off, lm_idx_off, lm_counter_off;
-    size_t epoch_off, ll_off, trace_off, total;
+    size_t epoch_off, ll_off, eng_part_off, trace_off, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -64,7 +64,8 @@ static StepLayout step_layout(const hq_model* m, int capacity)
     L.lm_counter_off = L.lm_idx_off + align256(size_t(L.lm_blocks) * 4);
     L.epoch_off = L.lm_counter_off + align256(size_t(ticket_words(L.lm_blocks)) * 4);
     L.ll_off = L.epoch_off + 256;
-    L.trace_off = L.ll_off + align256(engine_ll_entries(m) * 8);
+    L.eng_part_off = L.ll_off + align256(engine_ll_entries(m) * 8);
+    L.trace_off = L.eng_part_off + align256(size_t(m->heads) * L.max_chunks * (m->head_dim + 2) * 8);
     L.total = L.trace_off + engine_trace_bytes(m);
     return L;
 }
@@ -143,8 +144,8 @@ static hipError_t enqueue_layers(const hq_model* m, const hq_state* st, hipStrea
                        ? engine_blocks(m) : 0;
     if (nb > 0) {
         e = launch_engine(m, st, reinterpret_cast<uint64_t*>(ws + Ly.ll_off),
-                          reinterpret_cast<uint32_t*>(ws + Ly.epoch_off), reinterpret_cast<float*>(ws),
-                          reinterpret_cast<int32_t*>(ws + Ly.attn_counter_off), Ly.max_chunks, nb,
+                          reinterpret_cast<uint32_t*>(ws + Ly.epoch_off),
+                          reinterpret_cast<uint64_t*>(ws + Ly.eng_part_off), Ly.max_chunks, nb,
                           engine_trace_bytes(m) ? reinterpret_cast<uint32_t*>(ws + Ly.trace_off) : nullptr, s);
         if (e != hipSuccess) return e;
     }
