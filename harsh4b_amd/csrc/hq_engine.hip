@@ -58,7 +58,7 @@ constexpr int kMaxHidden = 2560;
 constexpr int kMaxOwn = 16;                      // residual rows per block
 constexpr int kMaxRes = 64;                      // outputs of one GEMV phase per block
 constexpr int kMaxLayers = 64;                   // layer table copy in LDS
-constexpr int kKvBufs = 2;                       // attention items with prefetched K/V
+constexpr int kGroup = 4;                         // chunks of 64 positions per attention item
 constexpr unsigned kSpinLimit = 1u << 22;           // rounds one wait may spin
 #ifdef HQ_ENGINE_TRACE
 // Timestamps (low 32 bits of the 100 MHz clock) of layers kTraceL0 ..
@@ -142,9 +142,12 @@ struct Shared {
     int xq_seq;                         // input-wave xq posts, 4 per phase (input -> weight)
     int done;                           // weight-wave completions (weight -> input)
     int ibar;                           // input-wave barrier arrivals
-    KvBuf kv[kKvBufs];                  // K/V chunks of the attention items
+    int hs;                             // hand-offs received by the input waves, 4 per phase
+    KvBuf kv[kGroup];                   // K/V chunks of the block's attention item
     alignas(16) float aq[kD];           // attention: the normalized, rotated query head
-    alignas(16) float as[kAttnChunk];   // attention: the chunk's scores
+    alignas(16) float as[kGroup * kAttnChunk];   // attention: the item's scores
+    alignas(16) float po[kGroup][kD];   // attention: chunk partials o, m, l
+    float pm[kGroup], pl[kGroup];
     hq_layer lay[kMaxLayers];
 #ifdef HQ_ENGINE_TRACE
     uint32_t trace[kTraceWords];
@@ -400,6 +403,13 @@ __device__ __forceinline__ void post_xq(float act)
     if (lane_id() == 0) __hip_atomic_fetch_add(&S.xq_seq, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// This input wave has received a phase's hand-off: the weight waves time
+// their next loads by it.
+__device__ __forceinline__ void post_hs()
+{
+    if (lane_id() == 0) __hip_atomic_fetch_add(&S.hs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 template <int NPT>
 __device__ __forceinline__ void load_gamma(const float* g, int n, float (&out)[NPT])
 {
@@ -418,6 +428,27 @@ __device__ __forceinline__ void load_gamma(const float* g, int n, float (&out)[N
 // weights are read once per step).
 constexpr int kBufNT = 2;
 
+// Weight-load pacing: a weight wave waits WAVE_GAP (s_sleep units of 64
+// clocks) per wave index before a phase's loads and CHUNK_GAP between its
+// chunk loads, so the next phase's weights stream in over a few
+// microseconds instead of one burst that would queue ahead of the
+// hand-off reads in the memory system.
+constexpr int pace(int wave_gap, int chunk_gap) { return wave_gap << 8 | chunk_gap; }
+constexpr int kPaceQkv = pace(0, 0), kPaceO = pace(0, 0), kPaceGu = pace(0, 0), kPaceDown = pace(0, 0);
+
+template <int P>
+__device__ __forceinline__ void pace_start(int ww)
+{
+    if constexpr ((P >> 8) > 0)
+        for (int i = 0; i < ww; ++i) __builtin_amdgcn_s_sleep(P >> 8);
+}
+template <int P>
+__device__ __forceinline__ void pace_chunk(int j)
+{
+    if constexpr ((P & 255) > 0)
+        if (j > 0) __builtin_amdgcn_s_sleep(P & 255);
+}
+
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
     typedef unsigned int v4u __attribute__((ext_vector_type(4)));
@@ -431,7 +462,7 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // activations).  Each lane also loads the scale of its own row.  A wave
 // without rows loads the block's last row and discards it (a conditional
 // load would keep the registers' previous contents alive across the loop).
-template <int LPR, int C>
+template <int LPR, int C, int P>
 __device__ __forceinline__ void load_rows(uint4 (&w)[C], float& s, const uint8_t* W, const float* Sc, int r0,
                                           int r1, int K, int ww)
 {
@@ -443,9 +474,13 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[C], float& s, const uint8_t
     const int li = lane % LPR;
     const int nch = K >> 5;
     const uint32_t off = uint32_t(row) * uint32_t(K >> 1);
-#pragma unroll
-    for (int j = 0; j < C; ++j) w[j] = bload16(rw, off + uint32_t(min(li + j * LPR, nch - 1)) * 16u);
+    pace_start<P>(ww);
     s = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(rs, uint32_t(row) * 4u, 0, 0));
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        pace_chunk<P>(j);
+        w[j] = bload16(rw, off + uint32_t(min(li + j * LPR, nch - 1)) * 16u);
+    }
 }
 
 // SwiGLU rows: pairs [p0, p1) of the I gate rows; weight wave ww owns pairs
@@ -463,9 +498,13 @@ __device__ __forceinline__ void load_pairs(uint4 (&w)[kGuC], float& s, const uin
     const int li = lane & 7;
     const int nch = K >> 5;
     const uint32_t off = uint32_t(row) * uint32_t(K >> 1);
-#pragma unroll
-    for (int j = 0; j < kGuC; ++j) w[j] = bload16(rw, off + uint32_t(min(li + j * 8, nch - 1)) * 16u);
+    pace_start<kPaceGu>(ww);
     s = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(rs, uint32_t(row) * 4u, 0, 0));
+#pragma unroll
+    for (int j = 0; j < kGuC; ++j) {
+        pace_chunk<kPaceGu>(j);
+        w[j] = bload16(rw, off + uint32_t(min(li + j * 8, nch - 1)) * 16u);
+    }
 }
 
 // 16 * partial dot product of this lane's C chunks with the LDS activations.
@@ -516,23 +555,36 @@ struct Rows {
     int h0, h1, q0, q1, g0, g1;
 };
 
+// Weight loads are issued once the input waves have received hand-off e
+// (4 per layer: inputs of qkv, o, gate_up and down): the weights then stream
+// while the input waves compute, not while the next hand-off is in flight.
+constexpr bool kLoadInWindows = true;
+
+__device__ __forceinline__ void load_window(int e, unsigned& budget, int32_t* status)
+{
+    if constexpr (kLoadInWindows) wait_lds_geq(&S.hs, kIWaves * (e + 1), budget, status);
+}
+
 __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsigned& budget)
 {
     const int H = p.H, I = p.I;
     const int qd = p.heads * kD;
     const int lane = lane_id();
-    const bool has_q = R.q0 + ww * 2 < R.q1;
+    // every wave runs every dot (a wave without rows of a GEMV computes on
+    // the clamped last row and stores nothing), so each dot waits for exactly
+    // its own weight loads on every path
     const bool has_o = R.h0 + ww < R.h1;
-    const bool has_g = R.g0 + ww * 4 < R.g1;
-    // Loads are issued in the order the phases use them, each right after the
-    // dot that frees its registers: gate_up after qkv, down after o, the next
-    // layer's qkv after gate_up and its o after down.  Every GEMV's weights
-    // so have one to three hand-offs of lead time while a wave holds at most
+    // Loads are issued in the order the phases use them, each after the dot
+    // that frees its registers and once the input waves hold the next
+    // hand-off: gate_up once the attention output is in, down once the
+    // attention residual is in, the next layer's qkv once the down input is
+    // in and its o once the layer output is in.  Every GEMV's weights so
+    // have one to two hand-offs of lead time while a wave holds at most
     // about two phases of weights.
     uint4 wq[kQkvC] = {}, wo[kOC] = {}, wg[kGuC] = {}, wd[kDownC] = {};
     float sq = 0.0f, so = 0.0f, sg = 0.0f, sd = 0.0f;
-    load_rows<kQkvLPR, kQkvC>(wq, sq, S.lay[0].qkv, S.lay[0].qkv_scales, R.q0, R.q1, H, ww);
-    load_rows<kOLPR, kOC>(wo, so, S.lay[0].o, S.lay[0].o_scales, R.h0, R.h1, qd, ww);
+    load_rows<kQkvLPR, kQkvC, pace(0, 0)>(wq, sq, S.lay[0].qkv, S.lay[0].qkv_scales, R.q0, R.q1, H, ww);
+    load_rows<kOLPR, kOC, pace(0, 0)>(wo, so, S.lay[0].o, S.lay[0].o_scales, R.h0, R.h1, qd, ww);
 #pragma unroll 1
     for (int l = 0; l < p.L; ++l) {
         const bool more = l + 1 < p.L;
@@ -541,7 +593,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsign
         // ---- P1: qkv
         wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 1), budget, p.status);
         if (ww == 0) TRACE(l, 16);
-        if (has_q) {
+        {
             const float act = S.act;
             const int acc = rows_acc<kQkvLPR, 0, 2>(reg_dot<kQkvLPR, kQkvC>(wq, S.xq));
             const int row = R.q0 + ww * 2 + lane;
@@ -550,22 +602,27 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsign
         }
         post_done();
         if (ww == 0) TRACE(l, 17);
+        if (ww == kWWaves - 1) TRACE(l, 47);
+        load_window(4 * l + 1, budget, p.status);
         load_pairs(wg, sg, Ly.gate_up, Ly.gate_up_scales, R.g0, R.g1, I, H, ww);
         // ---- P3: o (the residual add is the input waves')
         wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 2), budget, p.status);
         if (ww == 0) TRACE(l, 18);
-        if (has_o) {
+        if (ww == kWWaves - 1) TRACE(l, 45);
+        {
             const float act = S.act;
             const int acc = rows_acc<kOLPR, 0, 1>(reg_dot<kOLPR, kOC>(wo, S.xq));
-            if (lane == 0) S.res[ww] = (float(acc) * act) * so;
+            if (has_o && lane == 0) S.res[ww] = (float(acc) * act) * so;
         }
         post_done();
         if (ww == 0) TRACE(l, 19);
-        load_rows<kDownLPR, kDownC>(wd, sd, Ly.down, Ly.down_scales, R.h0, R.h1, I, ww);
+        if (ww == kWWaves - 1) TRACE(l, 46);
+        load_window(4 * l + 2, budget, p.status);
+        load_rows<kDownLPR, kDownC, kPaceDown>(wd, sd, Ly.down, Ly.down_scales, R.h0, R.h1, I, ww);
         // ---- P4: gate_up + SwiGLU
         wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 3), budget, p.status);
         if (ww == 0) TRACE(l, 20);
-        if (has_g) {
+        {
             const float act = S.act;
             const int part = reg_dot<kGuLPR, kGuC>(wg, S.xq);
             const int acc = rows_acc<kGuLPR, 0, 4>(part);
@@ -587,18 +644,24 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsign
         }
         post_done();
         if (ww == 0) TRACE(l, 21);
-        if (more) load_rows<kQkvLPR, kQkvC>(wq, sq, Ln.qkv, Ln.qkv_scales, R.q0, R.q1, H, ww);
+        // (after the last layer the same loads, all of one 16-byte block:
+        // the instruction sequence, and so every dot's wait, is the same on
+        // every path)
+        load_window(4 * l + 3, budget, p.status);
+        load_rows<kQkvLPR, kQkvC, kPaceQkv>(wq, sq, Ln.qkv, Ln.qkv_scales, R.q0, more ? R.q1 : R.q0 + 1,
+                                            more ? H : 32, ww);
         // ---- P5: down (the residual add is the input waves')
         wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 4), budget, p.status);
         if (ww == 0) TRACE(l, 22);
-        if (has_o) {
+        {
             const float act = S.act;
             const int acc = rows_acc<kDownLPR, 0, 1>(reg_dot<kDownLPR, kDownC>(wd, S.xq));
-            if (lane == 0) S.res[ww] = (float(acc) * act) * sd;
+            if (has_o && lane == 0) S.res[ww] = (float(acc) * act) * sd;
         }
         post_done();
         if (ww == 0) TRACE(l, 23);
-        if (more) load_rows<kOLPR, kOC>(wo, so, Ln.o, Ln.o_scales, R.h0, R.h1, qd, ww);
+        if (more) load_window(4 * (l + 1), budget, p.status);
+        load_rows<kOLPR, kOC, kPaceO>(wo, so, Ln.o, Ln.o_scales, R.h0, more ? R.h1 : R.h0 + 1, more ? qd : 32, ww);
     }
 }
 
@@ -662,14 +725,64 @@ __device__ __forceinline__ void prefetch_kv(const EngineParams& p, int l, int kv
     }
 }
 
-// Attention item (query head h, chunk c) of one block.  The four input waves
-// split the chunk's scores (16 positions each) and its V accumulation (32
-// dims each); each wave computes the softmax of the 64 scores itself (same
-// operations on the same values, same bits).  With several chunks, every
-// item publishes its partial (m, l, o) and the item of the last chunk
-// combines them in ascending chunk order as they arrive.  Same arithmetic as
+// K/V of chunks c0 .. c0+ncg-1 of kv head kvh into S.kv[0 .. ncg).
+__device__ __forceinline__ void prefetch_group(const EngineParams& p, int l, int kvh, int c0, int ncg, int n,
+                                               int pos)
+{
+    for (int c = 0; c < ncg; ++c) prefetch_kv(p, l, kvh, (c0 + c) * kAttnChunk, n, pos, c);
+}
+
+// V accumulation of one or two chains per lane: o[d] = fmaf chain of
+// e_t * v_t[d] over ascending t of a chunk (positions past the context have
+// e_t = 0 and zero V rows: their fmaf returns the accumulator unchanged, bit
+// for bit).  V values are read eight positions ahead of the chain.
+template <int NCH>
+__device__ __forceinline__ void v_chains(const uint16_t* va, const uint16_t* vb, float ea, float eb, float& oa,
+                                         float& ob)
+{
+    constexpr int kB = 8 / NCH;
+    uint16_t xa[2][kB], xb[2][kB];
+    static_for<kB>([&](auto j) {
+        xa[0][j] = va[j * kD];
+        if constexpr (NCH == 2) xb[0][j] = vb[j * kD];
+    });
+    static_for<kAttnChunk / kB>([&](auto bt) {
+        constexpr int t0 = bt * kB;
+        constexpr int cur = bt & 1;
+        if constexpr (t0 + kB < kAttnChunk)
+            static_for<kB>([&](auto j) {
+                xa[cur ^ 1][j] = va[(t0 + kB + j) * kD];
+                if constexpr (NCH == 2) xb[cur ^ 1][j] = vb[(t0 + kB + j) * kD];
+            });
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<kB>([&](auto j) {
+            oa = __builtin_fmaf(lane_f(ea, t0 + j), f16_to_f32(xa[cur][j]), oa);
+            if constexpr (NCH == 2) ob = __builtin_fmaf(lane_f(eb, t0 + j), f16_to_f32(xb[cur][j]), ob);
+        });
+    });
+}
+
+// Softmax terms of chunk c of the item (scores in S.as): the chunk maximum,
+// e_t in lane t, and the tree sum of the e_t.
+__device__ __forceinline__ void chunk_softmax(int c, int tn, float& m, float& ex, float& ls)
+{
+    const int lane = lane_id();
+    const float sc = S.as[c * kAttnChunk + lane];
+    m = wave_max64_all(sc);
+    ex = (lane < tn) ? spec_expf(sc - m) : 0.0f;
+    ls = wave_tree_sum64_all(ex);
+}
+
+// Attention item (query head h, chunk group g of ng) of one block: chunks
+// c0 = 4g .. c0+ncg-1.  The four input waves split the group's scores (four
+// positions per pass); then wave w accumulates V of chunk w/2 (and 2 + w/2)
+// for dims 64*(w&1) + lane, each wave computing the softmax terms of its
+// chunks itself (same operations on the same values, same bits).  A single
+// group combines its chunks in LDS; with several groups every item publishes
+// its chunks' partials (m, l, o) and the item of the last group combines all
+// chunks of the head in ascending order as they arrive.  Same arithmetic as
 // attention_kernel's STEP mode (hq_attention.hip).
-__device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly, int l, int h, int c, int nc,
+__device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l, int h, int g, int ng, int nc,
                                int n, int pos, uint32_t epoch_qkv, uint32_t epoch_att, int& bseq,
                                unsigned& budget)
 {
@@ -678,18 +791,17 @@ __device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly
     const int G = p.G;
     const int kvh = h / G;
     const int qd = p.heads * kD;
-    const int t0 = c * kAttnChunk;
-    const int tn = min(kAttnChunk, n - t0);
-    const bool cur = c == nc - 1;            // the chunk holding the current position
-    KvBuf& buf = S.kv[kb];
+    const int c0 = g * kGroup;
+    const int ncg = min(kGroup, nc - c0);
+    const bool cur = g == ng - 1;            // the group holding the current position
 
     if (w == 0) {
-        // q of head h (dims lane, lane+64); for the current chunk also k and
+        // q of head h (dims lane, lane+64); for the current group also k and
         // v of the kv head
         const float qn0 = gmem(Ly.q_norm)[lane], qn1 = gmem(Ly.q_norm)[lane + 64];
         const float kn0 = gmem(Ly.k_norm)[lane], kn1 = gmem(Ly.k_norm)[lane + 64];
-        const float c0 = gmem(p.rope_cos)[size_t(pos) * (kD / 2) + lane];
-        const float s0 = gmem(p.rope_sin)[size_t(pos) * (kD / 2) + lane];
+        const float cs = gmem(p.rope_cos)[size_t(pos) * (kD / 2) + lane];
+        const float sn = gmem(p.rope_sin)[size_t(pos) * (kD / 2) + lane];
         const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(p.ll_qkv);
         const uint32_t vo = uint32_t(lane) * 8u;
         const int sq_ = h * kD * 8;
@@ -730,12 +842,12 @@ __device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly
             const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
             const float y0 = (x0 / r) * qn0;
             const float y1 = (x1 / r) * qn1;
-            S.aq[lane] = y0 * c0 - y1 * s0;
-            S.aq[lane + 64] = y1 * c0 + y0 * s0;
+            S.aq[lane] = y0 * cs - y1 * sn;
+            S.aq[lane + 64] = y1 * cs + y0 * sn;
         }
         if (cur) {
-            // k (norm + RoPE) and v of this position, as fp16, into the
-            // chunk's row; one query head of the group writes the cache row
+            // k (norm + RoPE) and v of this position, as fp16, into the row
+            // of the last chunk; one query head of the group writes the cache
             const float x0 = bits_f32(uint32_t(ek0)), x1 = bits_f32(uint32_t(ek1));
             float s = __builtin_fmaf(x0, x0, 0.0f);
             s = __builtin_fmaf(x1, x1, s);
@@ -743,13 +855,14 @@ __device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly
             const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
             const float y0 = (x0 / r) * kn0;
             const float y1 = (x1 / r) * kn1;
-            const uint16_t k0 = f32_to_f16(y0 * c0 - y1 * s0), k1 = f32_to_f16(y1 * c0 + y0 * s0);
+            const uint16_t k0 = f32_to_f16(y0 * cs - y1 * sn), k1 = f32_to_f16(y1 * cs + y0 * sn);
             const uint16_t v0 = f32_to_f16(bits_f32(uint32_t(ev0))), v1 = f32_to_f16(bits_f32(uint32_t(ev1)));
-            const int rr = pos - t0;
-            buf.k[rr * kD + lane] = k0;
-            buf.k[rr * kD + lane + 64] = k1;
-            buf.v[rr * kD + lane] = v0;
-            buf.v[rr * kD + lane + 64] = v1;
+            KvBuf& lb = S.kv[ncg - 1];
+            const int rr = pos - (nc - 1) * kAttnChunk;
+            lb.k[rr * kD + lane] = k0;
+            lb.k[rr * kD + lane + 64] = k1;
+            lb.v[rr * kD + lane] = v0;
+            lb.v[rr * kD + lane + 64] = v1;
             if (h % G == 0) {
                 uint16_t* kl = p.keys + size_t(l) * size_t(p.kv_layer) + size_t(pos) * size_t(p.kv_stride) +
                                size_t(kvh) * kD;
@@ -767,82 +880,104 @@ __device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly
     ibar(bseq, budget, p.status);
     TRACE(l, 26);
 
-    // scores of positions 16w .. 16w+15: 16 lanes per position, 8 dims each
-    const float scale = 1.0f / __builtin_sqrtf(float(kD));
-    const int l16 = lane & 15;
-    const int grp = lane >> 4;
+    // scores: pass P of a chunk covers its positions 4P .. 4P+3, 16 lanes
+    // per position (8 dims each); wave w takes passes w, w+4, w+8, w+12
     {
+        const float scale = 1.0f / __builtin_sqrtf(float(kD));
+        const int l16 = lane & 15;
+        const int grp = lane >> 4;
         float qv[8];
         const float4 qa = *reinterpret_cast<const float4*>(&S.aq[l16 * 8]);
         const float4 qb = *reinterpret_cast<const float4*>(&S.aq[l16 * 8 + 4]);
         qv[0] = qa.x; qv[1] = qa.y; qv[2] = qa.z; qv[3] = qa.w;
         qv[4] = qb.x; qv[5] = qb.y; qv[6] = qb.z; qv[7] = qb.w;
+        // four passes at a time (all of one chunk): rows read first, then
+        // four independent chains
+        for (int c = 0; c < ncg; ++c) {
+            const int tn = min(kAttnChunk, n - (c0 + c) * kAttnChunk);
+            uint4 kw[4];
+            static_for<4>([&](auto j) {
+                const int t = (w + kIWaves * j) * 4 + grp;
+                kw[j] = *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]);
+            });
+            float pp[4];
+            static_for<4>([&](auto j) {
+                const uint32_t kk[4] = {kw[j].x, kw[j].y, kw[j].z, kw[j].w};
+                float a = 0.0f;
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int t = 16 * w + 4 * pass + grp;
-            const uint4 kw = *reinterpret_cast<const uint4*>(&buf.k[t * kD + l16 * 8]);
-            const uint32_t kk[4] = {kw.x, kw.y, kw.z, kw.w};
-            float pp = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                pp = __builtin_fmaf(qv[2 * j], f16_to_f32(uint16_t(kk[j])), pp);
-                pp = __builtin_fmaf(qv[2 * j + 1], f16_to_f32(uint16_t(kk[j] >> 16)), pp);
-            }
-            const float dot = row_tree_sum16(pp);
-            if (l16 == 0) S.as[t] = t < tn ? dot * scale : -__builtin_inff();
+                for (int i = 0; i < 4; ++i) {
+                    a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
+                    a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
+                }
+                pp[j] = a;
+            });
+            static_for<4>([&](auto j) { pp[j] = row_tree_sum16(pp[j]); });
+            if (l16 == 0)
+                static_for<4>([&](auto j) {
+                    const int t = (w + kIWaves * j) * 4 + grp;
+                    S.as[c * kAttnChunk + t] = t < tn ? pp[j] * scale : -__builtin_inff();
+                });
         }
     }
     ibar(bseq, budget, p.status);
     TRACE(l, 27);
-    const float sc = S.as[lane];
-    const float m = wave_max64_all(sc);
-    const float ex = (lane < tn) ? spec_expf(sc - m) : 0.0f;
-    const float ls = wave_tree_sum64_all(ex);
 
-    // o[d] = fmaf chain of e_t * v_t[d] over ascending t, dims 32w .. 32w+31
-    // (positions past the context have e_t = 0 and zero V rows: their fmaf
-    // returns the accumulator unchanged, bit for bit)
-    const int d = 32 * w + (lane & 31);
-    // V rows are read eight positions ahead of the chain that consumes them
-    float o = 0.0f;
+    // chunk partials: wave w, dims 64*(w&1) + lane of chunks w/2 and 2 + w/2
     {
-        constexpr int kB = 8;
-        uint16_t va[kB], vb[kB];
-        static_for<kB>([&](auto j) { va[j] = buf.v[j * kD + d]; });
-        static_for<kAttnChunk / kB>([&](auto bt) {
-            constexpr int t0 = bt * kB;
-            uint16_t* cur = (bt & 1) ? vb : va;
-            uint16_t* nxt = (bt & 1) ? va : vb;
-            if constexpr (t0 + kB < kAttnChunk)
-                static_for<kB>([&](auto j) { nxt[j] = buf.v[(t0 + kB + j) * kD + d]; });
-            __builtin_amdgcn_sched_barrier(0);
-            static_for<kB>([&](auto j) { o = __builtin_fmaf(lane_f(ex, t0 + j), f16_to_f32(cur[j]), o); });
-        });
+        const int ca = w >> 1, cb = 2 + (w >> 1);
+        const int d = (w & 1) * kD / 2 + lane;
+        if (ca < ncg) {
+            float ma, ea, la, mb = 0.0f, eb = 0.0f, lb = 0.0f;
+            chunk_softmax(ca, min(kAttnChunk, n - (c0 + ca) * kAttnChunk), ma, ea, la);
+            float oa = 0.0f, ob = 0.0f;
+            if (cb < ncg) {
+                chunk_softmax(cb, min(kAttnChunk, n - (c0 + cb) * kAttnChunk), mb, eb, lb);
+                v_chains<2>(&S.kv[ca].v[d], &S.kv[cb].v[d], ea, eb, oa, ob);
+                S.po[cb][d] = ob;
+                if ((w & 1) == 0 && lane == 0) { S.pm[cb] = mb; S.pl[cb] = lb; }
+            } else {
+                v_chains<1>(&S.kv[ca].v[d], nullptr, ea, 0.0f, oa, ob);
+            }
+            S.po[ca][d] = oa;
+            if ((w & 1) == 0 && lane == 0) { S.pm[ca] = ma; S.pl[ca] = la; }
+        }
     }
     TRACE(l, 28);
+    ibar(bseq, budget, p.status);
 
-    if (nc == 1) {
-        // combine over the single chunk: a = exp(m - M) with M = m
-        const float al = spec_expf(m - m);
-        const float L = __builtin_fmaf(al, ls, 0.0f);
-        const float O = __builtin_fmaf(al, o, 0.0f);
+    const int d = 32 * w + (lane & 31);   // combine: 32 dims per wave
+    if (ng == 1) {
+        // the head's chunks are all here: M = max m_c, then L and O over
+        // ascending chunks with a_c = exp(m_c - M)
+        float M = S.pm[0];
+        for (int c = 1; c < ncg; ++c) M = fmaxf(M, S.pm[c]);
+        float L = 0.0f, O = 0.0f;
+        for (int c = 0; c < ncg; ++c) {
+            const float al = spec_expf(S.pm[c] - M);
+            L = __builtin_fmaf(al, S.pl[c], L);
+            O = __builtin_fmaf(al, S.po[c][d], O);
+        }
         if (lane < 32) ll_store(p.ll_att + size_t(h) * kD + d, O * (1.0f / L), epoch_att);
     } else {
         constexpr int pstride = kD + 2;
         uint64_t* hp = p.ll_part + size_t(h) * size_t(p.max_chunks) * pstride;
-        uint64_t* cp = hp + size_t(c) * pstride;
-        if (w == 0 && lane == 0) {
-            ll_store(cp, m, epoch_att);
-            ll_store(cp + 1, ls, epoch_att);
+        if (w < ncg) {
+            // wave w publishes chunk w of the group
+            uint64_t* cp = hp + size_t(c0 + w) * pstride;
+            if (lane == 0) {
+                ll_store(cp, S.pm[w], epoch_att);
+                ll_store(cp + 1, S.pl[w], epoch_att);
+            }
+            ll_store(cp + 2 + lane, S.po[w][lane], epoch_att);
+            ll_store(cp + 2 + lane + 64, S.po[w][lane + 64], epoch_att);
         }
-        if (lane < 32) ll_store(cp + 2 + d, o, epoch_att);
         if (cur) {
             // M over all chunks: lane i watches chunk c0 + i of each group of 64
             const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(hp, nc * pstride * 8);
             unsigned spins = 0;
             float M = -__builtin_inff();
-            for (int c0 = 0; c0 < nc; c0 += kWave) {
-                const int cc = min(c0 + lane, nc - 1);
+            for (int b0 = 0; b0 < nc; b0 += kWave) {
+                const int cc = min(b0 + lane, nc - 1);
                 uint64_t em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
                 while (budget != 0) {
                     if (ll_ready(em, epoch_att)) break;
@@ -857,10 +992,10 @@ __device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly
             // L and O over ascending chunks, eight chunks' entries in flight
             // (their m entries have all arrived above)
             float L = 0.0f, O = 0.0f;
-            for (int c0 = 0; c0 < nc; c0 += 8) {
+            for (int b0 = 0; b0 < nc; b0 += 8) {
                 uint64_t em[8], el[8], eo[8];
                 static_for<8>([&](auto j) {
-                    const int cc = min(c0 + j, nc - 1);
+                    const int cc = min(b0 + j, nc - 1);
                     em[j] = ll_load(rp, 0u, (cc * pstride) * 8);
                     el[j] = ll_load(rp, 0u, (cc * pstride + 1) * 8);
                     eo[j] = ll_load(rp, uint32_t(d) * 8u, (cc * pstride + 2) * 8);
@@ -873,13 +1008,13 @@ __device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly
                     if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
                     compiler_fence();
                     static_for<8>([&](auto j) {
-                        const int cc = min(c0 + j, nc - 1);
+                        const int cc = min(b0 + j, nc - 1);
                         if (!ll_ready(el[j], epoch_att)) el[j] = ll_load(rp, 0u, (cc * pstride + 1) * 8);
                         if (!ll_ready(eo[j], epoch_att)) eo[j] = ll_load(rp, uint32_t(d) * 8u, (cc * pstride + 2) * 8);
                     });
                 }
                 static_for<8>([&](auto j) {
-                    if (c0 + j < nc) {
+                    if (b0 + j < nc) {
                         const float al = spec_expf(bits_f32(uint32_t(em[j])) - M);
                         L = __builtin_fmaf(al, bits_f32(uint32_t(el[j])), L);
                         O = __builtin_fmaf(al, bits_f32(uint32_t(eo[j])), O);
@@ -890,7 +1025,8 @@ __device__ void attention_item(const EngineParams& p, int kb, const hq_layer& Ly
         }
     }
     TRACE(l, 29);
-    // the item's LDS (K/V chunk, q, scores) may be reused once every wave is done
+    // the item's LDS (K/V chunks, q, scores, partials) may be reused once
+    // every wave is done
     ibar(bseq, budget, p.status);
 }
 
@@ -910,7 +1046,8 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
     const int nown = R.h1 - R.h0;
     const int n = pos + 1;
     const int nc = (n + kAttnChunk - 1) / kAttnChunk;
-    const int items = p.heads * nc;   // attention items: (query head, chunk)
+    const int ng = (nc + kGroup - 1) / kGroup;   // chunk groups per head
+    const int items = p.heads * ng;              // attention items: (query head, chunk group)
     const int NB = gridDim.x;
     const int b = blockIdx.x;
     int bseq = 0;   // input-barrier count
@@ -938,6 +1075,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
                 TRACE(l, 1);
                 poll_into<kHidNPT>(p.ll_x5, H, E, xin, budget, p.status);
             }
+            post_hs();
             TRACE(l, 2);
             const float act = rmsnorm_quant(xin, H, gin, p.eps, kQkvLPR * kQkvC * 32, bseq, budget, p.status, l, 37);
             post_xq(act);
@@ -945,17 +1083,16 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         }
         // this layer's attention K/V: copies start now and land while the
         // qkv hand-off travels
-        for (int it = b, k = 0; it < items && k < kKvBufs; it += NB, ++k)
-            prefetch_kv(p, l, (it / nc) / p.G, (it % nc) * kAttnChunk, n, pos, k);
+        if (b < items) prefetch_group(p, l, (b / ng) / p.G, (b % ng) * kGroup, min(kGroup, nc - (b % ng) * kGroup), n, pos);
         wait_lds_geq(&S.done, kWWaves * (g + 1), budget, p.status);
         TRACE(l, 4);
         publish_rows(p.ll_qkv + R.q0, R.q1 - R.q0, E + 1);
 
         // ---- P2: attention ------------------------------------------------------------
-        for (int it = b, k = 0; it < items; it += NB, ++k) {
-            const int kb = k < kKvBufs ? k : (k & 1);
-            if (k >= kKvBufs) prefetch_kv(p, l, (it / nc) / p.G, (it % nc) * kAttnChunk, n, pos, kb);
-            attention_item(p, kb, Ly, l, it / nc, it % nc, nc, n, pos, E + 1, E + 2, bseq, budget);
+        for (int it = b; it < items; it += NB) {
+            // a later item's copies start once the previous item is done with the buffers
+            if (it != b) prefetch_group(p, l, (it / ng) / p.G, (it % ng) * kGroup, min(kGroup, nc - (it % ng) * kGroup), n, pos);
+            attention_item(p, Ly, l, it / ng, it % ng, ng, nc, n, pos, E + 1, E + 2, bseq, budget);
         }
 
         // ---- P3: quant -> (o) -> residual ---------------------------------------------
@@ -967,6 +1104,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             ibar(bseq, budget, p.status);
             TRACE(l, 6);
             poll_into<kAttNPT>(p.ll_att, qd, E + 2, att, budget, p.status);
+            post_hs();
             load_gamma(Ly.post_norm, H, gpost);
             const float act = quantize(att, qd, kOLPR * kOC * 32, bseq, budget, p.status);
             post_xq(act);
@@ -986,6 +1124,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             ibar(bseq, budget, p.status);
             TRACE(l, 9);
             poll_into<kHidNPT>(p.ll_x3, H, E + 3, xp, budget, p.status);
+            post_hs();
             const float act = rmsnorm_quant(xp, H, gpost, p.eps, kGuLPR * kGuC * 32, bseq, budget, p.status, l, 32);
             post_xq(act);
             TRACE(l, 10);
@@ -1029,6 +1168,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             // the whole vector's bytes, one 4-byte word per entry
             float pk[kHidNPT];
             poll_into<kHidNPT>(p.ll_pk, I / 4, E + 4, pk, budget, p.status);
+            post_hs();
 #ifdef HQ_ENGINE_TRACE
             if (f32_bits(pk[0]) == 0x7fc00001u) S.red[0] = 0.0f;   // (trace: wait for the poll's data)
 #endif
@@ -1086,6 +1226,7 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         S.xq_seq = 0;
         S.done = 0;
         S.ibar = 0;
+        S.hs = 0;
     }
     __syncthreads();
     unsigned budget = 1;   // nonzero while this thread still waits (see kSpinLimit)

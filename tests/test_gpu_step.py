@@ -145,7 +145,7 @@ def test_qwen3_4b_first_tokens_bit_exact(qwen):
     st.check_status()
 
 
-@pytest.mark.parametrize("ctx", [300, 4000])
+@pytest.mark.parametrize("ctx", [100, 130, 300, 4000])
 def test_qwen3_4b_long_context_bit_exact(qwen, ctx):
     # an fp16 N(0,1) cache of `ctx` positions on both sides, then two steps
     model, ref = qwen
@@ -202,7 +202,7 @@ def test_tiny_model_layer_kernel_matches_per_layer_kernels(forward_golden):
     b.check_status()
 
 
-@pytest.mark.parametrize("ctx", [0, 300])
+@pytest.mark.parametrize("ctx", [0, 200, 300])
 def test_qwen3_4b_layer_kernel_matches_per_layer_kernels(qwen, ctx):
     model, _ = qwen
     assert model.layer_kernel_blocks > 0, "Qwen3-4B fits the persistent layer kernel"
