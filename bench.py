@@ -47,9 +47,11 @@ def parse():
     ap.add_argument("--gemv-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("decode", "gemv"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "gemv", "copy"), default="decode",
                     help="decode: configs[2] (the reported line); gemv: configs[0], one fused "
-                         "quant + int4 GEMV 2560 -> 9728 over rotating weight copies")
+                         "quant + int4 GEMV 2560 -> 9728 over rotating weight copies; copy: a "
+                         "plain 256 MiB device-to-device copy, the calibration kernel of the PMC "
+                         "traffic counters")
     return ap.parse_args()
 
 
@@ -246,6 +248,34 @@ def bench_gemv(args):
     print(json.dumps(result), flush=True)
 
 
+def bench_copy(args):
+    """Calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a plain copy
+    of 256 MiB (256 MiB read + 256 MiB written per dispatch), so a counter's
+    reading per dispatch divided into the known bytes gives its scale."""
+    import torch
+    nbytes = 256 << 20
+    dev = torch.device("cuda", 0)
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    reps = max(1, min(args.steps, 16))
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    gbs = 2 * nbytes / (us * 1e-6) / 1e9
+    print(json.dumps({"metric": "device copy GB/s (read + write), PMC calibration", "value": round(gbs, 1),
+                      "unit": "GB/s", "n_gpus": 1, "steps": reps, "warmup": 1, "bytes_read": nbytes,
+                      "bytes_written": nbytes, "us_per_copy": round(us, 2), "higher_is_better": True,
+                      "dtype": "int32", "data": "synthetic",
+                      "config": {"workload": "copy 256 MiB"}}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -254,6 +284,9 @@ def main():
         sys.exit(2)
     if args.workload == "gemv":
         bench_gemv(args)
+        return
+    if args.workload == "copy":
+        bench_copy(args)
         return
     import numpy as np
     import torch
