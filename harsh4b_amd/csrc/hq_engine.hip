@@ -65,7 +65,7 @@ constexpr unsigned kSpinLimit = 1u << 22;           // rounds one wait may spin
 // kTraceL0+3: input wave 0 at points 0-15, weight wave 0 at points 16-23,
 // attention (input wave 0) at points 24-31.
 constexpr int kTraceL0 = 16;
-constexpr int kTracePoints = 48;
+constexpr int kTracePoints = 96;   // 48-63: per-wave act polled, 64-79: per-wave xq written, 80-95: per-wave act phase entry
 constexpr int kTraceWords = 4 * kTracePoints;
 #endif
 
@@ -77,6 +77,7 @@ constexpr int kDownLPR = 64, kDownC = 5;         // K <= 10240, 1 row per wave
 // Phase inputs held in registers by the input threads.
 constexpr int kHidNPT = kMaxHidden / kIThreads;  // 10
 constexpr int kAttNPT = 16;                      // heads*D <= 4096
+constexpr int kActNPT = kMaxVec / kThreads;      // 10: SwiGLU entries per thread (all waves), I <= 10240
 
 }  // namespace eng
 
@@ -98,9 +99,7 @@ struct EngineParams {
     uint64_t* ll_x5;          // [H] x after down + residual
     uint64_t* ll_qkv;         // [qkv_rows]
     uint64_t* ll_att;         // [heads * D]
-    uint64_t* ll_act;         // [I]
-    uint64_t* ll_amax;        // [gridDim.x] max |act| of each block's rows
-    uint64_t* ll_pk;          // [I / 4] quantized act, 4 int8 per entry in S.xq's byte order
+    uint64_t* ll_act;         // [I] SwiGLU output
     uint32_t* epoch;
     uint64_t* ll_part;        // attention chunk partials [heads, max_chunks, D + 2] (m, l, o)
     int max_chunks;
@@ -139,10 +138,11 @@ struct Shared {
     float red[kIThreads];               // input-wave reductions
     float wmax[kIWaves];
     float act;                          // dequant multiplier of xq
-    int xq_seq;                         // input-wave xq posts, 4 per phase (input -> weight)
+    int xq_seq;                         // input-wave xq posts, 4 per GEMV input of P1/P3/P4 (input -> weight)
     int done;                           // weight-wave completions (weight -> input)
     int ibar;                           // input-wave barrier arrivals
     int hs;                             // hand-offs received by the input waves, 4 per phase
+    float amx[kWaves];                  // P5: each wave's max |SwiGLU output| of its entries
     KvBuf kv[kGroup];                   // K/V chunks of the block's attention item
     alignas(16) float aq[kD];           // attention: the normalized, rotated query head
     alignas(16) float as[kGroup * kAttnChunk];   // attention: the item's scores
@@ -292,7 +292,7 @@ __device__ __forceinline__ void watch_spread(const uint64_t* src, int n, uint32_
 // flight at once; while waiting, a thread re-reads the entries that are not
 // current yet (the caller has watched a spread sample of the vector first,
 // so the burst rarely needs a second round).
-template <int NPT>
+template <int NPT, int STRIDE = kIThreads>
 __device__ __forceinline__ void poll_into(const uint64_t* src, int n, uint32_t epoch, float (&out)[NPT],
                                           unsigned& budget, int32_t* status)
 {
@@ -300,19 +300,19 @@ __device__ __forceinline__ void poll_into(const uint64_t* src, int n, uint32_t e
     const __amdgpu_buffer_rsrc_t r = buffer_rsrc(src, n * 8);   // entries past n read as 0
     const uint32_t vo = uint32_t(t) * 8u;
     uint64_t v[NPT];
-    static_for<NPT>([&](auto j) { v[j] = ll_load(r, vo, j * kIThreads * 8); });
+    static_for<NPT>([&](auto j) { v[j] = ll_load(r, vo, j * STRIDE * 8); });
     unsigned spins = 0;
     while (budget != 0) {
         uint64_t pending = 0;
         static_for<NPT>([&](auto j) {
-            pending |= uint64_t(int(t + kIThreads * j < n) & int(!ll_ready(v[j], epoch))) << j;
+            pending |= uint64_t(int(t + STRIDE * j < n) & int(!ll_ready(v[j], epoch))) << j;
         });
         if (pending == 0) break;
         __builtin_amdgcn_s_sleep(1);
         if (++spins == kSpinLimit) { budget = 0; atomicOr(status, HQ_STEP_SYNC); }
         compiler_fence();
         static_for<NPT>([&](auto j) {
-            if ((pending >> j) & 1) v[j] = ll_load(r, vo, j * kIThreads * 8);
+            if ((pending >> j) & 1) v[j] = ll_load(r, vo, j * STRIDE * 8);
         });
     }
     static_for<NPT>([&](auto j) { out[j] = bits_f32(uint32_t(v[j])); });   // 0 past n
@@ -418,6 +418,53 @@ __device__ __forceinline__ void load_gamma(const float* g, int n, float (&out)[N
     static_for<NPT>([&](auto j) {
         out[j] = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(r, uint32_t(t) * 4u, j * kIThreads * 4, 0));
     });
+}
+
+// ---- P5 input, all sixteen waves ------------------------------------------------------
+//
+// The SwiGLU output arrives as fp32 hand-off entries (every block's rows).
+// Input wave 0 watches a spread sample of them; then every thread T of the
+// block reads entries T, T+1024, ..., the waves agree on the maximum |value|
+// through LDS, and each thread quantizes its own entries into S.xq.  The
+// weight waves hold only the down rows at this point (their loads have long
+// landed), so their polls do not queue behind weight loads.  Returns the
+// dequant multiplier amax/127 (the same in every wave).
+__device__ float act_phase(const EngineParams& p, int l, uint32_t epoch, unsigned& budget)
+{
+    const int T = opaque_tid();
+    const int w = T / kWave;
+    const int I = p.I;
+    // Every wave of the block calls this once per layer, so the block
+    // barriers below match up across the two roles.
+    if (w == 0) watch_spread(p.ll_act, I, epoch, budget, p.status);
+    __syncthreads();
+    if (w == 0) TRACE(l, 12);
+    if (w == kIWaves) TRACE(l, 15);
+    float a[kActNPT];
+    poll_into<kActNPT, kThreads>(p.ll_act, I, epoch, a, budget, p.status);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kActNPT; ++j) m = fmaxf(m, fabsf(a[j]));   // 0 past I
+    m = wave_max64_all(m);
+    if (lane_id() == 0) S.amx[w] = m;
+    __syncthreads();
+    if (w == 0) TRACE(l, 42);
+    if (w == kIWaves) TRACE(l, 30);
+    float amax = S.amx[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) amax = fmaxf(amax, S.amx[i]);
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+#pragma unroll
+    for (int j = 0; j < kActNPT; ++j) {
+        const int e = T + kThreads * j;
+        if (e < I) S.xq[xq_offset(e)] = uint8_t(quant_i8(a[j], inv));
+    }
+    for (int i = I + T; i < kDownLPR * kDownC * 32; i += kThreads) S.xq[i] = 0;
+    __syncthreads();
+    if (w == 0) TRACE(l, 44);
+    if (w == kIWaves) TRACE(l, 31);
+    return amax / 127.0f;
 }
 
 // ---- weight waves ---------------------------------------------------------------
@@ -565,7 +612,7 @@ __device__ __forceinline__ void load_window(int e, unsigned& budget, int32_t* st
     if constexpr (kLoadInWindows) wait_lds_geq(&S.hs, kIWaves * (e + 1), budget, status);
 }
 
-__device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsigned& budget)
+__device__ void weight_role(const EngineParams& p, const Rows& R, int ww, uint32_t base, unsigned& budget)
 {
     const int H = p.H, I = p.I;
     const int qd = p.heads * kD;
@@ -591,7 +638,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsign
         const hq_layer& Ly = S.lay[l];
         const hq_layer& Ln = S.lay[more ? l + 1 : l];
         // ---- P1: qkv
-        wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 1), budget, p.status);
+        wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 1), budget, p.status);
         if (ww == 0) TRACE(l, 16);
         {
             const float act = S.act;
@@ -606,7 +653,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsign
         load_window(4 * l + 1, budget, p.status);
         load_pairs(wg, sg, Ly.gate_up, Ly.gate_up_scales, R.g0, R.g1, I, H, ww);
         // ---- P3: o (the residual add is the input waves')
-        wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 2), budget, p.status);
+        wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 2), budget, p.status);
         if (ww == 0) TRACE(l, 18);
         if (ww == kWWaves - 1) TRACE(l, 45);
         {
@@ -620,7 +667,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsign
         load_window(4 * l + 2, budget, p.status);
         load_rows<kDownLPR, kDownC, kPaceDown>(wd, sd, Ly.down, Ly.down_scales, R.h0, R.h1, I, ww);
         // ---- P4: gate_up + SwiGLU
-        wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 3), budget, p.status);
+        wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 3), budget, p.status);
         if (ww == 0) TRACE(l, 20);
         {
             const float act = S.act;
@@ -647,14 +694,13 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, unsign
         // (after the last layer the same loads, all of one 16-byte block:
         // the instruction sequence, and so every dot's wait, is the same on
         // every path)
-        load_window(4 * l + 3, budget, p.status);
+        // ---- P5: down (the residual add is the input waves')
+        const float act5 = act_phase(p, l, base + 5u * uint32_t(l) + 4u, budget);
         load_rows<kQkvLPR, kQkvC, kPaceQkv>(wq, sq, Ln.qkv, Ln.qkv_scales, R.q0, more ? R.q1 : R.q0 + 1,
                                             more ? H : 32, ww);
-        // ---- P5: down (the residual add is the input waves')
-        wait_lds_geq(&S.xq_seq, kIWaves * (4 * l + 4), budget, p.status);
         if (ww == 0) TRACE(l, 22);
         {
-            const float act = S.act;
+            const float act = act5;
             const int acc = rows_acc<kDownLPR, 0, 1>(reg_dot<kDownLPR, kDownC>(wd, S.xq));
             if (has_o && lane == 0) S.res[ww] = (float(acc) * act) * sd;
         }
@@ -1052,8 +1098,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
     const int b = blockIdx.x;
     int bseq = 0;   // input-barrier count
     float xown = t0 < nown ? p.x[R.h0 + t0] : 0.0f;
-    float gin[kHidNPT];
-    load_gamma(S.lay[0].input_norm, H, gin);
 
 #pragma unroll 1
     for (int l = 0; l < p.L; ++l) {
@@ -1065,6 +1109,8 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         // ---- P1: RMSNorm(input) -> quant -> (qkv) -------------------------------------
         TRACE(l, 0);
         {
+            float gin[kHidNPT];
+            load_gamma(Ly.input_norm, H, gin);
             float xin[kHidNPT];
             if (l == 0) {
 #pragma unroll
@@ -1131,58 +1177,17 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         }
         wait_lds_geq(&S.done, kWWaves * (g + 3), budget, p.status);
         TRACE(l, 11);
-        // The SwiGLU output is handed on quantized: first every block's
-        // max |value| (the vector's absmax is their maximum), then each
-        // block's own values as int8, four to an entry.
+        // The SwiGLU output is handed on as fp32 values: every block reads
+        // the whole vector, takes its maximum |value| (order-free) and
+        // quantizes it into its own S.xq, so one hand-off carries both the
+        // act scale and the down GEMV's input.
         const int na = R.g1 - R.g0;
-        float av = 0.0f;   // this thread's SwiGLU output (threads t < na)
-        if (t < kWave) {
-            av = t < na ? S.res[t] : 0.0f;
-            const float bm = wave_max64_all(fabsf(av));
-            if (t == 0) ll_store(p.ll_amax + b, bm, E + 4);
-        }
+        if (t < na) ll_store(p.ll_act + R.g0 + t, S.res[t], E + 4);
 
-        // ---- P5: quant -> (down) -> residual ------------------------------------------
-        {
-            float bm[1];
-            poll_into<1>(p.ll_amax, NB, E + 4, bm, budget, p.status);
-            TRACE(l, 12);
-            const float amax = fmaxf(inputs_max(bm[0], bseq, budget, p.status), 1e-5f);
-            const float inv = 127.0f / amax;
-            if (t < kWave) {
-                // This block's values, quantized, as the bytes of S.xq they
-                // occupy: entry k of the block holds xq bytes 4k .. 4k+3 of
-                // its rows, i.e. rows 8m+p, 8m+p+2, 8m+p+4, 8m+p+6 (m = k/2,
-                // p = k%2: even rows first, then odd, per group of 8).
-                const uint32_t q = uint32_t(uint8_t(quant_i8(av, inv)));
-                const int k = lane_id() & 15;
-                const int r0 = 8 * (k >> 1) + (k & 1);
-                const uint32_t b0 = __builtin_amdgcn_ds_bpermute(r0 * 4, q);
-                const uint32_t b1 = __builtin_amdgcn_ds_bpermute((r0 + 2) * 4, q);
-                const uint32_t b2 = __builtin_amdgcn_ds_bpermute((r0 + 4) * 4, q);
-                const uint32_t b3 = __builtin_amdgcn_ds_bpermute((r0 + 6) * 4, q);
-                const uint32_t packed = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-                if (t < na / 4) ll_store(p.ll_pk + R.g0 / 4 + t, bits_f32(packed), E + 4);
-            }
-            TRACE(l, 42);
-            // the whole vector's bytes, one 4-byte word per entry
-            float pk[kHidNPT];
-            poll_into<kHidNPT>(p.ll_pk, I / 4, E + 4, pk, budget, p.status);
-            post_hs();
-#ifdef HQ_ENGINE_TRACE
-            if (f32_bits(pk[0]) == 0x7fc00001u) S.red[0] = 0.0f;   // (trace: wait for the poll's data)
-#endif
-            TRACE(l, 43);
-            static_for<kHidNPT>([&](auto j) {
-                const int e = t + kIThreads * j;
-                if (e < I / 4) reinterpret_cast<uint32_t*>(S.xq)[e] = f32_bits(pk[j]);
-            });
-            for (int i = I + t; i < kDownLPR * kDownC * 32; i += kIThreads) S.xq[i] = 0;
-            TRACE(l, 44);
-            if (l + 1 < p.L) load_gamma(S.lay[l + 1].input_norm, H, gin);
-            TRACE(l, 13);
-            post_xq(amax / 127.0f);
-        }
+        // ---- P5: quant (all waves) -> (down) -> residual --------------------------------
+        act_phase(p, l, E + 4, budget);
+        post_hs();
+        TRACE(l, 13);
         wait_lds_geq(&S.done, kWWaves * (g + 4), budget, p.status);
         TRACE(l, 14);
         if (t < nown) {
@@ -1235,7 +1240,7 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     for (int i = tid; i < kTraceWords; i += kThreads) S.trace[i] = 0;
     __syncthreads();
 #endif
-    if (wave >= kIWaves) weight_role(p, R, wave - kIWaves, budget);
+    if (wave >= kIWaves) weight_role(p, R, wave - kIWaves, base, budget);
     else input_role(p, R, pos, base, budget);
 #ifdef HQ_ENGINE_TRACE
     __syncthreads();
@@ -1255,7 +1260,7 @@ bool engine_fits(const hq_model* m)
     if (m->layers > kMaxLayers) return false;
     const int H = m->hidden, I = m->intermediate, qd = m->heads * kD;
     if (H > kMaxHidden || I > kMaxVec || qd > kMaxVec) return false;
-    if (H > kIThreads * kHidNPT || qd > kIThreads * kAttNPT || I / 4 > kIThreads * kHidNPT) return false;
+    if (H > kIThreads * kHidNPT || qd > kIThreads * kAttNPT || I > kThreads * kActNPT) return false;
     if (I % 8) return false;   // SwiGLU rows are handed on in groups of 8
     if ((H >> 5) > kQkvLPR * kQkvC || (H >> 5) > kGuLPR * kGuC) return false;
     if ((qd >> 5) > kOLPR * kOC || (I >> 5) > kDownLPR * kDownC) return false;
@@ -1280,7 +1285,6 @@ int engine_blocks(const hq_model* m)
     if (cus[dev] <= 0) return 0;
     const int qrows = m->heads * kD + 2 * m->kv_heads * kD;
     int nb = min(min(cus[dev], m->hidden), min(qrows, m->intermediate / 8));
-    nb = min(nb, kIThreads);   // the block maxima are polled one per input thread
     // per-block capacities of the weight waves and the residual rows
     auto ceil_div = [](int a, int b) { return (a + b - 1) / b; };
     if (ceil_div(qrows, nb) > kWWaves * (kWave / kQkvLPR) || ceil_div(m->hidden, nb) > kWWaves ||
@@ -1304,8 +1308,7 @@ size_t engine_ll_entries(const hq_model* m)
 {
     const int qd = m->heads * m->head_dim;
     const int qrows = qd + 2 * m->kv_heads * m->head_dim;
-    return size_t(2 * m->hidden) + size_t(qrows) + size_t(qd) + size_t(m->intermediate) +
-           size_t(eng::kIThreads) + size_t(m->intermediate / 4);
+    return size_t(2 * m->hidden) + size_t(qrows) + size_t(qd) + size_t(m->intermediate);
 }
 
 hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, uint32_t* epoch,
@@ -1337,8 +1340,6 @@ hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, ui
     p.ll_qkv = p.ll_x5 + m->hidden;
     p.ll_att = p.ll_qkv + p.qkv_rows;
     p.ll_act = p.ll_att + qd;
-    p.ll_amax = p.ll_act + m->intermediate;
-    p.ll_pk = p.ll_amax + eng::kIThreads;
     p.epoch = epoch;
     p.ll_part = part;
     p.max_chunks = max_chunks;
