@@ -42,16 +42,19 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--ctx", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=None,
+                    help="context before the timed decode (default 64; 4096 for --workload long)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--gemv-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("decode", "gemv", "copy"), default="decode",
-                    help="decode: configs[2] (the reported line); gemv: configs[0], one fused "
-                         "quant + int4 GEMV 2560 -> 9728 over rotating weight copies; copy: a "
-                         "plain 256 MiB device-to-device copy, the calibration kernel of the PMC "
-                         "traffic counters")
+    ap.add_argument("--workload", choices=("decode", "long", "batched", "gemv", "copy"), default="decode",
+                    help="decode: configs[2] (the reported line); long: configs[4], the same decode "
+                         "at context 4096 over an N(0,1) fp16 KV cache; batched: configs[3], the "
+                         "body GEMMs of M = 8/16/32 sequences on int8 MFMA against M GEMVs; gemv: "
+                         "configs[0], one fused quant + int4 GEMV 2560 -> 9728 over rotating weight "
+                         "copies; copy: a plain 256 MiB device-to-device copy, the calibration kernel "
+                         "of the PMC traffic counters")
     return ap.parse_args()
 
 
@@ -248,6 +251,98 @@ def bench_gemv(args):
     print(json.dumps(result), flush=True)
 
 
+def bench_batched(args):
+    """the body GEMMs of one decode step for M = 8, 16 and 32
+    concurrent sequences (fused per-sequence quant + int4 x int8 GEMM on MFMA,
+    hq_quant_int4_gemm), 36 layers x (qkv, o, gate_up, down) with distinct
+    weights, against the same work as M batch-1 fused GEMVs (hq_quant_int4_gemv)
+    per sequence.  Each GEMM reads a layer's weights once for all M
+    sequences; value = sequences x steps per second of the body GEMMs at
+    M = 32 (the GEMM's roofline is HBM: weights once per step)."""
+    import torch
+    from harsh4b_amd.config import QWEN3_4B, body_bytes, shapes
+    from harsh4b_amd.lightspark import quant_int4_gemm, quant_int4_gemv
+    from harsh4b_amd.synthetic import random_model
+    cfg = QWEN3_4B
+    dev = torch.device("cuda", 0)
+    print(f"# building random Qwen3-4B int4 model (seed {args.seed})", file=sys.stderr, flush=True)
+    model = random_model(cfg, seed=args.seed)
+    sh = shapes(cfg)
+    L = int(cfg["num_hidden_layers"])
+    wbytes = body_bytes(cfg) + 4 * L * sum(r for r, _ in sh.values())
+    macs = L * sum(r * w for r, w in sh.values())
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    reps = max(2, min(args.gemv_reps, 20))
+
+    def timed(fn):
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+        with torch.cuda.stream(s):
+            g.replay()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    per_m = {}
+    for m in (8, 16, 32):
+        xs = {name: torch.randn((m, w), generator=gen, device=dev, dtype=torch.float32)
+              for name, (r, w) in sh.items()}
+        outs = {name: torch.empty((m, r), device=dev, dtype=torch.float32) for name, (r, w) in sh.items()}
+
+        def gemm_body():
+            for layer in model.layers:
+                for name in sh:
+                    quant_int4_gemm(xs[name], getattr(layer, name), out=outs[name], stream=s)
+
+        ms = timed(gemm_body)
+        gbs = wbytes / (ms * 1e-3) / 1e9
+        tops = 2 * m * macs / (ms * 1e-3) / 1e12
+        per_m[m] = {"us_per_step": round(ms * 1e3, 1), "seq_steps_per_s": round(m / (ms * 1e-3), 1),
+                    "weight_GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "int8_TOP/s": round(tops, 2), "mfma_frac": round(tops / 5000.0, 5)}
+        print(f"# M={m}: body GEMMs {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s of weights, {tops:.1f} TOP/s",
+              file=sys.stderr, flush=True)
+    # the GEMV alternative: one sequence's body GEMVs (M sequences cost M times this)
+    xv = {name: torch.randn(w, generator=gen, device=dev, dtype=torch.float32) for name, (r, w) in sh.items()}
+    ov = {name: torch.empty(r, device=dev, dtype=torch.float32) for name, (r, w) in sh.items()}
+
+    def gemv_body():
+        for layer in model.layers:
+            for name in sh:
+                quant_int4_gemv(xv[name], getattr(layer, name), out=ov[name], stream=s)
+
+    gemv_ms = timed(gemv_body)
+    print(f"# M=1 GEMVs: {gemv_ms * 1e3:.1f} us/step", file=sys.stderr, flush=True)
+    for m in per_m:
+        per_m[m]["gemv_us_per_step_for_M"] = round(m * gemv_ms * 1e3, 1)
+        per_m[m]["speedup_vs_M_gemvs"] = round(m * gemv_ms * 1e3 / per_m[m]["us_per_step"], 2)
+    top = per_m[32]
+    result = {"metric": "batched body GEMM sequence-steps/s (configs[3], M=32)", "value": top["seq_steps_per_s"],
+              "unit": "sequence-steps/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+              "ms_per_step": round(top["us_per_step"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+              "vs_baseline": None, "dtype": "int8", "data": "synthetic: random-init int4 weights, N(0,1) inputs",
+              "config": {"workload": "configs[3]: body GEMMs (36 layers x qkv, o, gate_up, down) of one decode "
+                                     "step for M = 8/16/32 sequences, int8 MFMA vs M batch-1 GEMVs"},
+              "roofline": {"kernel": "gemm_mfma_kernel (M=32)", "bound": "hbm", "achieved": top["weight_GB/s"],
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": top["hbm_frac"], "traffic": None,
+                           "algorithmic_bytes": wbytes},
+              "per_m": per_m, "gemv_m1_us_per_step": round(gemv_ms * 1e3, 1)}
+    print(json.dumps(result), flush=True)
+
+
 def bench_copy(args):
     """Calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a plain copy
     of 256 MiB (256 MiB read + 256 MiB written per dispatch), so a counter's
@@ -288,6 +383,9 @@ def main():
     if args.workload == "copy":
         bench_copy(args)
         return
+    if args.workload == "batched":
+        bench_batched(args)
+        return
     import numpy as np
     import torch
     from harsh4b_amd import _native
@@ -296,15 +394,31 @@ def main():
 
     cfg = QWEN3_4B
     lib = _native.lib()
+    long_ctx = args.workload == "long"
+    if args.ctx is None:
+        args.ctx = 4096 if long_ctx else 64
     print(f"# building random Qwen3-4B int4 model (seed {args.seed})", file=sys.stderr, flush=True)
     model = random_model(cfg, seed=args.seed)
     cap = args.ctx + args.warmup + args.steps + 4
     state = model.new_state(cap)
-    prompt = np.random.default_rng(3).integers(0, int(cfg["vocab_size"]), args.ctx)
-    for t in prompt:
-        model.forward_token(int(t), state)
-    state.synchronize()
-    print(f"# prefilled {args.ctx} tokens", file=sys.stderr, flush=True)
+    if long_ctx:
+        # the first ctx positions of every layer's cache hold
+        # N(0,1) keys and values (fp16); decoding starts at position ctx
+        gen = torch.Generator(device=state.keys.device)
+        gen.manual_seed(5)
+        for cache in (state.keys, state.values):
+            cache[:, :args.ctx].normal_(generator=gen)
+        state.device_position.fill_(args.ctx)
+        state.position = args.ctx
+        state.token.fill_(1000)
+        torch.cuda.synchronize()
+        print(f"# filled {args.ctx} cache positions with N(0,1)", file=sys.stderr, flush=True)
+    else:
+        prompt = np.random.default_rng(3).integers(0, int(cfg["vocab_size"]), args.ctx)
+        for t in prompt:
+            model.forward_token(int(t), state)
+        state.synchronize()
+        print(f"# prefilled {args.ctx} tokens", file=sys.stderr, flush=True)
 
     model.decode_greedy(state, args.warmup)          # captures the step graph
     state.synchronize()
@@ -359,8 +473,10 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic: random-init int4 weights, random prompt token ids",
-        "config": {"workload": "configs[2]: 36-layer Qwen3-4B-shaped int4 decode, batch 1, "
-                               f"context {args.ctx}, greedy, fp16 KV cache",
+        "config": {"workload": (f"configs[4]: 36-layer Qwen3-4B-shaped int4 decode, batch 1, context "
+                                f"{args.ctx} (N(0,1) fp16 KV cache), greedy" if long_ctx else
+                                "configs[2]: 36-layer Qwen3-4B-shaped int4 decode, batch 1, "
+                                f"context {args.ctx}, greedy, fp16 KV cache"),
                    "global_batch": 1, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "engine_kernel (persistent layer kernel: 36 decoder layers)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
