@@ -228,6 +228,42 @@ __device__ __forceinline__ int read_i(const int* p)
 // Wait until every memory operation this thread issued has completed.
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
+// A pointer every lane holds the same value of, as a scalar (SGPR) value:
+// loads through it take a 32-bit per-lane offset.
+template <class T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+    return reinterpret_cast<const T*>((uint64_t(hi) << 32) | lo);
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+    return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// One 16-byte global->LDS copy per active lane (gfx950 global_load_lds_dwordx4):
+// lane i reads base + off (base the same in every lane) and writes LDS bytes
+// lds + 16*i .. +15 (lds the same in every lane).  Written as asm (the
+// compiler's own tracking of this instruction would make unrelated later
+// instructions wait for it); the data may be read once the wave's memory
+// operations have been waited for (wait_all_memory) and, for other waves,
+// after a barrier.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds)
+{
+    const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+    const void* ub = uniform_ptr(base);
+    uint32_t saved;   // m0 is reserved to the compiler: restore it
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %2, %3\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(m), "v"(off), "s"(ub)
+                 : "memory");
+}
+
 constexpr int kTicketGroup = 32;   // blocks per first-level ticket counter
 
 // Two-level arrival ticket for `nblocks` blocks, called by one thread per

@@ -170,17 +170,6 @@ __device__ __forceinline__ int opaque_tid()
 }
 __device__ __forceinline__ int lane_id() { return opaque_tid() & (kWave - 1); }
 
-// A pointer every lane holds the same value of, as a scalar (SGPR) value:
-// loads through it take a 32-bit per-lane offset.
-template <class T>
-__device__ __forceinline__ const T* uniform_ptr(const T* p)
-{
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
-    return reinterpret_cast<const T*>((uint64_t(hi) << 32) | lo);
-}
-
 __device__ __forceinline__ int lds_load(const int* p)
 {
     return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -719,27 +708,6 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, uint32
 // attention_kernel's STEP mode in hq_attention.hip).  The chunk's K and V
 // rows are copied from HBM into LDS with gfx950's global->LDS loads before
 // the qkv hand-off is awaited, so they arrive while it travels.
-
-// One 16-byte global->LDS load per lane from base + off (base uniform) into
-// lds + 16*lane.  Written as asm (the compiler's own tracking of this
-// instruction would make unrelated later instructions wait for it); the data
-// is read only after the wave's memory operations have been waited for and
-// the input waves have met at a barrier.
-__device__ __forceinline__ uint32_t lds_addr(const void* p)
-{
-    return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
-}
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds)
-{
-    const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
-    const void* ub = uniform_ptr(base);
-    uint32_t saved;   // m0 is reserved to the compiler: restore it
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
-                 "global_load_lds_dwordx4 %2, %3\n\ts_nop 0\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "s"(m), "v"(off), "s"(ub)
-                 : "memory");
-}
 
 // Copies K and V rows [t0, t0 + 64) of kv head kvh into S.kv[kb]: rows
 // before the current position from the cache, rows after it as zeros; the

@@ -116,7 +116,8 @@ int hq_int4_i8_gemm(const int8_t* x, const float* act_scales, const uint8_t* wei
                     int32_t* acc_out, void* workspace, void* stream);
 /* Fused form: per-sequence quantization of fp32 x [m, width] (the A3 spec
  * applied to each row), then the GEMM.  q_out int8 [m, width] and
- * act_scales_out fp32 [m] are optional outputs. */
+ * act_scales_out fp32 [m] are optional outputs.  Here width <= 10240, x is
+ * 16-byte aligned and q_out (when given) 8-byte aligned. */
 int hq_quant_int4_gemm(const float* x, const uint8_t* weights, const float* scales,
                        float* output, int m, int rows, int width, int8_t* q_out,
                        float* act_scales_out, int32_t* acc_out, void* workspace,
