@@ -602,7 +602,10 @@ __device__ __forceinline__ void load_window(int e, unsigned& budget, int32_t* st
     if constexpr (kLoadInWindows) wait_lds_geq(&S.hs, kIWaves * (e + 1), budget, status);
 }
 
-__device__ void weight_role(const EngineParams& p, const Rows& R, int ww, uint32_t base, unsigned& budget)
+__device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, uint32_t epoch_qkv,
+                                unsigned& budget);
+
+__device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int pos, uint32_t base, unsigned& budget)
 {
     const int H = p.H, I = p.I;
     const int qd = p.heads * kD;
@@ -640,6 +643,8 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, uint32
         post_done();
         if (ww == 0) TRACE(l, 17);
         if (ww == kWWaves - 1) TRACE(l, 47);
+        // ---- P2: the block's attention items (all waves)
+        attention_phase(p, Ly, l, pos, base + 5u * uint32_t(l) + 1u, budget);
         load_window(4 * l + 1, budget, p.status);
         load_pairs(wg, sg, Ly.gate_up, Ly.gate_up_scales, R.g0, R.g1, I, H, ww);
         // ---- P3: o (the residual add is the input waves')
@@ -798,10 +803,9 @@ __device__ __forceinline__ void chunk_softmax(int c, int tn, float& m, float& ex
 // chunks of the head in ascending order as they arrive.  Same arithmetic as
 // attention_kernel's STEP mode (hq_attention.hip).
 __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l, int h, int g, int ng, int nc,
-                               int n, int pos, uint32_t epoch_qkv, uint32_t epoch_att, int& bseq,
-                               unsigned& budget)
+                               int n, int pos, uint32_t epoch_qkv, uint32_t epoch_att, unsigned& budget)
 {
-    const int w = threadIdx.x / kWave;
+    const int w = opaque_tid() / kWave;
     const int lane = lane_id();
     const int G = p.G;
     const int kvh = h / G;
@@ -847,7 +851,7 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             if (!ll_ready(ev0, epoch_qkv)) ev0 = ll_load(rq, vo, sv_);
             if (!ll_ready(ev1, epoch_qkv)) ev1 = ll_load(rq, vo, sv_ + 512);
         }
-        TRACE(l, 25);
+        if (w == 0) TRACE(l, 25);
         {
             // per-head RMSNorm + RoPE of q (as attention_kernel's STEP prologue)
             const float x0 = bits_f32(uint32_t(eq0)), x1 = bits_f32(uint32_t(eq1));
@@ -890,76 +894,70 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             }
         }
     }
-    // every wave's K/V copies have landed, q and the current row are in place
-    wait_all_memory();
-    ibar(bseq, budget, p.status);
-    TRACE(l, 26);
+    // the input waves' K/V copies have landed (they issued them), q and the
+    // current row are in place
+    if (w < kIWaves) wait_all_memory();
+    __syncthreads();
+    if (w == 0) TRACE(l, 26);
 
     // scores: pass P of a chunk covers its positions 4P .. 4P+3, 16 lanes
-    // per position (8 dims each); wave w takes passes w, w+4, w+8, w+12
+    // per position (8 dims each); wave w takes pass w of every chunk (the
+    // rows of all chunks read first, then one independent chain per chunk)
     {
         const float scale = 1.0f / __builtin_sqrtf(float(kD));
         const int l16 = lane & 15;
         const int grp = lane >> 4;
+        const int t = w * 4 + grp;
         float qv[8];
         const float4 qa = *reinterpret_cast<const float4*>(&S.aq[l16 * 8]);
         const float4 qb = *reinterpret_cast<const float4*>(&S.aq[l16 * 8 + 4]);
         qv[0] = qa.x; qv[1] = qa.y; qv[2] = qa.z; qv[3] = qa.w;
         qv[4] = qb.x; qv[5] = qb.y; qv[6] = qb.z; qv[7] = qb.w;
-        // four passes at a time (all of one chunk): rows read first, then
-        // four independent chains
-        for (int c = 0; c < ncg; ++c) {
-            const int tn = min(kAttnChunk, n - (c0 + c) * kAttnChunk);
-            uint4 kw[4];
-            static_for<4>([&](auto j) {
-                const int t = (w + kIWaves * j) * 4 + grp;
-                kw[j] = *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]);
-            });
-            float pp[4];
-            static_for<4>([&](auto j) {
-                const uint32_t kk[4] = {kw[j].x, kw[j].y, kw[j].z, kw[j].w};
-                float a = 0.0f;
+        uint4 kw[kGroup];
+        static_for<kGroup>([&](auto c) {
+            kw[c] = c < ncg ? *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]) : make_uint4(0, 0, 0, 0);
+        });
+        float pp[kGroup];
+        static_for<kGroup>([&](auto c) {
+            const uint32_t kk[4] = {kw[c].x, kw[c].y, kw[c].z, kw[c].w};
+            float a = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
-                    a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
-                }
-                pp[j] = a;
-            });
-            static_for<4>([&](auto j) { pp[j] = row_tree_sum16(pp[j]); });
-            if (l16 == 0)
-                static_for<4>([&](auto j) {
-                    const int t = (w + kIWaves * j) * 4 + grp;
-                    S.as[c * kAttnChunk + t] = t < tn ? pp[j] * scale : -__builtin_inff();
-                });
-        }
-    }
-    ibar(bseq, budget, p.status);
-    TRACE(l, 27);
-
-    // chunk partials: wave w, dims 64*(w&1) + lane of chunks w/2 and 2 + w/2
-    {
-        const int ca = w >> 1, cb = 2 + (w >> 1);
-        const int d = (w & 1) * kD / 2 + lane;
-        if (ca < ncg) {
-            float ma, ea, la, mb = 0.0f, eb = 0.0f, lb = 0.0f;
-            chunk_softmax(ca, min(kAttnChunk, n - (c0 + ca) * kAttnChunk), ma, ea, la);
-            float oa = 0.0f, ob = 0.0f;
-            if (cb < ncg) {
-                chunk_softmax(cb, min(kAttnChunk, n - (c0 + cb) * kAttnChunk), mb, eb, lb);
-                v_chains<2>(&S.kv[ca].v[d], &S.kv[cb].v[d], ea, eb, oa, ob);
-                S.po[cb][d] = ob;
-                if ((w & 1) == 0 && lane == 0) { S.pm[cb] = mb; S.pl[cb] = lb; }
-            } else {
-                v_chains<1>(&S.kv[ca].v[d], nullptr, ea, 0.0f, oa, ob);
+            for (int i = 0; i < 4; ++i) {
+                a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
+                a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
             }
-            S.po[ca][d] = oa;
-            if ((w & 1) == 0 && lane == 0) { S.pm[ca] = ma; S.pl[ca] = la; }
-        }
+            pp[c] = a;
+        });
+        static_for<kGroup>([&](auto c) { pp[c] = row_tree_sum16(pp[c]); });
+        if (l16 == 0)
+            static_for<kGroup>([&](auto c) {
+                if (c < ncg) {
+                    const int tn = min(kAttnChunk, n - (c0 + c) * kAttnChunk);
+                    S.as[c * kAttnChunk + t] = t < tn ? pp[c] * scale : -__builtin_inff();
+                }
+            });
     }
-    TRACE(l, 28);
-    ibar(bseq, budget, p.status);
+    __syncthreads();
+    if (w == 0) TRACE(l, 27);
 
+    // chunk partials: wave w < 2*ncg takes dims 64*(w&1) + lane of chunk w/2
+    // and computes the chunk's softmax terms itself (same operations on the
+    // same values in both waves of a chunk, same bits)
+    if (w < 2 * ncg) {
+        const int ca = w >> 1;
+        const int d = (w & 1) * kD / 2 + lane;
+        float ma, ea, la;
+        chunk_softmax(ca, min(kAttnChunk, n - (c0 + ca) * kAttnChunk), ma, ea, la);
+        float oa = 0.0f, ob = 0.0f;
+        v_chains<1>(&S.kv[ca].v[d], nullptr, ea, 0.0f, oa, ob);
+        S.po[ca][d] = oa;
+        if ((w & 1) == 0 && lane == 0) { S.pm[ca] = ma; S.pl[ca] = la; }
+    }
+    if (w == 0) TRACE(l, 28);
+    __syncthreads();
+
+    // combine (input waves): 32 dims per wave
+    if (w < kIWaves) {
     const int d = 32 * w + (lane & 31);   // combine: 32 dims per wave
     if (ng == 1) {
         // the head's chunks are all here: M = max m_c, then L and O over
@@ -1039,10 +1037,31 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             if (lane < 32) ll_store(p.ll_att + size_t(h) * kD + d, O * (1.0f / L), epoch_att);
         }
     }
-    TRACE(l, 29);
+    }
+    if (w == 0) TRACE(l, 29);
     // the item's LDS (K/V chunks, q, scores, partials) may be reused once
     // every wave is done
-    ibar(bseq, budget, p.status);
+    __syncthreads();
+}
+
+// All attention items of a layer for this block, run by all sixteen waves
+// (the weight waves join after their qkv dots; every wave executes the same
+// barriers).  Items are (query head, group of up to kGroup chunks); the
+// input waves copy each item's K/V chunks, the block's first item's copies
+// having been started in P1.
+__device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, uint32_t epoch_qkv,
+                                unsigned& budget)
+{
+    const int n = pos + 1;
+    const int nc = (n + kAttnChunk - 1) / kAttnChunk;
+    const int ng = (nc + kGroup - 1) / kGroup;
+    const int items = p.heads * ng;
+    const int b = blockIdx.x;
+    for (int it = b; it < items; it += gridDim.x) {
+        if (it != b && opaque_tid() < kIThreads)
+            prefetch_group(p, l, (it / ng) / p.G, (it % ng) * kGroup, min(kGroup, nc - (it % ng) * kGroup), n, pos);
+        attention_item(p, Ly, l, it / ng, it % ng, ng, nc, n, pos, epoch_qkv, epoch_qkv + 1u, budget);
+    }
 }
 
 // Publish the weight waves' results res[0, n) to dst (input threads t < n).
@@ -1063,7 +1082,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
     const int nc = (n + kAttnChunk - 1) / kAttnChunk;
     const int ng = (nc + kGroup - 1) / kGroup;   // chunk groups per head
     const int items = p.heads * ng;              // attention items: (query head, chunk group)
-    const int NB = gridDim.x;
     const int b = blockIdx.x;
     int bseq = 0;   // input-barrier count
     float xown = t0 < nown ? p.x[R.h0 + t0] : 0.0f;
@@ -1104,11 +1122,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         publish_rows(p.ll_qkv + R.q0, R.q1 - R.q0, E + 1);
 
         // ---- P2: attention ------------------------------------------------------------
-        for (int it = b; it < items; it += NB) {
-            // a later item's copies start once the previous item is done with the buffers
-            if (it != b) prefetch_group(p, l, (it / ng) / p.G, (it % ng) * kGroup, min(kGroup, nc - (it % ng) * kGroup), n, pos);
-            attention_item(p, Ly, l, it / ng, it % ng, ng, nc, n, pos, E + 1, E + 2, bseq, budget);
-        }
+        attention_phase(p, Ly, l, pos, E + 1, budget);
 
         // ---- P3: quant -> (o) -> residual ---------------------------------------------
         float gpost[kHidNPT];
@@ -1209,7 +1223,7 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     for (int i = tid; i < kTraceWords; i += kThreads) S.trace[i] = 0;
     __syncthreads();
 #endif
-    if (wave >= kIWaves) weight_role(p, R, wave - kIWaves, base, budget);
+    if (wave >= kIWaves) weight_role(p, R, wave - kIWaves, pos, base, budget);
     else input_role(p, R, pos, base, budget);
 #ifdef HQ_ENGINE_TRACE
     __syncthreads();
