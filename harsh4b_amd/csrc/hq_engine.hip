@@ -78,6 +78,10 @@ constexpr int kDownLPR = 64, kDownC = 5;         // K <= 10240, 1 row per wave
 constexpr int kHidNPT = kMaxHidden / kIThreads;  // 10
 constexpr int kAttNPT = 16;                      // heads*D <= 4096
 constexpr int kActNPT = kMaxVec / kThreads;      // 10: SwiGLU entries per thread (all waves), I <= 10240
+constexpr int kSerialChunks = 16;                // up to this many chunks a head's combine reads its
+                                                 // partials directly (two bursts of eight)
+constexpr int kPartChunks = 62;                  // chunk partials staged in LDS per combine burst
+constexpr int kPartNPT = (kPartChunks * (kD + 2) + kThreads - 1) / kThreads;   // 8 entries per thread
 
 }  // namespace eng
 
@@ -984,8 +988,10 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             ll_store(cp + 2 + lane, S.po[w][lane], epoch_att);
             ll_store(cp + 2 + lane + 64, S.po[w][lane + 64], epoch_att);
         }
-        if (cur) {
-            // M over all chunks: lane i watches chunk c0 + i of each group of 64
+        if (cur && nc <= kSerialChunks) {
+            // few chunks: the four input waves combine them directly from
+            // the hand-off entries.  M over all chunks: lane i watches chunk
+            // c0 + i of each group of 64
             const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(hp, nc * pstride * 8);
             unsigned spins = 0;
             float M = -__builtin_inff();
@@ -1037,6 +1043,67 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             if (lane < 32) ll_store(p.ll_att + size_t(h) * kD + d, O * (1.0f / L), epoch_att);
         }
     }
+    }
+    if (ng > 1 && cur && nc > kSerialChunks) {
+        // The item of the last group combines all nc chunks of head h, in
+        // ascending order: M = max m_c, a_c = exp(m_c - M), L and O fma
+        // chains over c, out = O * (1/L).  Wave 0 waits for every chunk's m
+        // entry (and takes M from them); then the block reads the chunks'
+        // partial entries into LDS (the K/V buffers, free now) in bursts of
+        // kPartChunks chunks, wave 0 writes their a_c, and threads 0..127
+        // carry one dimension's L and O each.
+        constexpr int pstride = kD + 2;
+        static_assert(kPartChunks * pstride * sizeof(float) <= sizeof(S.kv), "partials exceed the K/V buffers");
+        static_assert(kPartChunks <= kGroup * kAttnChunk, "chunk weights exceed the score buffer");
+        const uint64_t* hp = p.ll_part + size_t(h) * size_t(p.max_chunks) * pstride;
+        float* part = reinterpret_cast<float*>(&S.kv[0]);
+        const int T = opaque_tid();
+        if (w == 0) {
+            const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(hp, nc * pstride * 8);
+            unsigned spins = 0;
+            float M = -__builtin_inff();
+            for (int b0 = 0; b0 < nc; b0 += kWave) {
+                const int cc = min(b0 + lane, nc - 1);
+                uint64_t em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
+                while (budget != 0) {
+                    if (ll_ready(em, epoch_att)) break;
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
+                    compiler_fence();
+                    if (!ll_ready(em, epoch_att)) em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
+                }
+                M = fmaxf(M, bits_f32(uint32_t(em)));
+            }
+            M = wave_max64_all(M);
+            if (lane == 0) S.pm[0] = M;
+        }
+        __syncthreads();
+        float L = 0.0f, O = 0.0f;
+        for (int cb = 0; cb < nc; cb += kPartChunks) {
+            const int nb = min(kPartChunks, nc - cb);
+            float v[kPartNPT];
+            poll_into<kPartNPT, kThreads>(hp + size_t(cb) * pstride, nb * pstride, epoch_att, v, budget,
+                                          p.status);
+            static_for<kPartNPT>([&](auto j) {
+                const int e = T + kThreads * j;
+                if (e < nb * pstride) part[e] = v[j];
+            });
+            __syncthreads();
+            if (w == 0) {
+                const float M = S.pm[0];
+                for (int c = lane; c < nb; c += kWave) S.as[c] = spec_expf(part[c * pstride] - M);
+            }
+            __syncthreads();
+            if (T < kD) {
+                for (int c = 0; c < nb; ++c) {
+                    const float al = S.as[c];
+                    L = __builtin_fmaf(al, part[c * pstride + 1], L);
+                    O = __builtin_fmaf(al, part[c * pstride + 2 + T], O);
+                }
+            }
+            __syncthreads();
+        }
+        if (T < kD) ll_store(p.ll_att + size_t(h) * kD + T, O * (1.0f / L), epoch_att);
     }
     if (w == 0) TRACE(l, 29);
     // the item's LDS (K/V chunks, q, scores, partials) may be reused once
