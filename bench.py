@@ -375,7 +375,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(the path runs on one GPU's share; sharding across GPUs is not built)", file=sys.stderr)
         sys.exit(2)
     if args.workload == "gemv":
         bench_gemv(args)

@@ -64,6 +64,8 @@ _SIGNATURES = {
     "hq_gqa_decode": ([vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int, vp], c_int),
     "hq_argmax_workspace_bytes": ([c_int], c_size),
     "hq_argmax": ([vp, c_int, vp, vp, vp], c_int),
+    "hq_sample_workspace_bytes": ([c_int, c_int], c_size),
+    "hq_sample_token": ([vp, c_int, vp, c_int, c_float, c_float, c_int, c_float, vp, vp, vp, vp, vp, vp], c_int),
     "hq_gemm_workspace_bytes": ([c_int, c_int, c_int], c_size),
     "hq_int4_i8_gemm": ([vp, vp, vp, vp, vp, c_int, c_int, c_int, vp, vp, vp], c_int),
     "hq_quant_int4_gemm": ([vp, vp, vp, vp, c_int, c_int, c_int, vp, vp, vp, vp, vp], c_int),

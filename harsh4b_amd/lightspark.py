@@ -13,7 +13,7 @@ repository) on one gfx950 GPU:
   new_state / forward_token  :338, :424    new_state / forward_token
   _projection                :351-371      _projection (hq_int4_i8_gemv)
   _attention                 :389-422      _attention (hq_gqa_decode)
-  sample_logits (argmax)     :700-705      sample_logits (argmax branch)
+  sample_logits              :700-726      sample_logits (hq_argmax / hq_sample_token)
 
 All arithmetic runs in libhq.so; torch only allocates device memory and
 provides the stream.  There is no CPU fallback: a missing library or GPU is
@@ -33,7 +33,7 @@ from ._native import HqLayer, HqModel, HqState, check
 DEFAULT_GEMV_KERNEL = "hip-gfx950"
 
 
-# --------------------------------------------------------------------------- A1
+# --------------------------------------------------------------------------- packing
 def pack_int4(weights: np.ndarray) -> np.ndarray:
     """Pack signed [-7,+7] values as low/high nibbles (cpu_lightspark.py:139-146)."""
     if weights.dtype != np.int8 or weights.ndim != 2 or weights.shape[1] % 2:
@@ -58,7 +58,7 @@ def _stream_handle(stream: torch.cuda.Stream | None) -> int | None:
     return None if stream is None else stream.cuda_stream
 
 
-# --------------------------------------------------------------------------- A4
+# --------------------------------------------------------------------------- projections
 @dataclass(frozen=True)
 class LiteSparkProjection:
     """One row-scaled int4 matrix held on the device (cpu_lightspark.py:246-260)."""
@@ -119,7 +119,7 @@ def rope_tables(config: dict) -> tuple[np.ndarray, np.ndarray]:
     return np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
 
 
-# --------------------------------------------------------------------------- A9
+# --------------------------------------------------------------------------- decode state
 class QwenDecodeState:
     """Caller-owned device state for one sequence (cpu_lightspark.py:275-309).
 
@@ -202,7 +202,7 @@ class QwenDecodeState:
             pass
 
 
-# --------------------------------------------------------------------------- A12
+# --------------------------------------------------------------------------- model
 class LiteSparkQwen:
     """Qwen3 decode runtime on one MI355X (cpu_lightspark.py:312-468)."""
 
@@ -355,13 +355,20 @@ class LiteSparkQwen:
 
 
 def sample_logits(logits, generated, args, generator=None) -> int:
-    """Greedy branch of cpu_lightspark.py:700-705 (first maximal index).
+    """cpu_lightspark.py:700-726 on the device.
 
-    The stochastic branch (:706-726) is not part of this GPU path.
+    argmax: the first maximal index (:704-705).  Otherwise the reference's
+    policy (:706-726) through hq_sample_token; Generator.choice(ids, p)
+    consumes one generator.random() draw, which is taken here on the host
+    in the same place of the generator's stream and handed to the device.
     """
-    if not getattr(args, "argmax", False):
-        raise NotImplementedError("only greedy (argmax) sampling runs on the GPU path")
-    return argmax(logits)
+    if getattr(args, "argmax", False):
+        return argmax(logits)
+    if generator is None:
+        raise ValueError("stochastic sampling needs the run's numpy Generator")
+    token, _, _ = sample_token(logits, generated, args.repetition_penalty, args.temperature, args.top_k,
+                               args.top_p, generator.random())
+    return token
 
 
 # --------------------------------------------------------------------------- ops
@@ -488,3 +495,50 @@ def argmax(logits: torch.Tensor, stream=None) -> int:
     if stream is not None:
         stream.synchronize()
     return int(out.item())
+
+
+SAMPLE_MAX_TOP_K = 2048
+
+
+def sample_token(logits: torch.Tensor, generated, repetition_penalty: float, temperature: float, top_k: int,
+                 top_p: float, u: float, stream=None):
+    """One draw of the reference's stochastic policy (cpu_lightspark.py:706-726)
+    given the uniform number u in [0, 1): returns (token, ids, probabilities)
+    with the ranked top-k ids and their final probabilities as host arrays.
+
+    generated ids index the logits as numpy does (a negative id counts from
+    the end; one outside [-n, n) raises IndexError).
+    """
+    if logits.dtype != torch.float32 or not logits.is_cuda or not logits.is_contiguous():
+        raise ValueError("logits must be a contiguous float32 device tensor")
+    n = logits.numel()
+    if not 1 <= int(top_k) <= SAMPLE_MAX_TOP_K:
+        raise ValueError(f"top_k must be in [1, {SAMPLE_MAX_TOP_K}] on the GPU sampler")
+    if not (np.isfinite(temperature) and temperature > 0):
+        raise ValueError("temperature must be positive and finite")
+    if not (np.isfinite(top_p) and top_p > 0):
+        raise ValueError("top_p must be positive")
+    if not (np.isfinite(repetition_penalty) and repetition_penalty > 0):
+        raise ValueError("repetition_penalty must be positive")
+    if not 0.0 <= float(u) < 1.0:
+        raise ValueError("u must be in [0, 1)")
+    ids = np.asarray(list(generated) if generated is not None else [], dtype=np.int64).reshape(-1)
+    if ids.size and (ids.min() < -n or ids.max() >= n):
+        raise IndexError("a generated id is outside the logits")
+    ids = np.where(ids < 0, ids + n, ids).astype(np.int32)
+    device = logits.device
+    k = min(int(top_k), n)
+    lib = _native.lib()
+    ws = _zeroed_workspace(("sample", device.index), lib.hq_sample_workspace_bytes(n, k), device)
+    gen = torch.from_numpy(ids).to(device) if ids.size else None
+    draw = torch.tensor([float(u)], dtype=torch.float64, device=device)
+    out = torch.empty(1, dtype=torch.int32, device=device)
+    ranked = torch.empty(k, dtype=torch.int32, device=device)
+    probs = torch.empty(k, dtype=torch.float32, device=device)
+    check(lib.hq_sample_token(logits.data_ptr(), n, _ptr(gen), int(ids.size), float(repetition_penalty),
+                              float(temperature), int(top_k), float(top_p), draw.data_ptr(), out.data_ptr(),
+                              ranked.data_ptr(), probs.data_ptr(), ws.data_ptr(), _stream_handle(stream)),
+          "hq_sample_token")
+    if stream is not None:
+        stream.synchronize()
+    return int(out.item()), ranked.cpu().numpy(), probs.cpu().numpy()

@@ -35,7 +35,7 @@ const char* hq_status_string(int status);
 /* ABI version: 100 * major + minor. */
 int hq_abi_version(void);
 
-/* ------------------------------------------------------------------ A4 --
+/* ----------------------------------------------------------- int4 GEMV --
  * Packed signed-int4 x int8 GEMV.  Replaces litespark_int4_i8_gemv,
  * _nopf, _pf256 and _pf512 (cpu_kernels/litespark_int4.cpp:78-108; the four
  * differ only in a CPU prefetch distance), bound at cpu_lightspark.py:71-93:
@@ -47,7 +47,7 @@ int hq_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const float* scales
                     float activation_scale, float* output, int rows, int width,
                     void* stream);
 
-/* ---------------------------------------------------------------- A3+A4 --
+/* ----------------------------------------------- quantization + GEMV --
  * The fused hot-path projection: per-token int8 quantization of fp32 x
  * (replaces the third-party kernel.quantize_activation called at
  * cpu_lightspark.py:433,443,449,457,463) followed by the GEMV above, as
@@ -58,17 +58,17 @@ int hq_quant_int4_gemv(const float* x, const uint8_t* weights, const float* scal
                        float* output, int rows, int width, int8_t* q_out,
                        float* act_scale_out, int32_t* acc_out, void* stream);
 
-/* ------------------------------------------------------------------ A3 --
+/* ------------------------------------------------- quantization --
  * Per-token int8 quantization alone (kernel.quantize_activation,
  * cpu_lightspark.py:433): q int8 [n], act_scale fp32 [1] on the device. */
 int hq_quantize_activation(const float* x, int n, int8_t* q, float* act_scale, void* stream);
 
-/* ------------------------------------------------------------------ A7 --
+/* ------------------------------------------------------ RMSNorm --
  * RMSNorm y = (x / sqrt(mean(x^2) + eps)) * gamma over n values
  * (kernel.rmsnorm_into, cpu_lightspark.py:431,447,461). */
 int hq_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps, void* stream);
 
-/* ----------------------------------------------------------------- A10 --
+/* ------------------------------------------- GQA decode attention --
  * Fused single-token GQA attention (score, softmax and V accumulation in
  * one kernel).  Replaces litespark_gqa_decode (cpu_kernels/
  * litespark_int4.cpp:160-171, bound at cpu_lightspark.py:102-111).
@@ -87,7 +87,7 @@ int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* valu
                   void* workspace, float* output, int context, int kv_heads, int groups,
                   int head_dim, int kv_time_stride, void* stream);
 
-/* ----------------------------------------------------------------- A13 --
+/* ------------------------------------------------------- argmax --
  * Device argmax with np.argmax's order: the first maximal index, a NaN
  * beating every number (cpu_lightspark.py:704-705, the greedy branch of
  * sample_logits).  out_index int32 [1].  `workspace`:
@@ -96,10 +96,31 @@ int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* valu
 size_t hq_argmax_workspace_bytes(int n);
 int hq_argmax(const float* x, int n, int32_t* out_index, void* workspace, void* stream);
 
-/* ----------------------------------------------------------------- A14 --
+/* --------------------------------------------- stochastic sampler --
+ * Stochastic sampling of one token (the non-argmax branch of sample_logits,
+ * cpu_lightspark.py:706-726): repetition penalty over the ids in
+ * `generated` (repeats count once), temperature, the top_k largest values
+ * (value descending, equal values by ascending index), softmax, top-p
+ * (probabilities whose preceding cumulative mass reaches top_p set to 0,
+ * renormalised), then numpy Generator.choice's inverse-cdf draw with the
+ * uniform number *u (device double in [0,1), e.g. the host generator's
+ * random()).  logits fp32 [n]; generated int32 [n_generated] (ids outside
+ * [0,n) are skipped); out_token int32 [1]; ids_out int32 [k] and probs_out
+ * fp32 [k] (nullable) receive the ranked ids and final probabilities, k =
+ * min(top_k, n).  1 <= top_k <= 2048, temperature > 0, repetition_penalty
+ * > 0, top_p > 0 (>= 1: no top-p filtering).  `workspace`:
+ * hq_sample_workspace_bytes(n, top_k) bytes, 256-byte aligned (no zero fill
+ * needed). */
+size_t hq_sample_workspace_bytes(int n, int top_k);
+int hq_sample_token(const float* logits, int n, const int32_t* generated, int n_generated,
+                    float repetition_penalty, float temperature, int top_k, float top_p,
+                    const double* u, int32_t* out_token, int32_t* ids_out, float* probs_out,
+                    void* workspace, void* stream);
+
+/* -------------------------------------------------- batched GEMM --
  * Batched decode (M concurrent sequences share each weight read).  No
  * reference counterpart (forward_token is batch 1, cpu_lightspark.py:424);
- * defined as M independent A4 calls and bit-identical to them:
+ * defined as M independent hq_int4_i8_gemv calls and bit-identical to them:
  *   output[m, n] = ((float)sum_k W[n,k] * x[m,k] * act_scales[m]) * scales[n]
  * x int8 [m, width]; act_scales fp32 [m]; output fp32 [m, rows];
  * acc_out (nullable) int32 [m, rows].  The products run on int8 MFMA
@@ -114,7 +135,7 @@ size_t hq_gemm_workspace_bytes(int m, int rows, int width);
 int hq_int4_i8_gemm(const int8_t* x, const float* act_scales, const uint8_t* weights,
                     const float* scales, float* output, int m, int rows, int width,
                     int32_t* acc_out, void* workspace, void* stream);
-/* Fused form: per-sequence quantization of fp32 x [m, width] (the A3 spec
+/* Fused form: per-sequence quantization of fp32 x [m, width] (hq_quantize_activation's spec
  * applied to each row), then the GEMM.  q_out int8 [m, width] and
  * act_scales_out fp32 [m] are optional outputs.  Here width <= 10240, x is
  * 16-byte aligned and q_out (when given) 8-byte aligned. */
@@ -123,7 +144,7 @@ int hq_quant_int4_gemm(const float* x, const uint8_t* weights, const float* scal
                        float* act_scales_out, int32_t* acc_out, void* workspace,
                        void* stream);
 
-/* ------------------------------------------------------------- A6..A13 --
+/* ----------------------------------------------------- decode step --
  * One decode step of a Qwen3-shaped model, as LiteSparkQwen.forward_token
  * (cpu_lightspark.py:424-468): embedding row decode, per layer RMSNorm ->
  * quant -> fused qkv GEMV -> qk-norm -> RoPE -> fp16 KV write -> GQA

@@ -104,6 +104,11 @@ def _declare(L: ctypes.CDLL) -> None:
     L.or_gqa_decode_split_f32.argtypes = [vp] * 4 + [ctypes.c_int] * 4 + [ctypes.c_int64, ctypes.c_int]
     L.or_swiglu.argtypes = [vp, vp, vp, ctypes.c_int]
     L.or_argmax.argtypes = [vp, ctypes.c_int64]
+    L.or_pairwise_sum_f32.argtypes = [vp, ctypes.c_int]
+    L.or_pairwise_sum_f32.restype = ctypes.c_float
+    L.or_sample_token.argtypes = [vp, ctypes.c_int64, vp, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                  ctypes.c_int, ctypes.c_float, ctypes.c_double, vp, vp]
+    L.or_sample_token.restype = ctypes.c_int64
     L.or_argmax.restype = ctypes.c_int64
     L.or_embedding.argtypes = [ctypes.POINTER(OrModel), ctypes.c_int, vp]
     L.or_forward_token.argtypes = [ctypes.POINTER(OrModel), ctypes.POINTER(OrState), ctypes.c_int]
@@ -138,7 +143,7 @@ def f16_bits_to_f32(h) -> np.ndarray:
     return out
 
 
-# ---------------------------------------------------------------- A1 / A2
+# ---------------------------------------------------------------- packing
 def pack_int4(weights: np.ndarray) -> np.ndarray:
     """cpu_lightspark.py:139-146."""
     w = np.ascontiguousarray(weights, dtype=np.int8)
@@ -160,7 +165,7 @@ def unpack_int4(packed: np.ndarray, width: int) -> np.ndarray:
     return out
 
 
-# ---------------------------------------------------------------- A3 / A7 / A8
+# ---------------------------------------------------------------- quantization, norms
 def quantize_activation(x: np.ndarray):
     """Returns (int8 vector, act_scale)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
@@ -192,7 +197,7 @@ def rope(x: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.ndarray:
     return y
 
 
-# ---------------------------------------------------------------- A4
+# ---------------------------------------------------------------- int4 GEMV
 def int4_i8_gemv(x, weights, scales, activation_scale, rows, width) -> np.ndarray:
     """litespark_int4.cpp:78-108 signature."""
     x = np.ascontiguousarray(x, dtype=np.int8)
@@ -221,7 +226,7 @@ def int4_i8_gemm_acc(x, weights, rows, width) -> np.ndarray:
 
 
 def quant_int4_gemv(x, weights, scales):
-    """Fused A3 + A4.  Returns (out fp32, q int8, act_scale, acc int32)."""
+    """Fused quantization + GEMV.  Returns (out fp32, q int8, act_scale, acc int32)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     w = np.ascontiguousarray(weights, dtype=np.uint8)
     s = np.ascontiguousarray(scales, dtype=np.float32)
@@ -233,7 +238,7 @@ def quant_int4_gemv(x, weights, scales):
     return out, q, np.float32(act), acc
 
 
-# ---------------------------------------------------------------- A10
+# ---------------------------------------------------------------- GQA decode attention
 def gqa_decode_ref(query, keys, values, context, kv_heads, groups, head_dim, capacity):
     """litespark_int4.cpp:160-259 with fp32 keys/values [capacity, kv, d]."""
     q = np.ascontiguousarray(query, dtype=np.float32)
@@ -268,7 +273,7 @@ def gqa_decode_split_f32(query, keys, values, context, kv_heads, groups, head_di
     return out
 
 
-# ---------------------------------------------------------------- A11 / A13
+# ---------------------------------------------------------------- SwiGLU, argmax, sampler
 def swiglu(gate, up) -> np.ndarray:
     g = np.ascontiguousarray(gate, dtype=np.float32)
     u = np.ascontiguousarray(up, dtype=np.float32)
@@ -282,7 +287,25 @@ def argmax(x) -> int:
     return int(lib().or_argmax(_p(x), x.size))
 
 
-# ---------------------------------------------------------------- A6 / A12
+def pairwise_sum_f32(a) -> np.float32:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return np.float32(lib().or_pairwise_sum_f32(_p(a), a.size))
+
+
+def sample_token(logits, generated, repetition_penalty, temperature, top_k, top_p, u):
+    """The reference's stochastic sampler (cpu_lightspark.py:706-726) with the
+    uniform draw u given: returns (token, ids [k], probabilities [k])."""
+    x = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+    g = np.ascontiguousarray(generated, dtype=np.int32).reshape(-1)
+    k = max(1, min(int(top_k), x.size))
+    ids = np.empty(k, np.int32)
+    probs = np.empty(k, np.float32)
+    tok = lib().or_sample_token(_p(x), x.size, _p(g) if g.size else None, g.size, float(repetition_penalty),
+                                float(temperature), int(top_k), float(top_p), float(u), _p(ids), _p(probs))
+    return int(tok), ids, probs
+
+
+# ---------------------------------------------------------------- decode step
 class OracleModel:
     """Host copy of a model in the oracle's struct form.
 

@@ -111,7 +111,7 @@ void or_f16_to_f32_array(const uint16_t* h, float* x, int64_t n)
 }
 
 /* ------------------------------------------------------------------------ */
-/* A1 / A2: packing                                                          */
+/* packing and unpacking                                                    */
 /* ------------------------------------------------------------------------ */
 /*
  * cpu_lightspark.py:139-146 (_pack_int4): P[n,j] = (W[n,2j] & 0xF) |
@@ -152,7 +152,7 @@ int or_unpack_int4(const uint8_t* p, int rows, int width, int8_t* out)
 }
 
 /* ------------------------------------------------------------------------ */
-/* A3: per-token int8 activation quantization                                */
+/* per-token int8 activation quantization                                    */
 /* ------------------------------------------------------------------------ */
 /*
  * Stands in for the third-party kernel.quantize_activation called at
@@ -182,7 +182,7 @@ float or_quantize_activation(const float* x, int n, int8_t* q)
 }
 
 /* ------------------------------------------------------------------------ */
-/* A7: RMSNorm and per-head norm                                             */
+/* RMSNorm and per-head norm                                                 */
 /* ------------------------------------------------------------------------ */
 /*
  * Sum of squares with the spec's fixed tree: lane l of `lanes` accumulates
@@ -249,7 +249,7 @@ void or_rope(float* x, int heads, int head_dim, const float* cos_row, const floa
 }
 
 /* ------------------------------------------------------------------------ */
-/* A4: packed int4 x int8 GEMV                                               */
+/* packed int4 x int8 GEMV                                                   */
 /* ------------------------------------------------------------------------ */
 /*
  * litespark_int4.cpp:22-76.  acc = sum_k W[n,k] * x[k] in int32 (the NEON
@@ -291,7 +291,7 @@ void or_int4_i8_gemm_acc(const int8_t* x, const uint8_t* weights, int m, int row
                             acc + (int64_t)i * rows);
 }
 
-/* A3 + A4 as one call: the fused hot-path entry.  Returns act_scale. */
+/* Quantization + GEMV as one call: the fused hot-path entry.  Returns act_scale. */
 float or_quant_int4_gemv(const float* x, const uint8_t* weights, const float* scales,
                          float* output, int rows, int width, int8_t* q_out, int32_t* acc_out)
 {
@@ -306,7 +306,7 @@ float or_quant_int4_gemv(const float* x, const uint8_t* weights, const float* sc
 }
 
 /* ------------------------------------------------------------------------ */
-/* A10: GQA decode attention                                                 */
+/* GQA decode attention                                                      */
 /* ------------------------------------------------------------------------ */
 /*
  * Literal restatement of litespark_gqa_decode (litespark_int4.cpp:160-259)
@@ -476,7 +476,7 @@ void or_gqa_decode_split_f32(const float* query, const float* keys, const float*
 }
 
 /* ------------------------------------------------------------------------ */
-/* A11 SwiGLU, A13 argmax                                                    */
+/* SwiGLU, argmax                                                            */
 /* ------------------------------------------------------------------------ */
 /* cpu_lightspark.py:451-455: negate, exp, +1, divide, multiply. */
 void or_swiglu(const float* gate, const float* up, float* out, int n)
@@ -503,7 +503,129 @@ int64_t or_argmax(const float* x, int64_t n)
 }
 
 /* ------------------------------------------------------------------------ */
-/* A6 embedding, A12 forward_token                                           */
+/* stochastic sampler                                                        */
+/* ------------------------------------------------------------------------ */
+/* numpy's float32 add.reduce order for n <= 128 (pairwise_sum): n < 8 a
+ * sequential sum from 0; else eight strided accumulators, combined as
+ * ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then the n % 8 tail added in order. */
+float or_pairwise_sum_f32(const float* a, int n)
+{
+    /* numpy's pairwise_sum (umath loops_utils.h.src): < 8 values in order,
+       <= 128 values in eight running sums, larger halves split at a
+       multiple of 8 below n/2 */
+    if (n < 8) {
+        float r = 0.0f;
+        for (int i = 0; i < n; ++i) r += a[i];
+        return r;
+    }
+    if (n > 128) {
+        int n2 = n / 2;
+        n2 -= n2 % 8;
+        return or_pairwise_sum_f32(a, n2) + or_pairwise_sum_f32(a + n2, n - n2);
+    }
+    float r[8];
+    for (int j = 0; j < 8; ++j) r[j] = a[j];
+    int i = 8;
+    for (; i < n - (n % 8); i += 8)
+        for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+    float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; ++i) res += a[i];
+    return res;
+}
+
+/* Rank of a value: larger first, NaN after every number. */
+static int or_sample_before(float a, int64_t ia, float b, int64_t ib)
+{
+    const int na = a != a, nb = b != b;
+    if (na != nb) return nb;                 /* a number before a NaN */
+    if (!na && a != b) return a > b;
+    return ia < ib;                          /* equal values (or two NaNs): lower index */
+}
+
+/*
+ * cpu_lightspark.py:706-726, with the repo's exp (or_expf) and the top-k order
+ * among equal values fixed to ascending index (numpy leaves it open):
+ *   v = logits (fp32); for each distinct id in generated, when rp != 1:
+ *       v[id] = v[id] > 0 ? v[id] / rp : v[id] * rp
+ *   v[i] = v[i] / temperature                      (every element)
+ *   ids = the k = min(top_k, n) largest v, by value descending
+ *   s_i = v[ids[i]] - v[ids[0]];  p_i = exp(s_i);  p_i = p_i / sum(p)
+ *   if top_p < 1: c = cumsum(p) (fp32, in order); p_i = 0 where c_i - p_i >= top_p;
+ *                 p_i = p_i / sum(p)
+ *   Generator.choice(ids, p): cdf = cumsum((double)p); cdf_i = cdf_i / cdf_{k-1};
+ *                 index = #{i : cdf_i <= u} with u = generator.random()
+ * sums are or_pairwise_sum_f32 (numpy's order).  Writes the k ids and final
+ * probabilities when ids_out / probs_out are given; returns the token.
+ */
+int64_t or_sample_token(const float* logits, int64_t n, const int32_t* generated, int n_generated,
+                        float repetition_penalty, float temperature, int top_k, float top_p, double u,
+                        int32_t* ids_out, float* probs_out)
+{
+    float* v = (float*)malloc((size_t)n * sizeof(float));
+    for (int64_t i = 0; i < n; ++i) v[i] = logits[i];
+    if (repetition_penalty != 1.0f)
+        for (int g = 0; g < n_generated; ++g) {
+            const int32_t id = generated[g];
+            if (id < 0 || id >= n) continue;
+            const float x = logits[id];
+            v[id] = x > 0.0f ? x / repetition_penalty : x * repetition_penalty;
+        }
+    for (int64_t i = 0; i < n; ++i) v[i] = v[i] / temperature;
+    int k = top_k < n ? top_k : (int)n;
+    if (k < 1) k = 1;
+    int64_t* ids = (int64_t*)malloc((size_t)k * sizeof(int64_t));
+    int have = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        if (have == k && !or_sample_before(v[i], i, v[ids[k - 1]], ids[k - 1])) continue;
+        int pos = have < k ? have++ : k - 1;
+        while (pos > 0 && or_sample_before(v[i], i, v[ids[pos - 1]], ids[pos - 1])) {
+            ids[pos] = ids[pos - 1];
+            --pos;
+        }
+        ids[pos] = i;
+    }
+    float* p = (float*)malloc((size_t)k * sizeof(float));
+    const float top = v[ids[0]];
+    for (int i = 0; i < k; ++i) p[i] = or_expf(v[ids[i]] - top);
+    float s = or_pairwise_sum_f32(p, k);
+    for (int i = 0; i < k; ++i) p[i] = p[i] / s;
+    if (top_p < 1.0f) {
+        float c = 0.0f;
+        float* drop = (float*)malloc((size_t)k * sizeof(float));
+        for (int i = 0; i < k; ++i) {
+            c = c + p[i];
+            drop[i] = c - p[i];
+        }
+        for (int i = 0; i < k; ++i)
+            if (drop[i] >= top_p) p[i] = 0.0f;
+        free(drop);
+        s = or_pairwise_sum_f32(p, k);
+        for (int i = 0; i < k; ++i) p[i] = p[i] / s;
+    }
+    double* cdf = (double*)malloc((size_t)k * sizeof(double));
+    double c = 0.0;
+    for (int i = 0; i < k; ++i) {
+        c = c + (double)p[i];
+        cdf[i] = c;
+    }
+    const double last = cdf[k - 1];
+    int index = 0;
+    for (int i = 0; i < k; ++i) {
+        cdf[i] = cdf[i] / last;
+        if (cdf[i] <= u) index = i + 1;
+    }
+    if (index >= k) index = k - 1;
+    const int64_t token = ids[index];
+    if (ids_out)
+        for (int i = 0; i < k; ++i) ids_out[i] = (int32_t)ids[i];
+    if (probs_out)
+        for (int i = 0; i < k; ++i) probs_out[i] = p[i];
+    free(cdf); free(p); free(ids); free(v);
+    return token;
+}
+
+/* ------------------------------------------------------------------------ */
+/* embedding, forward_token                                                   */
 /* ------------------------------------------------------------------------ */
 /* cpu_lightspark.py:341-349: decode one int4 row, multiply by its scale. */
 void or_embedding(const or_model* m, int token, float* out)

@@ -12,7 +12,8 @@
  *                                    RoPE tables (:329-336), embedding (:341-349),
  *                                    projection (:351-371), qk-norm (:373-379),
  *                                    rope (:381-387), attention (:389-422),
- *                                    forward_token order (:424-468), argmax (:704-705)
+ *                                    forward_token order (:424-468), argmax (:704-705),
+ *                                    stochastic sampler (:706-726)
  *   MLX/bitnet_mlx.py:17-23          per-token absmax int8 quantization precedent
  *
  * The reference leaves the bits of several fp32 steps open (its kernels build
@@ -41,17 +42,17 @@ float or_f16_to_f32(uint16_t h);
 void or_f32_to_f16_array(const float* x, uint16_t* h, int64_t n);
 void or_f16_to_f32_array(const uint16_t* h, float* x, int64_t n);
 
-/* ---- A1 / A2 packing ---- */
+/* ---- packing ---- */
 int or_pack_int4(const int8_t* w, int rows, int width, uint8_t* out);
 int or_unpack_int4(const uint8_t* p, int rows, int width, int8_t* out);
 
-/* ---- A3 quantization, A7 norms ---- */
+/* ---- quantization, norms ---- */
 float or_quantize_activation(const float* x, int n, int8_t* q);
 void or_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps);
 void or_head_norm(float* x, const float* gamma, int heads, int head_dim, float eps);
 void or_rope(float* x, int heads, int head_dim, const float* cos_row, const float* sin_row);
 
-/* ---- A4 GEMV ---- */
+/* ---- GEMV ---- */
 void or_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const float* scales,
                      float activation_scale, float* output, int rows, int width);
 void or_int4_i8_gemv_acc(const int8_t* x, const uint8_t* weights, int rows, int width,
@@ -61,7 +62,7 @@ void or_int4_i8_gemm_acc(const int8_t* x, const uint8_t* weights, int m, int row
 float or_quant_int4_gemv(const float* x, const uint8_t* weights, const float* scales,
                          float* output, int rows, int width, int8_t* q_out, int32_t* acc_out);
 
-/* ---- A10 attention ---- */
+/* ---- attention ---- */
 void or_gqa_decode_ref(const float* query, const float* keys, const float* values,
                        float* scores, float* output, int context, int kv_heads,
                        int groups, int head_dim, int score_stride);
@@ -72,11 +73,17 @@ void or_gqa_decode_split_f32(const float* query, const float* keys, const float*
                              float* output, int context, int kv_heads, int groups,
                              int head_dim, int64_t time_stride, int chunk);
 
-/* ---- A11 / A13 ---- */
+/* ---- SwiGLU, argmax ---- */
 void or_swiglu(const float* gate, const float* up, float* out, int n);
 int64_t or_argmax(const float* x, int64_t n);
 
-/* ---- A6 / A12 full decode step ---- */
+/* ---- stochastic sampler (cpu_lightspark.py:706-726) ---- */
+float or_pairwise_sum_f32(const float* a, int n);
+int64_t or_sample_token(const float* logits, int64_t n, const int32_t* generated, int n_generated,
+                        float repetition_penalty, float temperature, int top_k, float top_p, double u,
+                        int32_t* ids_out, float* probs_out);
+
+/* ---- full decode step ---- */
 typedef struct or_layer {
     const uint8_t* qkv;      const float* qkv_scales;
     const uint8_t* o;        const float* o_scales;

@@ -47,6 +47,42 @@ def test_host_validation_rejects_bad_shapes_without_launching():
     assert lib.hq_gqa_workspace_bytes(64, 8, 4, 128) >= 32 * 130 * 4
 
 
+def test_sampler_rejects_bad_arguments_without_launching():
+    # every check returns before a HIP call; the pointers are never read
+    import ctypes
+    from harsh4b_amd import _native
+    lib = _native.lib()
+    buf = ctypes.create_string_buffer(1024)
+    p = ctypes.addressof(buf)
+    ws = (p + 255) & ~255
+
+    def call(n=1000, top_k=40, temperature=0.7, rp=1.08, top_p=0.9, workspace=ws, n_generated=0):
+        return lib.hq_sample_token(p, n, p, n_generated, rp, temperature, top_k, top_p, p, p, None, None,
+                                   workspace, None)
+
+    assert call(top_k=0) == 1 and call(top_k=2049) == 1
+    assert call(temperature=0.0) == 1 and call(temperature=float("nan")) == 1
+    assert call(rp=0.0) == 1 and call(top_p=0.0) == 1 and call(top_p=-1.0) == 1
+    assert call(n=0) == 1 and call(n_generated=-1) == 1
+    assert call(workspace=ws + 4) == 2                                          # 256-byte alignment
+    assert lib.hq_sample_token(None, 10, None, 0, 1.0, 1.0, 5, 1.0, p, p, None, None, ws, None) == 1
+    # values, then two candidate lists of k keys per 4096-value slice
+    assert lib.hq_sample_workspace_bytes(151936, 40) >= 151936 * 4 + 2 * 38 * 40 * 8
+    assert lib.hq_sample_workspace_bytes(10, 40) >= 10 * 4 + 2 * 10 * 8
+
+
+def test_sampler_host_checks():
+    torch = pytest.importorskip("torch")
+    from harsh4b_amd import lightspark as ls
+
+    class Args:
+        argmax, repetition_penalty, temperature, top_k, top_p = False, 1.08, 0.7, 40, 0.9
+    with pytest.raises(ValueError, match="Generator"):
+        ls.sample_logits(torch.zeros(4), [], Args())
+    with pytest.raises(ValueError, match="device tensor"):
+        ls.sample_token(torch.zeros(4), [], 1.0, 1.0, 2, 1.0, 0.5)
+
+
 def test_workspace_sizes_cover_qwen_step():
     import ctypes
     from harsh4b_amd import _native

@@ -24,7 +24,7 @@ def lightspark():
     return ls
 
 
-# ------------------------------------------------------------------ A4 GEMV
+# ------------------------------------------------------------------ GEMV
 def test_gemv_known_answer(kat):
     ls = lightspark()
     w = kat["gemv_w"]
@@ -137,7 +137,7 @@ def test_quantize_and_rmsnorm_standalone():
         assert_bits_equal(to_host(y), oracle.rmsnorm(x, g, 1e-6), f"rmsnorm n={n}")
 
 
-# ------------------------------------------------------------------ A10 attention
+# ------------------------------------------------------------------ attention
 def test_gqa_known_answer(kat):
     ls = lightspark()
     kv, g, ctx, cap, d = (int(v) for v in kat["gqa_shape"])
@@ -197,7 +197,7 @@ def test_gqa_repeated_calls_reuse_workspace():
         assert_bits_equal(to_host(out), ref, f"repeat ctx={ctx}")
 
 
-# ------------------------------------------------------------------ A13 argmax
+# ------------------------------------------------------------------ argmax
 def test_device_argmax_order(kat):
     ls = lightspark()
     assert ls.argmax(to_dev(kat["argmax_logits"])) == int(kat["argmax_expected"])
@@ -211,7 +211,82 @@ def test_device_argmax_order(kat):
     assert ls.argmax(to_dev(np.array([-0.0, 0.0], np.float32))) == 0
 
 
-# ------------------------------------------------------------------ A14 batched
+# ------------------------------------------------------------------ sampler
+def check_sample(logits, generated, rp, temperature, top_k, top_p, u, what):
+    ls = lightspark()
+    got = ls.sample_token(to_dev(logits), generated, rp, temperature, top_k, top_p, u)
+    want = oracle.sample_token(logits, generated, rp, temperature, top_k, top_p, u)
+    np.testing.assert_array_equal(got[1], want[1], err_msg=f"ids {what}")
+    assert_bits_equal(got[2], want[2], f"probabilities {what}")
+    assert got[0] == want[0], what
+    return got
+
+
+def test_sampler_reference_policy():
+    # the reference runner's defaults (temperature 0.7, top-k 40, top-p 0.9,
+    # repetition penalty 1.08) on Qwen3-4B's vocabulary
+    rng = np.random.default_rng(11)
+    for trial in range(12):
+        logits = (rng.standard_normal(151936) * rng.uniform(1, 6)).astype(np.float32)
+        generated = [int(t) for t in rng.integers(0, 151936, 40)]
+        generated += generated[:5]                                  # repeats count once
+        generated += [int(i) for i in np.argsort(-logits)[:8]]      # penalise some of the top
+        check_sample(logits, generated, 1.08, 0.7, 40, 0.9, float(rng.random()), f"trial {trial}")
+
+
+@pytest.mark.parametrize("n,top_k", [(151936, 1), (151936, 64), (151936, 107), (151936, 108), (151936, 500),
+                                     (151936, 2048), (4096, 40), (4097, 40), (4097, 2048), (10, 40), (5, 5),
+                                     (1, 3), (70000, 1500)])
+def test_sampler_sizes_and_merge_rounds(n, top_k):
+    rng = np.random.default_rng(n + top_k)
+    logits = (rng.standard_normal(n) * 3).astype(np.float32)
+    for u in (0.0, float(rng.random()), 0.999999):
+        for top_p in (1.0, 0.9, 0.3):
+            check_sample(logits, [0, n - 1], 1.3, 1.1, top_k, top_p, u, f"n={n} k={top_k} u={u} p={top_p}")
+
+
+def test_sampler_ties_signs_and_penalty():
+    rng = np.random.default_rng(3)
+    # values on a coarse grid: long runs of equal values rank by index
+    logits = (np.round(rng.standard_normal(151936) * 8) / 4).astype(np.float32)
+    for top_k in (40, 300, 2048):
+        check_sample(logits, [], 1.0, 1.0, top_k, 0.95, 0.37, f"ties k={top_k}")
+    # -0/+0, infinities, negative logits under the penalty, a tiny top-p
+    x = rng.standard_normal(50000).astype(np.float32) - 4
+    x[[10, 11, 12]] = [0.0, -0.0, 0.0]
+    x[[20, 21]] = -np.inf
+    gen = [int(i) for i in np.argsort(-x)[:30]] + [10, 11, 20]
+    check_sample(x, gen, 1.5, 0.5, 64, 0.9, 0.61, "signs")
+    check_sample(x, gen, 1.5, 0.5, 64, 1e-6, 0.99, "tiny top-p")
+    small = np.array([0.5, 3.0, -2.0, 2.9, 1.0], np.float32)
+    assert check_sample(small, [1, 1, 1], 2.0, 1.0, 5, 1.0, 0.0, "small")[0] == 3
+    assert check_sample(small, [], 1.0, 0.7, 1, 0.9, 0.999, "k=1")[0] == 1
+
+
+def test_sample_logits_follows_the_generator():
+    # sample_logits consumes the generator as Generator.choice does: one
+    # random() per token, so the device run and the oracle draw the same u
+    ls = lightspark()
+
+    class Args:
+        argmax, repetition_penalty, temperature, top_k, top_p = False, 1.08, 0.7, 40, 0.9
+    rng = np.random.default_rng(2)
+    g_dev, g_ref = np.random.default_rng(0), np.random.default_rng(0)
+    generated = []
+    for step in range(20):
+        logits = (rng.standard_normal(151936) * 2).astype(np.float32)
+        token = ls.sample_logits(to_dev(logits), generated, Args(), g_dev)
+        want = oracle.sample_token(logits, generated, 1.08, 0.7, 40, 0.9, g_ref.random())[0]
+        assert token == want, step
+        generated.append(token)
+    assert g_dev.random() == g_ref.random()
+    with pytest.raises(ValueError, match="top_k"):
+        ls.sample_token(to_dev(logits), [], 1.0, 1.0, 4096, 1.0, 0.5)
+    with pytest.raises(IndexError):
+        ls.sample_token(to_dev(logits), [151936], 1.08, 1.0, 4, 1.0, 0.5)
+
+
+# ------------------------------------------------------------------ batched
 @pytest.mark.parametrize("m", [1, 8, 16, 32, 40])
 @pytest.mark.parametrize("rows,width", [(2560, 9728), (6144, 2560), (100, 96)])
 def test_batched_gemm_bit_exact(m, rows, width):

@@ -12,7 +12,7 @@ import pytest
 import oracle
 
 
-# ----------------------------------------------------------------- A1 / A2
+# ----------------------------------------------------------------- packing
 def test_pack_golden_and_range_error(kat):
     np.testing.assert_array_equal(oracle.pack_int4(kat["pack_w"]), kat["pack_p"])
     with pytest.raises(ValueError, match=r"\[-7,\+7\]"):
@@ -35,7 +35,7 @@ def test_pack_unpack_roundtrip_and_nibble_layout():
     np.testing.assert_array_equal(np.where(hi > 7, hi - 16, hi), w[:, 1::2])
 
 
-# ----------------------------------------------------------------- A4
+# ----------------------------------------------------------------- GEMV
 def test_gemv_known_answer(kat):
     w = kat["gemv_w"]
     p = oracle.pack_int4(w)
@@ -85,7 +85,7 @@ def test_batched_gemm_equals_independent_gemvs():
     np.testing.assert_array_equal(acc, x.astype(np.int64) @ w.astype(np.int64).T)
 
 
-# ----------------------------------------------------------------- A3
+# ----------------------------------------------------------------- quantization
 def test_quantize_closed_form():
     rng = np.random.default_rng(11)
     x = rng.standard_normal(2560).astype(np.float32)
@@ -116,7 +116,7 @@ def test_quantize_ties_round_half_even():
     assert q.tolist() == [127, 0, 2, 2, 0, -2]
 
 
-# ----------------------------------------------------------------- A7 / A8
+# ----------------------------------------------------------------- norms
 def test_rmsnorm_against_float64():
     rng = np.random.default_rng(12)
     x = (rng.standard_normal(2560) * 3).astype(np.float32)
@@ -209,7 +209,7 @@ def test_f16_conversion_matches_numpy():
     np.testing.assert_array_equal(back, x.astype(np.float16).astype(np.float32))
 
 
-# ----------------------------------------------------------------- A10
+# ----------------------------------------------------------------- attention
 def test_gqa_known_answer(kat):
     kv, g, ctx, cap, d = (int(v) for v in kat["gqa_shape"])
     out, _ = oracle.gqa_decode_ref(kat["gqa_query"], kat["gqa_keys"], kat["gqa_values"],
@@ -261,7 +261,7 @@ def test_gqa_head_mapping():
     np.testing.assert_allclose(out[3:], 1.0, rtol=1e-6)
 
 
-# ----------------------------------------------------------------- A11 / A13
+# ----------------------------------------------------------------- SwiGLU, argmax
 def test_swiglu_against_float64():
     rng = np.random.default_rng(22)
     gt = (rng.standard_normal(9728) * 4).astype(np.float32)
