@@ -3,57 +3,157 @@
 // gfx950: repetition penalty, temperature, top-k, softmax, top-p and the
 // inverse-cdf draw of numpy's Generator.choice, given the uniform draw u.
 //
-//   1. values = logits                                   (sample_copy_kernel)
-//   2. values[id] = logits[id] > 0 ? logits[id] / rp : logits[id] * rp for
-//      every id of `generated` (a repeated id writes the same value again)
-//   3. v_i = values[i] / temperature; each block sorts its slice of v by
-//      (value descending, NaN last, index ascending) in LDS and keeps its
-//      first k entries as a sorted list                  (sample_block_kernel)
-//   4. while more than one list is left, each block sorts the union of
-//      kSampleSlice / k lists and keeps its first k      (sample_merge_kernel)
-//   5. one block runs softmax / top-p / cdf on the k survivors in the
-//      reference's order, with the repo's exp and numpy's float32 summation
-//      order; the ordered sums run on thread 0           (sample_finish_kernel)
+//   1. block b loads logits[b*S, (b+1)*S) into LDS and applies the penalty
+//      there: v[id] = logits[id] > 0 ? logits[id] / rp : logits[id] * rp for
+//      every id of `generated` in its slice (a repeated id writes the same
+//      value again)
+//   2. it turns v_i / temperature into 64-bit sort keys (value descending,
+//      NaN last, index ascending; the value is recoverable from the key)
+//      and radix-selects its k smallest keys, 8 bits per pass, into a
+//      candidate list in global memory
+//   3. the last block to finish (a ticket counter) selects the k smallest of
+//      all candidates the same way, sorts those k, and runs softmax / top-p
+//      / cdf in the reference's order with the repo's exp and numpy's float32
+//      summation order; the ordered sums run on thread 0
 // The result equals the oracle's or_sample_token bit for bit (ids,
-// probabilities, token).
+// probabilities, token).  One launch per token.
 #include "hq_device.h"
 #include "hq_internal.h"
 
 namespace hq {
 
-constexpr int kSampleBlock = 1024;      // threads of the slice and merge sorts
-constexpr int kSampleSlice = 4096;      // keys one sort holds (32 KiB of LDS)
-constexpr int kSampleFinish = 1024;     // threads of the finish kernel
-constexpr int kSampleMaxK = kSampleSlice / 2;   // a merge joins at least two lists
+constexpr int kSampleThreads = 1024;
+constexpr int kSampleSlice = 4096;               // logits per block; keys the LDS array holds
+constexpr int kSampleMaxK = kSampleSlice / 2;    // the last block's chunks add at least k keys
 
 // Sort key: ascending key order = value descending (NaN last), then index
-// ascending.  -0 and +0 rank as equal values.  ~0 pads a slice: it sorts
-// after every real key.
+// ascending.  -0 ranks (and is recovered) as +0.
 __device__ __forceinline__ uint64_t sample_key(float v, int i)
 {
-    uint32_t u = f32_bits(v);
     uint32_t hi;
     if (v != v) {
         hi = 0xFFFFFFFFu;
     } else {
+        uint32_t u = f32_bits(v);
         if (u == 0x80000000u) u = 0;
         const uint32_t asc = (u & 0x80000000u) ? ~u : (u | 0x80000000u);   // ascending with the value
-        hi = ~asc;                                                             // descending
+        hi = ~asc;
     }
     return (uint64_t(hi) << 32) | uint32_t(i);
 }
 
-// Ascending bitonic sort of kSampleSlice keys in LDS by kSampleBlock threads.
-__device__ void bitonic_sort(uint64_t* key)
+// Past the end of the logits: after every real key (NaN keys included,
+// whose indices are < n) and distinct, as the radix select needs.
+__device__ __forceinline__ uint64_t pad_key(int i) { return (uint64_t(0xFFFFFFFFu) << 32) | uint32_t(i); }
+
+__device__ __forceinline__ float key_value(uint64_t key)
 {
-    for (int k = 2; k <= kSampleSlice; k <<= 1) {
+    const uint32_t asc = ~uint32_t(key >> 32);
+    return __uint_as_float((asc & 0x80000000u) ? (asc & 0x7FFFFFFFu) : ~asc);
+}
+
+__device__ __forceinline__ int key_index(uint64_t key) { return int(uint32_t(key)); }
+
+__device__ __forceinline__ void publish_u64(uint64_t* p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t read_u64(const uint64_t* p)
+{
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct SampleShared {
+    uint64_t key[kSampleSlice];
+    union {
+        float v[kSampleSlice];                          // the slice's values (phase 1)
+        struct {
+            uint64_t win[kSampleMaxK];                  // selected keys (last block)
+            float p[kSampleMaxK];
+            float drop[kSampleMaxK];
+        } f;
+    } u;
+    int hist[256];
+    int digit, before, done, count, ticket;
+    float total;
+};
+
+// The k smallest of the `count` keys S.key[0..count) (k <= count; the keys
+// must be distinct, or the last bin could hand out more than k),
+// written unordered to out[0..k) by LDS-atomic positions.  Radix select on
+// 8-bit digits from the top: each pass histograms the keys that share the
+// digits chosen so far and picks the digit bin holding the k-th key; when
+// that bin is taken whole the selection stops early.  Every thread of the
+// block calls it; out may be global memory (published with agent scope).
+template <bool GLOBAL>
+__device__ void select_k(SampleShared& S, int count, int k, uint64_t* out)
+{
+    const int t = threadIdx.x;
+    uint64_t prefix = 0, mask = 0;
+    int need = k;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        if (t < 256) S.hist[t] = 0;
+        __syncthreads();
+        for (int j = t; j < count; j += kSampleThreads) {
+            const uint64_t x = S.key[j];
+            if ((x & mask) == prefix) atomicAdd(&S.hist[int(x >> shift) & 255], 1);
+        }
+        __syncthreads();
+        if (t < 64) {
+            int c[4], sum = 0;
+            for (int j = 0; j < 4; ++j) {
+                c[j] = S.hist[4 * t + j];
+                sum += c[j];
+            }
+            int incl = sum;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(incl, o, 64);
+                if (t >= o) incl += y;
+            }
+            int before = incl - sum;
+            if (before < need && need <= incl) {
+                for (int j = 0; j < 4; ++j) {
+                    if (need <= before + c[j]) {
+                        S.digit = 4 * t + j;
+                        S.before = before;
+                        S.done = (need - before) == c[j];
+                        break;
+                    }
+                    before += c[j];
+                }
+            }
+        }
+        __syncthreads();
+        need -= S.before;
+        prefix |= uint64_t(S.digit) << shift;
+        mask |= uint64_t(255) << shift;
+        const bool done = S.done;
+        __syncthreads();                       // digit/before/done are rewritten next pass
+        if (done) break;
+    }
+    if (t == 0) S.count = 0;
+    __syncthreads();
+    for (int j = t; j < count; j += kSampleThreads) {
+        const uint64_t x = S.key[j];
+        if ((x & mask) <= prefix) {
+            const int pos = atomicAdd(&S.count, 1);
+            if (GLOBAL) publish_u64(out + pos, x);
+            else out[pos] = x;
+        }
+    }
+    __syncthreads();
+}
+
+// Ascending bitonic sort of S.key[0..n) (n a power of two <= kSampleSlice).
+__device__ void bitonic_sort(uint64_t* key, int n)
+{
+    for (int k = 2; k <= n; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < kSampleSlice; i += kSampleBlock) {
+            for (int i = threadIdx.x; i < n; i += kSampleThreads) {
                 const int ixj = i ^ j;
                 if (ixj > i) {
                     const uint64_t a = key[i], b = key[ixj];
-                    const bool up = (i & k) == 0;
-                    if ((a > b) == up) {
+                    if ((a > b) == ((i & k) == 0)) {
                         key[i] = b;
                         key[ixj] = a;
                     }
@@ -62,51 +162,6 @@ __device__ void bitonic_sort(uint64_t* key)
             __syncthreads();
         }
     }
-}
-
-__global__ __launch_bounds__(kBlock) void sample_copy_kernel(const float* logits, int n, float* values)
-{
-    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) values[i] = logits[i];
-}
-
-// A repeated id writes the same value again, so duplicates need no removal.
-__global__ __launch_bounds__(kBlock) void sample_penalty_kernel(const float* logits, int n, const int32_t* generated,
-                                                                int n_generated, float rp, float* values)
-{
-    for (int g = blockIdx.x * kBlock + threadIdx.x; g < n_generated; g += gridDim.x * kBlock) {
-        const int id = generated[g];
-        if (id < 0 || id >= n) continue;
-        const float x = logits[id];
-        values[id] = x > 0.0f ? x / rp : x * rp;
-    }
-}
-
-__global__ __launch_bounds__(kSampleBlock) void sample_block_kernel(const float* values, int n, float temperature,
-                                                                    int k, uint64_t* lists)
-{
-    __shared__ uint64_t key[kSampleSlice];
-    const int base = blockIdx.x * kSampleSlice;
-    for (int j = threadIdx.x; j < kSampleSlice; j += kSampleBlock) {
-        const int i = base + j;
-        key[j] = i < n ? sample_key(values[i] / temperature, i) : ~uint64_t(0);
-    }
-    __syncthreads();
-    bitonic_sort(key);
-    for (int j = threadIdx.x; j < k; j += kSampleBlock) lists[size_t(blockIdx.x) * k + j] = key[j];
-}
-
-// Block b joins lists [b*group, min((b+1)*group, nlists)) of k keys each.
-__global__ __launch_bounds__(kSampleBlock) void sample_merge_kernel(const uint64_t* src, int nlists, int k, int group,
-                                                                    uint64_t* dst)
-{
-    __shared__ uint64_t key[kSampleSlice];
-    const int first = blockIdx.x * group;
-    const int count = (nlists - first < group ? nlists - first : group) * k;
-    const uint64_t* in = src + size_t(first) * k;
-    for (int j = threadIdx.x; j < kSampleSlice; j += kSampleBlock) key[j] = j < count ? in[j] : ~uint64_t(0);
-    __syncthreads();
-    bitonic_sort(key);
-    for (int j = threadIdx.x; j < k; j += kSampleBlock) dst[size_t(blockIdx.x) * k + j] = key[j];
 }
 
 // numpy's float32 add.reduce order (pairwise_sum of umath's loops_utils):
@@ -169,64 +224,129 @@ __device__ float pairwise_sum_f32(const float* a, int n)
     return ret;
 }
 
-__global__ __launch_bounds__(kSampleFinish) void sample_finish_kernel(const float* values, float temperature,
-                                                                      const uint64_t* list, int k, float top_p,
-                                                                      const double* u, int32_t* out_token,
-                                                                      int32_t* ids_out, float* probs_out)
+struct SampleParams {
+    const float* logits;
+    const int32_t* generated;
+    const double* u;
+    int32_t* out_token;
+    int32_t* ids_out;
+    float* probs_out;
+    uint64_t* cand;       // gridDim.x * k candidate keys
+    int* counter;         // zero between calls (the last block resets it)
+    int n, n_generated, k;
+    float rp, temperature, top_p;
+};
+
+// softmax / top-p / Generator.choice over the k sorted keys S.key[0..k).
+__device__ void sample_finish(SampleShared& S, const SampleParams& p)
 {
-    __shared__ int ids[kSampleMaxK];
-    __shared__ float p[kSampleMaxK];
-    __shared__ float drop[kSampleMaxK];
-    __shared__ float total;
     const int t = threadIdx.x;
-    // the k best values, recomputed exactly as the slice kernel computed them
-    const float top = values[int(uint32_t(list[0]))] / temperature;
-    for (int i = t; i < k; i += kSampleFinish) {
-        const int id = int(uint32_t(list[i]));
-        ids[i] = id;
-        p[i] = spec_expf(values[id] / temperature - top);
-    }
+    const int k = p.k;
+    float* prob = S.u.f.p;
+    float* drop = S.u.f.drop;
+    const float top = key_value(S.key[0]);
+    for (int i = t; i < k; i += kSampleThreads) prob[i] = spec_expf(key_value(S.key[i]) - top);
     __syncthreads();
-    if (t == 0) total = pairwise_sum_f32(p, k);
+    if (t == 0) S.total = pairwise_sum_f32(prob, k);
     __syncthreads();
-    for (int i = t; i < k; i += kSampleFinish) p[i] = p[i] / total;
+    for (int i = t; i < k; i += kSampleThreads) prob[i] = prob[i] / S.total;
     __syncthreads();
-    if (top_p < 1.0f) {
+    if (p.top_p < 1.0f) {
         if (t == 0) {
             float c = 0.0f;
             for (int i = 0; i < k; ++i) {
-                c = c + p[i];
-                drop[i] = c - p[i];
+                c = c + prob[i];
+                drop[i] = c - prob[i];
             }
         }
         __syncthreads();
-        for (int i = t; i < k; i += kSampleFinish)
-            if (drop[i] >= top_p) p[i] = 0.0f;
+        for (int i = t; i < k; i += kSampleThreads)
+            if (drop[i] >= p.top_p) prob[i] = 0.0f;
         __syncthreads();
-        if (t == 0) total = pairwise_sum_f32(p, k);
+        if (t == 0) S.total = pairwise_sum_f32(prob, k);
         __syncthreads();
-        for (int i = t; i < k; i += kSampleFinish) p[i] = p[i] / total;
+        for (int i = t; i < k; i += kSampleThreads) prob[i] = prob[i] / S.total;
         __syncthreads();
     }
     if (t == 0) {
-        // Generator.choice: cdf = cumsum(double(p)) / its last entry, the
+        // Generator.choice: cdf = cumsum(double(p)) / its last entry; the
         // token is ids[#{i : cdf_i <= u}]
         double last = 0.0;
-        for (int i = 0; i < k; ++i) last = last + double(p[i]);
-        const double draw = *u;
+        for (int i = 0; i < k; ++i) last = last + double(prob[i]);
+        const double draw = *p.u;
         double cdf = 0.0;
         int index = 0;
         for (int i = 0; i < k; ++i) {
-            cdf = cdf + double(p[i]);
+            cdf = cdf + double(prob[i]);
             if (cdf / last <= draw) index = i + 1;
         }
         if (index >= k) index = k - 1;
-        *out_token = ids[index];
+        *p.out_token = key_index(S.key[index]);
     }
-    if (ids_out)
-        for (int i = t; i < k; i += kSampleFinish) ids_out[i] = ids[i];
-    if (probs_out)
-        for (int i = t; i < k; i += kSampleFinish) probs_out[i] = p[i];
+    if (p.ids_out)
+        for (int i = t; i < k; i += kSampleThreads) p.ids_out[i] = key_index(S.key[i]);
+    if (p.probs_out)
+        for (int i = t; i < k; i += kSampleThreads) p.probs_out[i] = prob[i];
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleParams p)
+{
+    __shared__ SampleShared S;
+    const int t = threadIdx.x;
+    const int k = p.k;
+    const int base = blockIdx.x * kSampleSlice;
+    // 1. the slice's values, penalised
+    for (int j = t; j < kSampleSlice; j += kSampleThreads) {
+        const int i = base + j;
+        S.u.v[j] = i < p.n ? p.logits[i] : 0.0f;
+    }
+    __syncthreads();
+    if (p.rp != 1.0f) {
+        for (int g = t; g < p.n_generated; g += kSampleThreads) {
+            const int id = p.generated[g];
+            if (id < base || id >= base + kSampleSlice || id >= p.n) continue;
+            const float x = p.logits[id];
+            S.u.v[id - base] = x > 0.0f ? x / p.rp : x * p.rp;
+        }
+        __syncthreads();
+    }
+    // 2. keys, and this slice's k smallest into the candidate list
+    for (int j = t; j < kSampleSlice; j += kSampleThreads) {
+        const int i = base + j;
+        S.key[j] = i < p.n ? sample_key(S.u.v[j] / p.temperature, i) : pad_key(i);
+    }
+    __syncthreads();
+    select_k<true>(S, kSampleSlice, k, p.cand + size_t(blockIdx.x) * k);
+    // 3. the last block to finish reduces every slice's candidates
+    wait_all_memory();                         // this thread's candidate stores have completed
+    __syncthreads();
+    if (t == 0) S.ticket = atomicAdd(p.counter, 1);
+    __syncthreads();
+    if (S.ticket != int(gridDim.x) - 1) return;
+    const int total = int(gridDim.x) * k;
+    int have = 0;
+    for (int off = 0; off < total;) {
+        const int chunk = min(total - off, kSampleSlice - have);
+        for (int j = t; j < chunk; j += kSampleThreads) S.key[have + j] = read_u64(p.cand + off + j);
+        off += chunk;
+        const int count = have + chunk;
+        __syncthreads();
+        if (count > k) {
+            select_k<false>(S, count, k, S.u.f.win);
+            for (int j = t; j < k; j += kSampleThreads) S.key[j] = S.u.f.win[j];
+            __syncthreads();
+            have = k;
+        } else {
+            have = count;
+        }
+    }
+    int m = 1;
+    while (m < k) m <<= 1;
+    for (int j = k + t; j < m; j += kSampleThreads) S.key[j] = ~uint64_t(0);
+    __syncthreads();
+    bitonic_sort(S.key, m);
+    sample_finish(S, p);
+    if (t == 0) publish_i(p.counter, 0);
 }
 
 static size_t al256s(size_t v) { return (v + 255) & ~size_t(255); }
@@ -241,8 +361,7 @@ extern "C" size_t hq_sample_workspace_bytes(int n, int top_k)
 {
     if (n <= 0 || top_k <= 0) return 0;
     const int k = top_k < n ? top_k : n;
-    const size_t lists = al256s(size_t(sample_slices(n)) * size_t(k) * 8);
-    return al256s(size_t(n) * 4) + 2 * lists;
+    return 256 + al256s(size_t(sample_slices(n)) * size_t(k) * 8);   // counter, then candidates
 }
 
 extern "C" int hq_sample_token(const float* logits, int n, const int32_t* generated, int n_generated,
@@ -255,32 +374,23 @@ extern "C" int hq_sample_token(const float* logits, int n, const int32_t* genera
     if (top_k < 1 || top_k > kSampleMaxK) return HQ_ERR_ARG;
     if (!(temperature > 0.0f) || !(repetition_penalty > 0.0f) || !(top_p > 0.0f)) return HQ_ERR_ARG;
     if (reinterpret_cast<uintptr_t>(workspace) & 255u) return HQ_ERR_ALIGN;
-    const int k = top_k < n ? top_k : n;
-    int nlists = sample_slices(n);
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    SampleParams p;
+    p.logits = logits;
+    p.generated = generated;
+    p.u = u;
+    p.out_token = out_token;
+    p.ids_out = ids_out;
+    p.probs_out = probs_out;
+    p.n = n;
+    p.n_generated = n_generated;
+    p.k = top_k < n ? top_k : n;
+    p.rp = repetition_penalty;
+    p.temperature = temperature;
+    p.top_p = top_p;
+    const int blocks = sample_slices(n);
     char* ws = static_cast<char*>(workspace);
-    float* values = reinterpret_cast<float*>(ws);
-    const size_t list_bytes = al256s(size_t(nlists) * size_t(k) * 8);
-    uint64_t* a = reinterpret_cast<uint64_t*>(ws + al256s(size_t(n) * 4));
-    uint64_t* b = reinterpret_cast<uint64_t*>(ws + al256s(size_t(n) * 4) + list_bytes);
-    const int cb = (n + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL(sample_copy_kernel, dim3(cb < 1024 ? cb : 1024), dim3(kBlock), 0, s, logits, n, values);
-    if (repetition_penalty != 1.0f && n_generated > 0) {
-        const int gb = (n_generated + kBlock - 1) / kBlock;
-        hipLaunchKernelGGL(sample_penalty_kernel, dim3(gb < 64 ? gb : 64), dim3(kBlock), 0, s, logits, n, generated,
-                           n_generated, repetition_penalty, values);
-    }
-    hipLaunchKernelGGL(sample_block_kernel, dim3(nlists), dim3(kSampleBlock), 0, s, values, n, temperature, k, a);
-    const int group = kSampleSlice / k;       // >= 2 since k <= kSampleMaxK
-    while (nlists > 1) {
-        const int next = (nlists + group - 1) / group;
-        hipLaunchKernelGGL(sample_merge_kernel, dim3(next), dim3(kSampleBlock), 0, s, a, nlists, k, group, b);
-        uint64_t* swap = a;
-        a = b;
-        b = swap;
-        nlists = next;
-    }
-    hipLaunchKernelGGL(sample_finish_kernel, dim3(1), dim3(kSampleFinish), 0, s, values, temperature, a, k, top_p, u,
-                       out_token, ids_out, probs_out);
+    p.counter = reinterpret_cast<int*>(ws);     // at a fixed place: calls with any n and k share it
+    p.cand = reinterpret_cast<uint64_t*>(ws + 256);
+    hipLaunchKernelGGL(sample_kernel, dim3(blocks), dim3(kSampleThreads), 0, static_cast<hipStream_t>(stream), p);
     return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }

@@ -55,7 +55,11 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def _stream_handle(stream: torch.cuda.Stream | None) -> int | None:
-    return None if stream is None else stream.cuda_stream
+    """The HIP stream of `stream`, or torch's current stream when None (so
+    the op is ordered with the caller's other torch work)."""
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
 
 
 # --------------------------------------------------------------------------- projections
@@ -292,7 +296,9 @@ class LiteSparkQwen:
         """Consume one token and return its next-token logits (device tensor).
 
         The step is enqueued on ``state.stream``; the greedy (argmax) token
-        of the logits is written to ``state.token`` by the same step.
+        of the logits is written to ``state.token`` by the same step.  The
+        caller's current stream waits for the step, so work it enqueues
+        there (sample_logits, a copy) reads the finished logits.
         """
         self._check_token(token_id, state)
         with torch.cuda.stream(state.stream):
@@ -300,6 +306,7 @@ class LiteSparkQwen:
         check(_native.lib().hq_decode_step(ctypes.byref(self.struct), ctypes.byref(state.struct),
                                            state.stream.cuda_stream), "hq_decode_step")
         state.position += 1
+        torch.cuda.current_stream(self.device).wait_stream(state.stream)
         return state.logits
 
     def greedy_token(self, state: QwenDecodeState) -> int:
@@ -326,6 +333,62 @@ class LiteSparkQwen:
                 check(lib.hq_decode_step(ctypes.byref(self.struct), ctypes.byref(state.struct),
                                          state.stream.cuda_stream), "hq_decode_step")
         state.position += steps
+
+    def decode_sampled(self, state: QwenDecodeState, steps: int, args, generator, generated) -> list[int]:
+        """`steps` iterations of the reference's stochastic decode loop
+        (cpu_lightspark.py:869-880) with no host round trip per token: each
+        step forwards a token, samples the next one from its logits
+        (hq_sample_token, the policy of `args`) and feeds it back on the
+        device.
+
+        `generated` is the run's list of generated tokens; its last entry is
+        the token forwarded first (the reference appends a token before
+        forwarding it), and the penalty of step i sees the list plus the i
+        tokens sampled before.  Generator.choice consumes one
+        generator.random() per token, so the `steps` draws are taken here up
+        front, in the order the reference takes them.  Returns the sampled
+        tokens (the last one is left in ``state.token``, not yet forwarded).
+        The loop does not stop at end-of-turn tokens: the caller truncates.
+        """
+        if steps < 1:
+            return []
+        if state.position + steps > state.capacity:
+            raise ValueError("decode state capacity exhausted")
+        if len(generated) == 0:
+            raise ValueError("generated must end with the token to forward")
+        top_k = int(args.top_k)
+        if not 1 <= top_k <= SAMPLE_MAX_TOP_K:
+            raise ValueError(f"top_k must be in [1, {SAMPLE_MAX_TOP_K}] on the GPU sampler")
+        if not (np.isfinite(args.temperature) and args.temperature > 0 and np.isfinite(args.top_p)
+                and args.top_p > 0 and np.isfinite(args.repetition_penalty) and args.repetition_penalty > 0):
+            raise ValueError("temperature, top_p and repetition_penalty must be positive and finite")
+        vocab = int(self.config["vocab_size"])
+        history = np.asarray(list(generated), dtype=np.int64).reshape(-1)
+        if history.size and (history.min() < 0 or history.max() >= vocab):
+            raise IndexError("a generated id is outside the vocabulary")
+        n0 = int(history.size)
+        lib = _native.lib()
+        draws = np.array([generator.random() for _ in range(steps)], dtype=np.float64)
+        dev = self.device
+        with torch.cuda.stream(state.stream):
+            gen = torch.empty(n0 + steps, dtype=torch.int32, device=dev)
+            gen[:n0].copy_(torch.from_numpy(history.astype(np.int32)))
+            state.token.copy_(gen[n0 - 1:n0])
+            u = torch.from_numpy(draws).to(dev)
+        ws = _zeroed_workspace(("sample", dev.index), lib.hq_sample_workspace_bytes(vocab, top_k), dev)
+        model, st, stream = ctypes.byref(self.struct), ctypes.byref(state.struct), state.stream.cuda_stream
+        for i in range(steps):
+            check(lib.hq_decode_step(model, st, stream), "hq_decode_step")
+            out = gen[n0 + i:n0 + i + 1]
+            check(lib.hq_sample_token(state.logits.data_ptr(), vocab, gen.data_ptr(), n0 + i,
+                                      float(args.repetition_penalty), float(args.temperature), top_k,
+                                      float(args.top_p), u[i:].data_ptr(), out.data_ptr(), None, None,
+                                      ws.data_ptr(), stream), "hq_sample_token")
+            with torch.cuda.stream(state.stream):
+                state.token.copy_(out)
+        state.position += steps
+        state.synchronize()
+        return [int(t) for t in gen[n0:].cpu().tolist()]
 
     # -- the reference's per-op surface ---------------------------------------
     def _projection(self, projection: LiteSparkProjection, values, quantized: torch.Tensor,

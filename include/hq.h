@@ -108,9 +108,13 @@ int hq_argmax(const float* x, int n, int32_t* out_index, void* workspace, void* 
  * [0,n) are skipped); out_token int32 [1]; ids_out int32 [k] and probs_out
  * fp32 [k] (nullable) receive the ranked ids and final probabilities, k =
  * min(top_k, n).  1 <= top_k <= 2048, temperature > 0, repetition_penalty
- * > 0, top_p > 0 (>= 1: no top-p filtering).  `workspace`:
- * hq_sample_workspace_bytes(n, top_k) bytes, 256-byte aligned (no zero fill
- * needed). */
+ * > 0, top_p > 0 (>= 1: no top-p filtering).  One launch: each block
+ * radix-selects the top k of its 4096 logits, the last block to finish (a
+ * ticket counter in the workspace) selects and sorts the overall top k and
+ * draws.  `workspace`: hq_sample_workspace_bytes(n, top_k) bytes, 256-byte
+ * aligned, zero-filled before its first use; every call leaves the counter
+ * at zero, so a workspace serves later calls with any n and top_k it is
+ * large enough for.  Calls sharing a workspace must not overlap. */
 size_t hq_sample_workspace_bytes(int n, int top_k);
 int hq_sample_token(const float* logits, int n, const int32_t* generated, int n_generated,
                     float repetition_penalty, float temperature, int top_k, float top_p,

@@ -66,9 +66,9 @@ def test_sampler_rejects_bad_arguments_without_launching():
     assert call(n=0) == 1 and call(n_generated=-1) == 1
     assert call(workspace=ws + 4) == 2                                          # 256-byte alignment
     assert lib.hq_sample_token(None, 10, None, 0, 1.0, 1.0, 5, 1.0, p, p, None, None, ws, None) == 1
-    # values, then two candidate lists of k keys per 4096-value slice
-    assert lib.hq_sample_workspace_bytes(151936, 40) >= 151936 * 4 + 2 * 38 * 40 * 8
-    assert lib.hq_sample_workspace_bytes(10, 40) >= 10 * 4 + 2 * 10 * 8
+    # the ticket counter, then k candidate keys per 4096-logit slice
+    assert lib.hq_sample_workspace_bytes(151936, 40) >= 4 + 38 * 40 * 8
+    assert lib.hq_sample_workspace_bytes(10, 40) >= 4 + 10 * 8
 
 
 def test_sampler_host_checks():

@@ -266,3 +266,58 @@ def test_layer_kernel_graph_replays_continue_epochs(forward_golden):
     assert_bits_equal(to_host(a.logits), to_host(b.logits), "logits after 30 steps")
     a.check_status()
     b.check_status()
+
+
+class SamplerArgs:
+    argmax = False
+
+    def __init__(self, temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.08):
+        self.temperature, self.top_k, self.top_p = temperature, top_k, top_p
+        self.repetition_penalty = repetition_penalty
+
+
+def test_tiny_model_sampled_decode_matches_oracle(forward_golden):
+    # the reference's stochastic loop (cpu_lightspark.py:808-880): sample
+    # after the prompt with nothing generated, then append, forward, sample
+    from harsh4b_amd.lightspark import sample_logits
+    g = forward_golden
+    model = golden_model(g)
+    ref = oracle_of(model)
+    args = SamplerArgs(temperature=1.0, top_k=12, top_p=0.95, repetition_penalty=1.3)
+    prompt = [int(t) for t in g["tokens"][:4]]
+    steps = 10
+    st, rs = model.new_state(len(prompt) + steps), ref.new_state(len(prompt) + steps)
+    g_dev, g_ref = np.random.default_rng(9), np.random.default_rng(9)
+    for t in prompt:
+        logits = model.forward_token(t, st)
+        ref.forward_token(t, rs)
+    first = sample_logits(logits, [], args, g_dev)
+    want = [oracle.sample_token(rs.logits, [], 1.3, 1.0, 12, 0.95, g_ref.random())[0]]
+    assert first == want[0]
+    for _ in range(steps):
+        ref.forward_token(want[-1], rs)
+        want.append(oracle.sample_token(rs.logits, want, 1.3, 1.0, 12, 0.95, g_ref.random())[0])
+    got = [first] + model.decode_sampled(st, steps, args, g_dev, [first])
+    assert got == want
+    assert_bits_equal(to_host(st.logits), rs.logits, "logits after the loop")
+    assert g_dev.random() == g_ref.random()
+    st.check_status()
+
+
+def test_qwen3_4b_sampled_decode_matches_per_op_sampler(qwen):
+    # the device loop against forward_token + sample_logits per token, with
+    # the reference runner's default policy
+    from harsh4b_amd.lightspark import sample_logits
+    model, _ = qwen
+    args = SamplerArgs()
+    steps = 8
+    a, b = model.new_state(steps + 2), model.new_state(steps + 2)
+    g_a, g_b = np.random.default_rng(0), np.random.default_rng(0)
+    generated = [4242]
+    for _ in range(steps):
+        generated.append(sample_logits(model.forward_token(generated[-1], a), generated, args, g_a))
+    got = model.decode_sampled(b, steps, args, g_b, [4242])
+    assert got == generated[1:]
+    assert_bits_equal(to_host(a.logits), to_host(b.logits), "logits")
+    a.check_status()
+    b.check_status()
