@@ -423,12 +423,32 @@ def main():
         torch.cuda.synchronize()
         print(f"# filled {args.ctx} cache positions with N(0,1)", file=sys.stderr, flush=True)
     else:
-        prompt = np.random.default_rng(3).integers(0, int(cfg["vocab_size"]), args.ctx)
-        for t in prompt:
-            model.forward_token(int(t), state)
+        prompt = [int(t) for t in np.random.default_rng(3).integers(0, int(cfg["vocab_size"]), args.ctx)]
+        # the prompt through the batched prefill, and the same prompt token
+        # by token on a second state (the reference's loop), both timed
+        scratch = model.new_state(cap)
+        model.prefill(prompt[:2], scratch)          # first-use allocations and code loads
+        scratch.synchronize()
+        del scratch
+        t0 = time.perf_counter()
+        model.prefill(prompt, state)
         state.synchronize()
-        print(f"# prefilled {args.ctx} tokens", file=sys.stderr, flush=True)
+        prefill_s = time.perf_counter() - t0
+        loop_state = model.new_state(cap)
+        t0 = time.perf_counter()
+        for t in prompt:
+            model.forward_token(t, loop_state)
+        loop_state.synchronize()
+        loop_s = time.perf_counter() - t0
+        del loop_state
+        prefill_info = {"tokens": args.ctx, "ms_batched": round(prefill_s * 1e3, 2),
+                        "ms_token_loop": round(loop_s * 1e3, 2),
+                        "note": "wall time to logits of the last prompt token, one run each"}
+        print(f"# prefilled {args.ctx} tokens: batched {prefill_s * 1e3:.1f} ms, token loop "
+              f"{loop_s * 1e3:.1f} ms", file=sys.stderr, flush=True)
 
+    if long_ctx:
+        prefill_info = None
     policy = generator = None
     if args.workload == "sampled":
         from types import SimpleNamespace
@@ -516,6 +536,8 @@ def main():
                                   "GB/s": round(alg[k] / (per_kind_ms[k] * 1e-3) / 1e9, 1)}
                               for k in kinds},
     }
+    if prefill_info:
+        result["prefill"] = prefill_info
     if not args.no_cpu_baseline:
         print("# timing the CPU oracle baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(model, state, args.ctx, args.cpu_seconds)

@@ -72,6 +72,8 @@ _SIGNATURES = {
     "hq_step_layer_blocks": ([ctypes.POINTER(HqModel)], c_int),
     "hq_step_workspace_bytes": ([ctypes.POINTER(HqModel), c_int], c_size),
     "hq_decode_step": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), vp], c_int),
+    "hq_prefill_workspace_bytes": ([ctypes.POINTER(HqModel), c_int], c_size),
+    "hq_prefill": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), vp, c_int, c_int, vp, vp], c_int),
     "hq_step_gemv": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), c_int, c_int, vp], c_int),
     "hq_step_layers": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), vp], c_int),
     "hq_graph_capture": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), c_int, vp,

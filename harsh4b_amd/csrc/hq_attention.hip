@@ -97,8 +97,13 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         n = pos + 1;
     } else {
         pos = -1;
-        n = a.context;
+        n = a.context + int(blockIdx.z);     // query z of a batch sees z more positions
     }
+    // per-query regions of a batch (blockIdx.z = 0 outside PLAIN batches)
+    const size_t zq = size_t(blockIdx.z) * size_t(a.kv_heads) * G * D;
+    float* const out = a.out + zq;
+    float* const part = a.part + size_t(blockIdx.z) * size_t(a.kv_heads) * G * a.max_chunks * (D + 2);
+    int32_t* const counters = a.counters + size_t(blockIdx.z) * a.kv_heads;
     const int nc = (n + C - 1) / C;
     const int nsplit = (nc + CPB - 1) / CPB;
     if (split >= nsplit) return;
@@ -163,7 +168,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
             }
         }
     } else {
-        for (int i = tid; i < G * D; i += kBlock) q_s[i / D][i % D] = a.q[size_t(g * G) * D + i];
+        for (int i = tid; i < G * D; i += kBlock) q_s[i / D][i % D] = a.q[zq + size_t(g * G) * D + i];
     }
     __syncthreads();
 
@@ -305,7 +310,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                 L = __builtin_fmaf(al, l_s[h][ci], L);
                 O = __builtin_fmaf(al, o_s[ci][h][d], O);
             }
-            a.out[size_t(g * G + h) * D + d] = O * (1.0f / L);
+            out[size_t(g * G + h) * D + d] = O * (1.0f / L);
         }
         return;
     }
@@ -317,7 +322,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         for (int r = 0; r < PAIRS; ++r) {
             const int h = h0 + HSTEP * r;
             if (h >= G) continue;
-            float* pp = a.part + (size_t(g * G + h) * a.max_chunks + c) * pstride;
+            float* pp = part + (size_t(g * G + h) * a.max_chunks + c) * pstride;
             publish_f(pp + 2 + d, o_s[ci][h][d]);
             if (d == 0) { publish_f(pp, m_s[h][ci]); publish_f(pp + 1, l_s[h][ci]); }
         }
@@ -325,7 +330,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     wait_all_memory();
     __syncthreads();
     if (tid == 0) {
-        const int ticket = atomicAdd(a.counters + g, 1);
+        const int ticket = atomicAdd(counters + g, 1);
         last_flag = (ticket == nsplit - 1);
     }
     __syncthreads();
@@ -334,7 +339,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     for (int r = 0; r < PAIRS; ++r) {
         const int h = h0 + HSTEP * r;
         if (h >= G) continue;
-        const float* base = a.part + size_t(g * G + h) * a.max_chunks * pstride;
+        const float* base = part + size_t(g * G + h) * a.max_chunks * pstride;
         float M = -__builtin_inff();
         for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, read_f(base + size_t(cc) * pstride));
         float L = 0.0f, O = 0.0f;
@@ -347,9 +352,9 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
             L = __builtin_fmaf(al, lc, L);
             O = __builtin_fmaf(al, oc, O);
         }
-        a.out[size_t(g * G + h) * D + d] = O * (1.0f / L);
+        out[size_t(g * G + h) * D + d] = O * (1.0f / L);
     }
-    if (tid == 0) publish_i(a.counters + g, 0);
+    if (tid == 0) publish_i(counters + g, 0);
 }
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim)
@@ -369,7 +374,8 @@ template <int D, int GMAX, bool STEP>
 static hipError_t launch_attn(const AttnParams& a, hipStream_t s)
 {
     const int splits = (a.max_chunks + kChunksPerBlock - 1) / kChunksPerBlock;
-    hipLaunchKernelGGL((attention_kernel<D, GMAX, STEP, kChunksPerBlock>), dim3(a.kv_heads, splits),
+    const int batch = (!STEP && a.batch > 1) ? a.batch : 1;
+    hipLaunchKernelGGL((attention_kernel<D, GMAX, STEP, kChunksPerBlock>), dim3(a.kv_heads, splits, batch),
                        dim3(kBlock), 0, s, a);
     return hipGetLastError();
 }

@@ -315,6 +315,15 @@ static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, 
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+int gemm_padded_k(int k) { return padded_k(k); }
+int gemm_padded_m(int m) { return padded_m(m); }
+size_t gemm_scratch_bytes(int m, int n, int k) { return gemm_layout(m, n, k).q_off; }
+hipError_t gemm_run(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* out, int m, int n,
+                    int k, char* scratch, hipStream_t s)
+{
+    return run_gemm(x, act, w, ws, out, m, n, k, nullptr, scratch, s);
+}
+
 }  // namespace hq
 
 using namespace hq;

@@ -59,7 +59,10 @@ struct AttnParams {
     const int32_t* position;    // STEP: device position (context = pos + 1)
     int32_t capacity;           // STEP: bound for the KV write
     int32_t* status;            // STEP: error flag
-    int context;                // PLAIN
+    int context;                // PLAIN: positions of query 0
+    int batch;                  // PLAIN: queries (grid z); query z sees context + z positions,
+                                // reads q + z*heads*D, writes out + z*heads*D and uses its own
+                                // part / counters regions (max_chunks and kv_heads apart)
     int kv_heads, groups, head_dim;
     int max_chunks;             // grid.y
     float* part;                // [heads, max_chunks, head_dim + 2]
@@ -68,6 +71,17 @@ struct AttnParams {
 };
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);
+
+// ---- batched GEMM driver (hq_gemm.hip) ---------------------------------------
+// x: int8 activations de-interleaved per 8 columns (even columns, then odd),
+// gemm_padded_m(m) rows of gemm_padded_k(k) bytes (padding zero); act fp32
+// [m]; out fp32 [m, n] = ((float)acc * act) * ws.  scratch: gemm_scratch_bytes
+// (m, n, k), zero before first use (left zero by every call).
+int gemm_padded_k(int k);
+int gemm_padded_m(int m);
+size_t gemm_scratch_bytes(int m, int n, int k);
+hipError_t gemm_run(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* out, int m, int n,
+                    int k, char* scratch, hipStream_t s);
 hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s);
 
 // ---- persistent layer kernel ---------------------------------------------------

@@ -180,6 +180,7 @@ class QwenDecodeState:
         s.workspace = self.workspace.data_ptr()
         self.struct = s
         self._graph = None
+        self._prefill_ws = None
 
     def synchronize(self) -> None:
         self.stream.synchronize()
@@ -308,6 +309,40 @@ class LiteSparkQwen:
         state.position += 1
         torch.cuda.current_stream(self.device).wait_stream(state.stream)
         return state.logits
+
+    def prefill(self, token_ids, state: QwenDecodeState) -> torch.Tensor:
+        """Consume a prompt and return the logits after its last token, as a
+        loop of forward_token over it would (the reference's prompt loop,
+        cpu_lightspark.py:809-810, inference_runtime.py:177-181), with the
+        same bits: every token but the last goes through hq_prefill (layer by
+        layer for up to 128 tokens at once, the projections as int8 MFMA
+        GEMMs), the last through the decode step, which computes the logits
+        and the greedy token."""
+        ids = np.asarray(list(token_ids), dtype=np.int64).reshape(-1)
+        if ids.size == 0:
+            raise ValueError("prefill needs at least one token")
+        vocab = int(self.config["vocab_size"])
+        if ids.min() < 0 or ids.max() >= vocab:
+            raise ValueError("a prompt token ID is outside the vocabulary")
+        if state.position + ids.size > state.capacity:
+            raise ValueError("decode state capacity exhausted")
+        head = ids[:-1]
+        if head.size:
+            lib = _native.lib()
+            if state._prefill_ws is None:
+                nbytes = lib.hq_prefill_workspace_bytes(ctypes.byref(self.struct), state.capacity)
+                if nbytes == 0:
+                    raise ValueError("model shape is not supported by the batched prefill")
+                state._prefill_ws = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+            state.stream.wait_stream(torch.cuda.current_stream(self.device))   # the workspace's zero fill
+            with torch.cuda.stream(state.stream):
+                dev_ids = torch.from_numpy(head.astype(np.int32)).to(self.device)
+            check(lib.hq_prefill(ctypes.byref(self.struct), ctypes.byref(state.struct), dev_ids.data_ptr(),
+                                 int(head.size), int(state.position), state._prefill_ws.data_ptr(),
+                                 state.stream.cuda_stream), "hq_prefill")
+            dev_ids.record_stream(state.stream)
+            state.position += int(head.size)
+        return self.forward_token(int(ids[-1]), state)
 
     def greedy_token(self, state: QwenDecodeState) -> int:
         state.synchronize()

@@ -215,6 +215,21 @@ int hq_step_layer_blocks(const hq_model* model);
  * so the same launch sequence serves every position (graph-capturable). */
 int hq_decode_step(const hq_model* model, const hq_state* state, void* stream);
 
+/* Batched prefill: consume tokens[0..count) (device int32) at positions
+ * start .. start+count-1 layer by layer for up to 128 tokens at a time (the
+ * body projections as int8 MFMA GEMMs, attention batched over the tokens,
+ * each query seeing its own causal context), with the arithmetic of
+ * hq_decode_step, so the K/V rows written are the bits count steps would
+ * write.  No logits are computed: forward the prompt's last token with
+ * hq_decode_step.  Leaves *state->position = start + count.  Bad token IDs
+ * set HQ_STEP_BAD_TOKEN.  `workspace`: hq_prefill_workspace_bytes(model,
+ * state->capacity) bytes, 256-byte aligned, zero-filled before first use.
+ * Reference counterpart: the token-by-token prompt loop of
+ * cpu_lightspark.py:809-810 and inference_runtime.py:177-181. */
+size_t hq_prefill_workspace_bytes(const hq_model* model, int capacity);
+int hq_prefill(const hq_model* model, const hq_state* state, const int32_t* tokens, int count, int start,
+               void* workspace, void* stream);
+
 /* Launch one body GEMV of the step (the kernel the step launches) for one
  * layer on the state's buffers, so a kernel can be timed in isolation.
  * kind: 0 = RMSNorm+qkv, 1 = o + residual, 2 = RMSNorm+gate_up+SwiGLU,

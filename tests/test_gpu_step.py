@@ -321,3 +321,62 @@ def test_qwen3_4b_sampled_decode_matches_per_op_sampler(qwen):
     assert_bits_equal(to_host(a.logits), to_host(b.logits), "logits")
     a.check_status()
     b.check_status()
+
+
+def _prefill_vs_steps(model, prompt, cap, start_tokens=()):
+    """Batched prefill against forward_token per token: K/V rows, logits,
+    greedy token and position, bit for bit."""
+    a, b = model.new_state(cap), model.new_state(cap)
+    for t in start_tokens:                       # an earlier turn, decoded token by token
+        model.forward_token(int(t), a)
+        model.forward_token(int(t), b)
+    la = to_host(model.prefill(prompt, a)).copy()
+    for t in prompt:
+        lb = model.forward_token(int(t), b)
+    lb = to_host(lb).copy()
+    n = len(start_tokens) + len(prompt)
+    assert a.position == b.position == n
+    assert int(a.device_position.item()) == n
+    assert_bits_equal(to_host(a.keys)[:, :n].view(np.uint16), to_host(b.keys)[:, :n].view(np.uint16), "keys")
+    assert_bits_equal(to_host(a.values)[:, :n].view(np.uint16), to_host(b.values)[:, :n].view(np.uint16),
+                      "values")
+    assert_bits_equal(la, lb, "logits after the prompt")
+    assert model.greedy_token(a) == model.greedy_token(b)
+    a.check_status()
+    b.check_status()
+    return a
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 10])
+def test_tiny_model_prefill_matches_token_steps(forward_golden, n):
+    g = forward_golden
+    model = golden_model(g)
+    prompt = [int(t) for t in g["tokens"][:n]]
+    st = _prefill_vs_steps(model, prompt, 16)
+    # and against the oracle
+    ref = oracle_of(model)
+    rs = ref.new_state(16)
+    for t in prompt:
+        ref.forward_token(t, rs)
+    assert_bits_equal(to_host(st.logits), rs.logits, "oracle logits")
+    _prefill_vs_steps(model, prompt, 24, start_tokens=[3, 4, 5])
+
+
+def test_tiny_model_prefill_flags_bad_tokens(forward_golden):
+    g = forward_golden
+    model = golden_model(g)
+    st = model.new_state(8)
+    with pytest.raises(ValueError, match="outside the vocabulary"):
+        model.prefill([1, int(g["config"]["vocab_size"])], st)
+    with pytest.raises(ValueError, match="capacity"):
+        model.prefill(list(range(9)), st)
+    assert st.position == 0
+
+
+def test_qwen3_4b_prefill_matches_token_steps(qwen):
+    # 200 tokens: two batches of the prefill (128 + 71), contexts up to four
+    # attention splits, the layer kernel for the comparison steps
+    model, _ = qwen
+    rng = np.random.default_rng(21)
+    prompt = [int(t) for t in rng.integers(0, 151936, 200)]
+    _prefill_vs_steps(model, prompt, 208, start_tokens=[11, 12])
