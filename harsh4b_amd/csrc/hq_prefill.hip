@@ -25,6 +25,7 @@
 namespace hq {
 
 constexpr int kPrefillBatch = 128;      // tokens per pass over the layers
+constexpr int kPrefillMaxWidth = 10240; // intermediate size the SwiGLU row kernel holds in LDS
 
 enum RowMode { ROW_NORM = 0, ROW_RESID_NORM = 1, ROW_PLAIN = 2, ROW_SWIGLU = 3 };
 
@@ -104,13 +105,27 @@ __global__ __launch_bounds__(kBlock) void prefill_rows_kernel(RowParams p)
         const float total = block_tree_sum256(ss, red);
         r = __builtin_sqrtf(total / float(p.k) + p.eps);
     }
-    float amax = 0.0f;
-    for (int i = tid; i < p.k; i += kBlock) amax = fmaxf(amax, fabsf(row_value<MODE>(p, m, i, r)));
-    amax = block_max_nonneg(amax, red);
-    amax = fmaxf(amax, 1e-5f);
-    const float inv = 127.0f / amax;
     int8_t* qr = p.q + size_t(m) * p.kp;
-    for (int i = tid; i < p.k; i += kBlock) qr[deint_offset(i)] = quant_i8(row_value<MODE>(p, m, i, r), inv);
+    float amax = 0.0f;
+    if constexpr (MODE == ROW_SWIGLU) {
+        // the SwiGLU values (one exp each) are kept in LDS for the quant pass
+        __shared__ float vals[kPrefillMaxWidth];
+        for (int i = tid; i < p.k; i += kBlock) {
+            const float v = row_value<MODE>(p, m, i, r);
+            vals[i] = v;
+            amax = fmaxf(amax, fabsf(v));
+        }
+        amax = block_max_nonneg(amax, red);
+        amax = fmaxf(amax, 1e-5f);
+        const float inv = 127.0f / amax;
+        for (int i = tid; i < p.k; i += kBlock) qr[deint_offset(i)] = quant_i8(vals[i], inv);
+    } else {
+        for (int i = tid; i < p.k; i += kBlock) amax = fmaxf(amax, fabsf(row_value<MODE>(p, m, i, r)));
+        amax = block_max_nonneg(amax, red);
+        amax = fmaxf(amax, 1e-5f);
+        const float inv = 127.0f / amax;
+        for (int i = tid; i < p.k; i += kBlock) qr[deint_offset(i)] = quant_i8(row_value<MODE>(p, m, i, r), inv);
+    }
     if (tid == 0) p.act[m] = amax / 127.0f;
 }
 
@@ -219,6 +234,7 @@ static bool prefill_fits(const hq_model* m)
 {
     return m && m->layer && m->head_dim == 128 && m->kv_heads > 0 && m->heads % m->kv_heads == 0 &&
            m->heads / m->kv_heads <= 8 && (m->hidden & 31) == 0 && (m->intermediate & 31) == 0 &&
+           m->intermediate <= kPrefillMaxWidth &&
            m->hidden > 0 && m->intermediate > 0 && m->vocab > 0;
 }
 
