@@ -120,7 +120,7 @@ class HipLiteSparkRuntime(Runtime):
     def __init__(self, model, tokenizer, rng=None):
         import torch
         self.model, self.tokenizer = model, tokenizer
-        self.rng = rng if rng is not None else np.random.mtrand._rand
+        self.rng = rng if rng is not None else np.random     # np.random.random_sample: the global RandomState
         self.hardware = torch.cuda.get_device_name(model.device)
 
     @classmethod
@@ -141,7 +141,9 @@ class HipLiteSparkRuntime(Runtime):
     def sample(self, logits, generated, temperature):
         """sample_numpy (inference_runtime.py:144-163): penalty 1.15 on the
         generated ids, then argmax when temperature <= 0.01 (no draw), else
-        temperature, top-k 50, top-p 0.9 and np.random.choice's draw."""
+        temperature, top-k 50, top-p 0.9 and np.random.choice's draw.  (The
+        argmax branch ranks NaN after every number, where numpy's argmax
+        would pick the first NaN.)"""
         from .lightspark import sample_token
         if temperature <= GREEDY_TEMPERATURE:
             return sample_token(logits, generated, RUNTIME_REPETITION_PENALTY, 1.0, 1, 1.0, 0.0)[0]
