@@ -380,3 +380,13 @@ def test_qwen3_4b_prefill_matches_token_steps(qwen):
     rng = np.random.default_rng(21)
     prompt = [int(t) for t in rng.integers(0, 151936, 200)]
     _prefill_vs_steps(model, prompt, 208, start_tokens=[11, 12])
+
+
+def test_qwen3_4b_prefill_after_a_long_turn(qwen):
+    # a 300-token prompt after a 300-token earlier turn: query contexts 301-600
+    # (up to ten chunks, three attention splits), three prefill batches
+    model, _ = qwen
+    rng = np.random.default_rng(33)
+    earlier = [int(t) for t in rng.integers(0, 151936, 300)]
+    prompt = [int(t) for t in rng.integers(0, 151936, 300)]
+    _prefill_vs_steps(model, prompt, 604, start_tokens=earlier)
