@@ -464,7 +464,7 @@ constexpr int kMaxWidth = 40 * kBlock;   // 10240: register-resident activation 
 //   LM head  K 2560   8 lanes/row 10 chunks/lane 4748 tiles, persistent:
 //            2 blocks per CU loop over the tiles
 constexpr int kQkvLPR = 16, kOLPR = 32, kGateLPR = 8, kDownLPR = 32, kHeadLPR = 8;
-constexpr int kPersistBlocks = 512;
+constexpr int kPersistBlocks = 512;   // LM head: 39.0 us; 256 / 768 / 1024 blocks measured 47.4 / 40.2 / 45.4
 constexpr int kDefaultLPR = 32;
 constexpr int kDefaultRB = 4 * (kWave / kDefaultLPR);
 
