@@ -410,7 +410,8 @@ class LiteSparkQwen:
             gen[:n0].copy_(torch.from_numpy(history.astype(np.int32)))
             state.token.copy_(gen[n0 - 1:n0])
             u = torch.from_numpy(draws).to(dev)
-        ws = _zeroed_workspace(("sample", dev.index), lib.hq_sample_workspace_bytes(vocab, top_k), dev)
+        ws = _zeroed_workspace(("sample", dev.index), lib.hq_sample_workspace_bytes(vocab, top_k), dev,
+                               state.stream)
         model, st, stream = ctypes.byref(self.struct), ctypes.byref(state.struct), state.stream.cuda_stream
         for i in range(steps):
             check(lib.hq_decode_step(model, st, stream), "hq_decode_step")
@@ -473,13 +474,16 @@ def sample_logits(logits, generated, args, generator=None) -> int:
 _workspaces: dict[tuple, torch.Tensor] = {}
 
 
-def _zeroed_workspace(key: tuple, nbytes: int, device) -> torch.Tensor:
+def _zeroed_workspace(key: tuple, nbytes: int, device, stream=None) -> torch.Tensor:
     """A zero-filled device workspace kept for reuse under `key` (the library
-    returns the regions it needs zeroed to zero after every call)."""
+    returns the regions it needs zeroed to zero after every call).  The zero
+    fill runs on the current stream; a given `stream` is made to wait for it."""
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
+    if stream is not None:
+        stream.wait_stream(torch.cuda.current_stream(device))
     return ws
 
 
@@ -537,7 +541,7 @@ def gqa_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, ou
         raise ValueError("context outside the cache")
     lib = _native.lib()
     nbytes = lib.hq_gqa_workspace_bytes(context, kv_heads, groups, head_dim)
-    ws = _zeroed_workspace(("gqa", query.device.index), nbytes, query.device)
+    ws = _zeroed_workspace(("gqa", query.device.index), nbytes, query.device, stream)
     check(lib.hq_gqa_decode(query.data_ptr(), keys.data_ptr(), values.data_ptr(), ws.data_ptr(),
                             out.data_ptr(), context, kv_heads, groups, head_dim,
                             keys.stride(0), _stream_handle(stream)), "hq_gqa_decode")
@@ -554,7 +558,7 @@ def int4_i8_gemm(x_q: torch.Tensor, act_scales: torch.Tensor, projection: LiteSp
     lib = _native.lib()
     nbytes = lib.hq_gemm_workspace_bytes(m, projection.output_size, projection.input_size)
     ws = _zeroed_workspace(("gemm", x_q.device.index, m, projection.output_size,
-                            projection.input_size), nbytes, x_q.device)
+                            projection.input_size), nbytes, x_q.device, stream)
     check(lib.hq_int4_i8_gemm(x_q.data_ptr(), act_scales.data_ptr(), projection.weights.data_ptr(),
                               projection.scales.data_ptr(), out.data_ptr(), m, projection.output_size,
                               projection.input_size, _ptr(acc_out), ws.data_ptr(),
@@ -571,7 +575,7 @@ def quant_int4_gemm(x: torch.Tensor, projection: LiteSparkProjection, out: torch
     lib = _native.lib()
     nbytes = lib.hq_gemm_workspace_bytes(m, projection.output_size, projection.input_size)
     ws = _zeroed_workspace(("gemm", x.device.index, m, projection.output_size,
-                            projection.input_size), nbytes, x.device)
+                            projection.input_size), nbytes, x.device, stream)
     check(lib.hq_quant_int4_gemm(x.data_ptr(), projection.weights.data_ptr(), projection.scales.data_ptr(),
                                  out.data_ptr(), m, projection.output_size, projection.input_size,
                                  _ptr(q_out), _ptr(act_out), _ptr(acc_out), ws.data_ptr(),
@@ -586,7 +590,7 @@ def argmax(logits: torch.Tensor, stream=None) -> int:
     lib = _native.lib()
     n = logits.numel()
     ws = _zeroed_workspace(("argmax", logits.device.index), lib.hq_argmax_workspace_bytes(n),
-                           logits.device)
+                           logits.device, stream)
     out = torch.empty(1, dtype=torch.int32, device=logits.device)
     check(lib.hq_argmax(logits.data_ptr(), n, out.data_ptr(), ws.data_ptr(), _stream_handle(stream)),
           "hq_argmax")
@@ -627,7 +631,7 @@ def sample_token(logits: torch.Tensor, generated, repetition_penalty: float, tem
     device = logits.device
     k = min(int(top_k), n)
     lib = _native.lib()
-    ws = _zeroed_workspace(("sample", device.index), lib.hq_sample_workspace_bytes(n, k), device)
+    ws = _zeroed_workspace(("sample", device.index), lib.hq_sample_workspace_bytes(n, k), device, stream)
     gen = torch.from_numpy(ids).to(device) if ids.size else None
     draw = torch.tensor([float(u)], dtype=torch.float64, device=device)
     out = torch.empty(1, dtype=torch.int32, device=device)
