@@ -263,6 +263,17 @@ def test_sampler_ties_signs_and_penalty():
     assert check_sample(small, [], 1.0, 0.7, 1, 0.9, 0.999, "k=1")[0] == 1
 
 
+def test_sampler_long_history_and_penalty_below_one():
+    # 5000 generated ids (repeats included) spread over every 4096-logit
+    # slice; a penalty below 1 raises positive logits and lowers negative ones
+    rng = np.random.default_rng(17)
+    logits = (rng.standard_normal(151936) * 3).astype(np.float32)
+    generated = [int(t) for t in rng.integers(0, 151936, 4000)]
+    generated += generated[:1000]
+    for rp, k, p in ((1.08, 40, 0.9), (0.9, 64, 0.95), (1.5, 500, 1.0)):
+        check_sample(logits, generated, rp, 0.8, k, p, float(rng.random()), f"rp={rp} k={k}")
+
+
 def test_sample_logits_follows_the_generator():
     # sample_logits consumes the generator as Generator.choice does: one
     # random() per token, so the device run and the oracle draw the same u
