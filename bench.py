@@ -54,11 +54,12 @@ def parse():
     ap.add_argument("--gemv-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("decode", "sampled", "long", "batched", "gemv", "copy"),
+    ap.add_argument("--workload", choices=("decode", "sampled", "sample", "long", "batched", "gemv", "copy"),
                     default="decode",
                     help="decode: configs[2] (the reported line); sampled: the same decode with the "
                          "reference runner's default stochastic sampler (temperature 0.7, top-k 40, "
-                         "top-p 0.9, repetition penalty 1.08) on the GPU; long: configs[4], the same decode "
+                         "top-p 0.9, repetition penalty 1.08) on the GPU; sample: that sampler alone, per "
+                         "top-k; long: configs[4], the same decode "
                          "at context 4096 over an N(0,1) fp16 KV cache; batched: configs[3], the "
                          "body GEMMs of M = 8/16/32 sequences on int8 MFMA against M GEMVs; gemv: "
                          "configs[0], one fused quant + int4 GEMV 2560 -> 9728 over rotating weight "
@@ -352,6 +353,53 @@ def bench_batched(args):
     print(json.dumps(result), flush=True)
 
 
+def bench_sample(args):
+    """hq_sample_token alone over Qwen3-4B's vocabulary (151936 logits, 64
+    generated ids): mean time per call from HIP events over `--steps` calls,
+    at the reference runner's default policy (temperature 0.7, top-k 40,
+    top-p 0.9, penalty 1.08) and at other top-k."""
+    import torch
+    from harsh4b_amd import _native
+    lib = _native.lib()
+    dev = torch.device("cuda", 0)
+    n = 151936
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    logits = torch.randn(n, device=dev, generator=gen) * 3
+    ids = torch.randint(0, n, (64,), device=dev, dtype=torch.int32, generator=gen)
+    u = torch.tensor([0.37], dtype=torch.float64, device=dev)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream()
+    per_k = {}
+    for k in (40, 1, 64, 512, 2048):
+        ws = torch.zeros(lib.hq_sample_workspace_bytes(n, k), dtype=torch.uint8, device=dev)
+
+        def call():
+            if lib.hq_sample_token(logits.data_ptr(), n, ids.data_ptr(), 64, 1.08, 0.7, k, 0.9, u.data_ptr(),
+                                   out.data_ptr(), None, None, ws.data_ptr(), s.cuda_stream):
+                raise RuntimeError("hq_sample_token failed")
+        for _ in range(args.warmup):
+            call()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(args.steps):
+            call()
+        e1.record(s)
+        torch.cuda.synchronize()
+        per_k[k] = e0.elapsed_time(e1) * 1e3 / args.steps
+        print(f"# top_k {k:5d}: {per_k[k]:8.2f} us per token", file=sys.stderr, flush=True)
+    result = {"metric": "GPU stochastic sampler tokens/s (151936 logits, reference runner's default policy)",
+              "value": round(1e6 / per_k[40], 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+              "warmup": args.warmup, "ms_per_step": round(per_k[40] / 1e3, 5), "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+              "data": "synthetic: N(0,9) logits, 64 random generated ids",
+              "config": {"workload": "hq_sample_token alone: temperature 0.7, top-k 40, top-p 0.9, penalty 1.08"},
+              "us_per_token_by_top_k": {str(k): round(v, 2) for k, v in per_k.items()}}
+    print(json.dumps(result), flush=True)
+
+
 def bench_copy(args):
     """Calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: a plain copy
     of 256 MiB (256 MiB read + 256 MiB written per dispatch), so a counter's
@@ -391,6 +439,9 @@ def main():
         return
     if args.workload == "copy":
         bench_copy(args)
+        return
+    if args.workload == "sample":
+        bench_sample(args)
         return
     if args.workload == "batched":
         bench_batched(args)
