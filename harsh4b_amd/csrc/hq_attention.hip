@@ -399,35 +399,39 @@ hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s)
 
 using namespace hq;
 
-extern "C" size_t hq_gqa_workspace_bytes(int context, int kv_heads, int groups, int head_dim)
+extern "C" size_t hq_gqa_workspace_bytes(int score_stride, int kv_heads, int groups, int head_dim)
 {
-    if (context <= 0 || kv_heads <= 0 || groups <= 0 || head_dim <= 0) return 0;
-    const int nc = (context + kAttnChunk - 1) / kAttnChunk;
+    if (score_stride <= 0 || kv_heads <= 0 || groups <= 0 || head_dim <= 0) return 0;
+    const int nc = (score_stride + kAttnChunk - 1) / kAttnChunk;
     // arrival counters in the first 256 bytes (a fixed place, so one zeroed
-    // workspace serves every context up to the one it was sized for), then
-    // the chunk partials
+    // workspace serves every context up to score_stride), then the chunk
+    // partials
     return 256 + attention_workspace_floats(kv_heads * groups, nc, head_dim) * 4;
 }
 
+// The reference's argument list (litespark_int4.cpp:160-171): the K/V time
+// stride is kv_heads * head_dim (:172), and score_stride is the row stride of
+// its `scores` scratch, i.e. the context capacity that scratch was sized for
+// (cpu_lightspark.py:405 passes state.capacity).  Here the workspace takes
+// the scratch's place and is sized by the same number.
 extern "C" int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* values,
                              void* workspace, float* output, int context, int kv_heads,
-                             int groups, int head_dim, int kv_time_stride, void* stream)
+                             int groups, int head_dim, int score_stride, void* stream)
 {
     if (!query || !keys || !values || !workspace || !output) return HQ_ERR_ARG;
     if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return HQ_ERR_ALIGN;
     if (context <= 0 || kv_heads <= 0 || groups <= 0 || groups > 8) return HQ_ERR_ARG;
+    if (score_stride < context) return HQ_ERR_ARG;
     if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128) return HQ_ERR_ARG;
-    if (kv_time_stride < kv_heads * head_dim) return HQ_ERR_ARG;
     if (kv_heads * 256 > 256 * 64) return HQ_ERR_ARG;   // counters fit in 256 bytes
-    if ((reinterpret_cast<uintptr_t>(keys) & 15u) != 0 ||
-        (reinterpret_cast<uintptr_t>(values) & 15u) != 0 || (kv_time_stride % 8) != 0)
+    if ((reinterpret_cast<uintptr_t>(keys) & 15u) != 0 || (reinterpret_cast<uintptr_t>(values) & 15u) != 0)
         return HQ_ERR_ALIGN;
     const int nc = (context + kAttnChunk - 1) / kAttnChunk;
     AttnParams a{};
     a.q = query;
     a.keys = const_cast<uint16_t*>(keys);
     a.values = const_cast<uint16_t*>(values);
-    a.time_stride = kv_time_stride;
+    a.time_stride = kv_heads * head_dim;
     a.context = context;
     a.kv_heads = kv_heads;
     a.groups = groups;

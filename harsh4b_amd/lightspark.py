@@ -348,9 +348,15 @@ class LiteSparkQwen:
         state.synchronize()
         return int(state.token.item())
 
-    def decode_greedy(self, state: QwenDecodeState, steps: int, use_graph: bool = True) -> None:
+    def decode_greedy(self, state: QwenDecodeState, steps: int, use_graph: bool = True,
+                      check_status: bool = True) -> None:
         """Run `steps` greedy steps feeding each argmax token back on the device
-        (the token already in ``state.token`` is consumed first)."""
+        (the token already in ``state.token`` is consumed first).
+
+        With `check_status` (the default) the call waits for the steps and
+        raises if the device status word reports a bad token, an exhausted
+        cache or a persistent-kernel wait that gave up; a caller that times
+        the steps passes False and calls ``state.check_status()`` itself."""
         if state.position + steps > state.capacity:
             raise ValueError("decode state capacity exhausted")
         lib = _native.lib()
@@ -368,6 +374,8 @@ class LiteSparkQwen:
                 check(lib.hq_decode_step(ctypes.byref(self.struct), ctypes.byref(state.struct),
                                          state.stream.cuda_stream), "hq_decode_step")
         state.position += steps
+        if check_status:
+            state.check_status()
 
     def decode_sampled(self, state: QwenDecodeState, steps: int, args, generator, generated) -> list[int]:
         """`steps` iterations of the reference's stochastic decode loop
@@ -423,7 +431,7 @@ class LiteSparkQwen:
             with torch.cuda.stream(state.stream):
                 state.token.copy_(out)
         state.position += steps
-        state.synchronize()
+        state.check_status()
         return [int(t) for t in gen[n0:].cpu().tolist()]
 
     # -- the reference's per-op surface ---------------------------------------
@@ -474,10 +482,17 @@ def sample_logits(logits, generated, args, generator=None) -> int:
 _workspaces: dict[tuple, torch.Tensor] = {}
 
 
-def _zeroed_workspace(key: tuple, nbytes: int, device, stream=None) -> torch.Tensor:
-    """A zero-filled device workspace kept for reuse under `key` (the library
-    returns the regions it needs zeroed to zero after every call).  The zero
-    fill runs on the current stream; a given `stream` is made to wait for it."""
+def _zeroed_workspace(kind: tuple, nbytes: int, device, stream=None) -> torch.Tensor:
+    """A zero-filled device workspace kept for reuse (the library returns the
+    regions it needs zeroed to zero after every call).
+
+    Workspaces are keyed by the stream the call runs on as well as by `kind`:
+    calls on one stream run in order, while calls on two streams may overlap,
+    and overlapping calls on one workspace would share its ticket counters.
+    The zero fill runs on the current stream; a given `stream` is made to
+    wait for it."""
+    handle = (stream if stream is not None else torch.cuda.current_stream(device)).cuda_stream
+    key = (*kind, handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
@@ -534,17 +549,24 @@ def rmsnorm(x: torch.Tensor, gamma: torch.Tensor, eps: float, out: torch.Tensor 
 
 def gqa_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, out: torch.Tensor,
                context: int, kv_heads: int, groups: int, head_dim: int, stream=None) -> torch.Tensor:
-    """Fused GQA decode over an fp16 [time, kv_heads, head_dim] cache (hq_gqa_decode)."""
+    """Fused GQA decode over an fp16 [capacity, kv_heads, head_dim] cache
+    (hq_gqa_decode, the reference's litespark_gqa_decode call at
+    cpu_lightspark.py:394-406 with score_stride = the cache's capacity)."""
     if keys.dtype != torch.float16 or values.dtype != torch.float16:
         raise ValueError("keys/values must be float16")
-    if context < 1 or context > keys.shape[0]:
+    shape = (keys.shape[0], kv_heads, head_dim)
+    if (keys.dim() != 3 or tuple(keys.shape) != shape or tuple(values.shape) != shape
+            or not keys.is_contiguous() or not values.is_contiguous()):
+        raise ValueError("keys/values must be contiguous float16 [capacity, kv_heads, head_dim]")
+    capacity = int(keys.shape[0])
+    if context < 1 or context > capacity:
         raise ValueError("context outside the cache")
     lib = _native.lib()
-    nbytes = lib.hq_gqa_workspace_bytes(context, kv_heads, groups, head_dim)
+    nbytes = lib.hq_gqa_workspace_bytes(capacity, kv_heads, groups, head_dim)
     ws = _zeroed_workspace(("gqa", query.device.index), nbytes, query.device, stream)
     check(lib.hq_gqa_decode(query.data_ptr(), keys.data_ptr(), values.data_ptr(), ws.data_ptr(),
                             out.data_ptr(), context, kv_heads, groups, head_dim,
-                            keys.stride(0), _stream_handle(stream)), "hq_gqa_decode")
+                            capacity, _stream_handle(stream)), "hq_gqa_decode")
     return out
 
 

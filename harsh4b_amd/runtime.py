@@ -122,6 +122,7 @@ class HipLiteSparkRuntime(Runtime):
         self.model, self.tokenizer = model, tokenizer
         self.rng = rng if rng is not None else np.random     # np.random.random_sample: the global RandomState
         self.hardware = torch.cuda.get_device_name(model.device)
+        self._session = None    # the decode state of the last prefill/decode
 
     @classmethod
     def from_cache(cls, directory, norms, tokenizer, model_path=None, config=None, rng=None):
@@ -133,9 +134,11 @@ class HipLiteSparkRuntime(Runtime):
         """A fresh session holding the prompt; the prompt runs through the
         batched prefill (the same bits as the reference's token loop)."""
         state = self.model.new_state(len(ids) + max_tokens)
+        self._session = state
         return self.model.prefill(ids, state), state
 
     def decode(self, token, session):
+        self._session = session
         return self.model.forward_token(int(token), session)
 
     def sample(self, logits, generated, temperature):
@@ -146,10 +149,16 @@ class HipLiteSparkRuntime(Runtime):
         would pick the first NaN.)"""
         from .lightspark import sample_token
         if temperature <= GREEDY_TEMPERATURE:
-            return sample_token(logits, generated, RUNTIME_REPETITION_PENALTY, 1.0, 1, 1.0, 0.0)[0]
-        u = float(self.rng.random_sample())
-        return sample_token(logits, generated, RUNTIME_REPETITION_PENALTY, float(temperature), RUNTIME_TOP_K,
-                            RUNTIME_TOP_P, u)[0]
+            token = sample_token(logits, generated, RUNTIME_REPETITION_PENALTY, 1.0, 1, 1.0, 0.0)[0]
+        else:
+            u = float(self.rng.random_sample())
+            token = sample_token(logits, generated, RUNTIME_REPETITION_PENALTY, float(temperature),
+                                 RUNTIME_TOP_K, RUNTIME_TOP_P, u)[0]
+        # the token's step has finished (its logits were read): its status
+        # word says whether that step ran as specified
+        if self._session is not None:
+            self._session.check_status()
+        return token
 
     def memory_gib(self):
         import torch

@@ -71,21 +71,25 @@ int hq_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps, v
 /* ------------------------------------------- GQA decode attention --
  * Fused single-token GQA attention (score, softmax and V accumulation in
  * one kernel).  Replaces litespark_gqa_decode (cpu_kernels/
- * litespark_int4.cpp:160-171, bound at cpu_lightspark.py:102-111).
+ * litespark_int4.cpp:160-171, bound at cpu_lightspark.py:102-111) with the
+ * same argument list and meaning:
  * query fp32 [kv_heads*groups, head_dim], heads ordered [kv_head, group];
- * keys/values fp16 (IEEE binary16 bits) with element (t, h, d) at
- * t*kv_time_stride + h*head_dim + d (the reference's [time, kv_head, dim]
- * layout when kv_time_stride = kv_heads*head_dim); output fp32 like query.
- * `workspace` takes the place of the reference's `scores` scratch: at least
- * hq_gqa_workspace_bytes(context, ...) bytes, 256-byte aligned, zero-filled
- * before its first use; every call leaves its counter words at zero, so one
- * workspace serves any later call whose context needs no more bytes.
- * head_dim in {16, 32, 64, 128}; groups <= 8; context >= 1; keys and
- * values 16-byte aligned and kv_time_stride a multiple of 8. */
-size_t hq_gqa_workspace_bytes(int context, int kv_heads, int groups, int head_dim);
+ * keys/values fp16 (IEEE binary16 bits) [time, kv_heads, head_dim], element
+ * (t, h, d) at t*kv_heads*head_dim + h*head_dim + d (the time stride is
+ * derived as in litespark_int4.cpp:172); output fp32 like query.
+ * score_stride is the row stride of the reference's `scores` scratch
+ * [kv_heads*groups, score_stride] (the caller passes state.capacity,
+ * cpu_lightspark.py:405), so context <= score_stride.  `workspace` takes the
+ * place of that scratch: at least hq_gqa_workspace_bytes(score_stride, ...)
+ * bytes, 256-byte aligned, zero-filled before its first use; every call
+ * leaves its counter words at zero, so one workspace serves every later call
+ * with the same or a smaller score_stride.  Calls sharing a workspace must
+ * not overlap.  head_dim in {16, 32, 64, 128}; groups <= 8; context >= 1;
+ * keys and values 16-byte aligned. */
+size_t hq_gqa_workspace_bytes(int score_stride, int kv_heads, int groups, int head_dim);
 int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* values,
                   void* workspace, float* output, int context, int kv_heads, int groups,
-                  int head_dim, int kv_time_stride, void* stream);
+                  int head_dim, int score_stride, void* stream);
 
 /* ------------------------------------------------------- argmax --
  * Device argmax with np.argmax's order: the first maximal index, a NaN

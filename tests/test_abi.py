@@ -36,6 +36,7 @@ def test_status_strings_and_version():
 
 
 def test_host_validation_rejects_bad_shapes_without_launching():
+    import ctypes
     # These return before any HIP call, so they run without a GPU.
     from harsh4b_amd import _native
     lib = _native.lib()
@@ -43,6 +44,15 @@ def test_host_validation_rejects_bad_shapes_without_launching():
     assert lib.hq_quant_int4_gemv(None, None, None, None, 4, 0, None, None, None, None) == 1
     assert lib.hq_int4_i8_gemv(None, None, None, 1.0, None, 0, 64, None) == 0    # empty: no-op
     assert lib.hq_gqa_decode(None, None, None, None, None, 1, 1, 1, 16, 16, None) == 1
+    # score_stride (the reference's scores row stride, state.capacity) below
+    # the context is refused before any launch
+    buf = ctypes.create_string_buffer(1024)
+    p = ctypes.addressof(buf)
+    ws = (p + 255) & ~255
+    assert lib.hq_gqa_decode(p, p, p, ws, p, 10, 8, 4, 128, 9, None) == 1
+    assert lib.hq_gqa_decode(p, p, p, ws + 16, p, 10, 8, 4, 128, 10, None) == 2
+    # the workspace is sized by score_stride, like the reference's scores
+    assert lib.hq_gqa_workspace_bytes(4096, 8, 4, 128) == 256 + 32 * 64 * 130 * 4
     assert lib.hq_gemm_workspace_bytes(0, 1, 1) == 0
     assert lib.hq_gqa_workspace_bytes(64, 8, 4, 128) >= 32 * 130 * 4
 

@@ -197,6 +197,33 @@ def test_gqa_repeated_calls_reuse_workspace():
         assert_bits_equal(to_host(out), ref, f"repeat ctx={ctx}")
 
 
+def test_gqa_reference_call_values():
+    # hq_gqa_decode called through the C ABI with exactly the integers the
+    # reference's _attention passes (cpu_lightspark.py:394-406): context =
+    # position + 1, kv_heads, groups, head_dim, score_stride = state.capacity,
+    # on one layer of a [layers, capacity, kv_heads, head_dim] cache
+    import ctypes
+    from harsh4b_amd import _native
+    lib = _native.lib()
+    rng = np.random.default_rng(405)
+    layers, capacity, kv, g, d = 3, 300, 8, 4, 128
+    keys = rng.standard_normal((layers, capacity, kv, d)).astype(np.float16)
+    values = rng.standard_normal((layers, capacity, kv, d)).astype(np.float16)
+    kd, vd = to_dev(keys), to_dev(values)
+    ws = torch.zeros(lib.hq_gqa_workspace_bytes(capacity, kv, g, d), dtype=torch.uint8, device=dev())
+    for layer, position in ((0, 0), (2, 137), (1, capacity - 1)):
+        end = position + 1
+        q = rng.standard_normal((kv * g, d)).astype(np.float32)
+        out = torch.empty((kv * g, d), dtype=torch.float32, device=dev())
+        status = lib.hq_gqa_decode(to_dev(q).data_ptr(), kd[layer].data_ptr(), vd[layer].data_ptr(),
+                                   ws.data_ptr(), out.data_ptr(), end, kv, g, d, capacity,
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert status == 0
+        ref = oracle.gqa_decode_split(q, keys[layer].view(np.uint16), values[layer].view(np.uint16), end,
+                                      kv, g, d)
+        assert_bits_equal(to_host(out), ref, f"gqa layer={layer} end={end}")
+
+
 # ------------------------------------------------------------------ argmax
 def test_device_argmax_order(kat):
     ls = lightspark()
@@ -299,8 +326,10 @@ def test_sample_logits_follows_the_generator():
 
 # ------------------------------------------------------------------ batched
 @pytest.mark.parametrize("m", [1, 8, 16, 32, 40])
-@pytest.mark.parametrize("rows,width", [(2560, 9728), (6144, 2560), (100, 96)])
+@pytest.mark.parametrize("rows,width", [(2560, 9728), (6144, 2560), (2560, 4096), (19456, 2560), (100, 96)])
 def test_batched_gemm_bit_exact(m, rows, width):
+    # Qwen3-4B's down, qkv, o (K split across blocks) and gate_up (unsplit,
+    # 304 row tiles) shapes, and a ragged one
     ls = lightspark()
     rng = np.random.default_rng(m * 31 + rows)
     w = random_int4(rng, rows, width)

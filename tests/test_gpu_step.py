@@ -145,9 +145,11 @@ def test_qwen3_4b_first_tokens_bit_exact(qwen):
     st.check_status()
 
 
-@pytest.mark.parametrize("ctx", [100, 130, 300, 4000])
+@pytest.mark.parametrize("ctx", [100, 130, 300, 4000, 4096, 4097])
 def test_qwen3_4b_long_context_bit_exact(qwen, ctx):
-    # an fp16 N(0,1) cache of `ctx` positions on both sides, then two steps
+    # an fp16 N(0,1) cache of `ctx` positions on both sides, then two steps.
+    # ctx 4000: 63-chunk contexts; 4096 and 4097: 65 and 66 chunks of 64
+    # positions, more attention items than one round of blocks
     model, ref = qwen
     cap = ctx + 2
     st = model.new_state(cap)
