@@ -62,6 +62,7 @@ _SIGNATURES = {
     "hq_rmsnorm": ([vp, vp, vp, c_int, c_float, vp], c_int),
     "hq_gqa_workspace_bytes": ([c_int, c_int, c_int, c_int], c_size),
     "hq_gqa_decode": ([vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int, vp], c_int),
+    "hq_gqa_decode_noalloc": ([vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int, vp], c_int),
     "hq_argmax_workspace_bytes": ([c_int], c_size),
     "hq_argmax": ([vp, c_int, vp, vp, vp], c_int),
     "hq_sample_workspace_bytes": ([c_int, c_int], c_size),

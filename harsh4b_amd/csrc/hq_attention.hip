@@ -23,6 +23,8 @@
 //           o[d] = fmaf chain of e_t * v_t[d] over ascending t;
 //   combine M = max m_c; a_c = exp(m_c - M); L and O[d] as fmaf chains over
 //           ascending c; out = O * (1 / L).
+#include <mutex>
+
 #include "hq_device.h"
 #include "hq_internal.h"
 
@@ -409,23 +411,23 @@ extern "C" size_t hq_gqa_workspace_bytes(int score_stride, int kv_heads, int gro
     return 256 + attention_workspace_floats(kv_heads * groups, nc, head_dim) * 4;
 }
 
-// The reference's argument list (litespark_int4.cpp:160-171): the K/V time
-// stride is kv_heads * head_dim (:172), and score_stride is the row stride of
-// its `scores` scratch, i.e. the context capacity that scratch was sized for
-// (cpu_lightspark.py:405 passes state.capacity).  Here the workspace takes
-// the scratch's place and is sized by the same number.
-extern "C" int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* values,
-                             void* workspace, float* output, int context, int kv_heads,
-                             int groups, int head_dim, int score_stride, void* stream)
+// Checks and launch shared by hq_gqa_decode and hq_gqa_decode_noalloc.
+static int gqa_check(const float* query, const uint16_t* keys, const uint16_t* values, const float* output,
+                     int context, int kv_heads, int groups, int head_dim, int score_stride)
 {
-    if (!query || !keys || !values || !workspace || !output) return HQ_ERR_ARG;
-    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return HQ_ERR_ALIGN;
+    if (!query || !keys || !values || !output) return HQ_ERR_ARG;
     if (context <= 0 || kv_heads <= 0 || groups <= 0 || groups > 8) return HQ_ERR_ARG;
     if (score_stride < context) return HQ_ERR_ARG;
     if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128) return HQ_ERR_ARG;
     if (kv_heads * 256 > 256 * 64) return HQ_ERR_ARG;   // counters fit in 256 bytes
     if ((reinterpret_cast<uintptr_t>(keys) & 15u) != 0 || (reinterpret_cast<uintptr_t>(values) & 15u) != 0)
         return HQ_ERR_ALIGN;
+    return HQ_OK;
+}
+
+static int gqa_launch(const float* query, const uint16_t* keys, const uint16_t* values, void* workspace,
+                      float* output, int context, int kv_heads, int groups, int head_dim, hipStream_t stream)
+{
     const int nc = (context + kAttnChunk - 1) / kAttnChunk;
     AttnParams a{};
     a.q = query;
@@ -440,6 +442,79 @@ extern "C" int hq_gqa_decode(const float* query, const uint16_t* keys, const uin
     a.counters = static_cast<int32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
     a.out = output;
-    const hipError_t e = launch_attention(a, false, static_cast<hipStream_t>(stream));
+    const hipError_t e = launch_attention(a, false, stream);
     return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+// The reference's argument list (litespark_int4.cpp:160-171): the K/V time
+// stride is kv_heads * head_dim (:172), and score_stride is the row stride of
+// its `scores` scratch, i.e. the context capacity that scratch was sized for
+// (cpu_lightspark.py:405 passes state.capacity).  Here the workspace takes
+// the scratch's place and is sized by the same number.
+extern "C" int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* values,
+                             void* workspace, float* output, int context, int kv_heads,
+                             int groups, int head_dim, int score_stride, void* stream)
+{
+    const int st = gqa_check(query, keys, values, output, context, kv_heads, groups, head_dim, score_stride);
+    if (st != HQ_OK) return st;
+    if (!workspace) return HQ_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return HQ_ERR_ALIGN;
+    return gqa_launch(query, keys, values, workspace, output, context, kv_heads, groups, head_dim,
+                      static_cast<hipStream_t>(stream));
+}
+
+// ---- the variant that allocates nothing ----------------------------------------
+//
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops that forbid hipMalloc): hq_gqa_decode with its
+// workspace in a file-scope device array instead of a caller buffer.  Each
+// GPU holds its own copy of `scratch` until the process ends.  The array's
+// name is only a host-side stand-in: its device address is taken with
+// hipGetSymbolAddress once per device, with that device current, and that
+// address is what the kernels receive.  Every call on a device shares the
+// device's array, so calls that overlap on one GPU race.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+// The device address of this device's `scratch` (nullptr on failure).
+static void* scratch_address(int dev)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+// Zero the arrival counters: a kernel, not hipMemsetAsync, so the call can
+// be captured into a graph.  The attention kernel leaves them at zero again,
+// so this only matters after an overlapping call left them inconsistent.
+__global__ void zero_counters_kernel(int32_t* c, int n)
+{
+    if (int(threadIdx.x) < n) c[threadIdx.x] = 0;
+}
+
+extern "C" int hq_gqa_decode_noalloc(const float* query, const uint16_t* keys, const uint16_t* values,
+                                     float* output, int context, int kv_heads, int groups, int head_dim,
+                                     int score_stride, void* stream)
+{
+    const int st = gqa_check(query, keys, values, output, context, kv_heads, groups, head_dim, score_stride);
+    if (st != HQ_OK) return st;
+    // the bytes this call uses (its context's chunk partials), not the
+    // score_stride sizing of the caller-workspace form
+    if (hq_gqa_workspace_bytes(context, kv_heads, groups, head_dim) > kNoAllocScratchBytes) return HQ_ERR_ARG;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return HQ_ERR_DEVICE;
+    void* ws = scratch_address(dev);
+    if (ws == nullptr) return HQ_ERR_DEVICE;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(zero_counters_kernel, dim3(1), dim3(64), 0, s, static_cast<int32_t*>(ws), 64);
+    if (hipGetLastError() != hipSuccess) return HQ_ERR_LAUNCH;
+    return gqa_launch(query, keys, values, ws, output, context, kv_heads, groups, head_dim, s);
 }

@@ -91,6 +91,21 @@ int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* valu
                   void* workspace, float* output, int context, int kv_heads, int groups,
                   int head_dim, int score_stride, void* stream);
 
+/* hq_gqa_decode without the workspace argument: the variant that allocates
+ * nothing.  No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  Same arguments, checks and results as hq_gqa_decode;
+ * the workspace is a 4 MiB file-scope device array that each GPU holds until
+ * the process ends, so the call returns HQ_ERR_ARG when
+ * hq_gqa_workspace_bytes(context, kv_heads, groups, head_dim) exceeds 4 MiB
+ * (32 query heads of 128 dims: context <= 16128).  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU race.  Each call launches a
+ * small kernel that zeroes the array's counter words before the attention
+ * kernel; no hipMalloc, hipFree or memset is called. */
+int hq_gqa_decode_noalloc(const float* query, const uint16_t* keys, const uint16_t* values,
+                          float* output, int context, int kv_heads, int groups, int head_dim,
+                          int score_stride, void* stream);
+
 /* ------------------------------------------------------- argmax --
  * Device argmax with np.argmax's order: the first maximal index, a NaN
  * beating every number (cpu_lightspark.py:704-705, the greedy branch of
