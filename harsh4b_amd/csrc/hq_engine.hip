@@ -15,10 +15,16 @@
 // Grid: one 1024-thread block per CU, co-resident by construction (at most
 // one block per CU, never more blocks than CUs).  Each block owns a slice of
 // the output rows of every GEMV.  A phase's output vector is handed to every
-// block as 64-bit entries {fp32 value, 32-bit epoch} written with
-// agent-scope stores and read with agent-scope loads until every epoch is
-// current; epochs grow by 5 per layer from a counter kept in the workspace,
-// so no buffer is cleared between steps.
+// block as 32-bit hand-off words written with agent-scope stores and read
+// with agent-scope loads until they are non-zero.  A word holds the value's
+// bits XOR kHsKey, the bits of a signalling NaN, which no arithmetic result
+// has, so an empty (zero) word and a published value never coincide.  Every
+// layer of a launch has its own slot of words, in one of two sets
+// alternating by launch: a launch clears the other set (written by the
+// previous launch, which has finished) layer by layer, and the launch
+// boundary makes those clears visible before the set is used again.  A
+// counter in the workspace (5 epochs per layer) selects the set and tags the
+// long-context attention partials, which stay 64-bit {value, epoch} entries.
 //
 // Wave roles (warp specialisation, no block barrier inside the layer loop):
 //  * Weight waves (waves 4-15) hold their rows of the coming GEMVs in
@@ -104,11 +110,8 @@ struct EngineParams {
     const int32_t* position;
     int32_t* status;
     float* x;                 // residual stream: embedding in, final out
-    uint64_t* ll_x3;          // [H] x after o + residual
-    uint64_t* ll_x5;          // [H] x after down + residual
-    uint64_t* ll_qkv;         // [qkv_rows]
-    uint64_t* ll_att;         // [heads * D]
-    uint64_t* ll_act;         // [I] SwiGLU output
+    uint32_t* hs;             // hand-off words: 2 sets x L layers x hs_layer words
+    int hs_layer;             // words per layer: x3 [H], x5 [H], qkv [qkv_rows], att [heads*D], act [I]
     uint32_t* epoch;
     uint64_t* ll_part;        // attention chunk partials [heads, max_chunks, D + 2] (m, l, o)
     int max_chunks;
@@ -219,7 +222,37 @@ __device__ __forceinline__ void ibar(int& seq, unsigned& budget, int32_t* status
 #define TRACE(l, point) do { } while (0)
 #endif
 
-// ---- global hand-off entries ---------------------------------------------------
+// ---- global hand-off words ------------------------------------------------------
+
+constexpr uint32_t kHsKey = 0x7FA5A5A5u;   // a signalling-NaN pattern (quiet bit clear)
+
+__device__ __forceinline__ void hs_store(uint32_t* p, float v)
+{
+    __hip_atomic_store(p, f32_bits(v) ^ kHsKey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool hs_ready(uint32_t w) { return w != 0u; }
+__device__ __forceinline__ float hs_value(uint32_t w) { return bits_f32(w ^ kHsKey); }
+
+// One layer's slot of hand-off words in the launch's set: x3 [H], x5 [H],
+// qkv [qkv_rows], att [heads*D], act [I].  Only the slot base is carried;
+// the vector addresses are recomputed where they are used (a few scalar
+// instructions), which holds fewer registers across the layer loop.
+struct Slot {
+    uint32_t* base;
+    int H, qkv_rows, qd;
+    __device__ __forceinline__ uint32_t* x3() const { return base; }
+    __device__ __forceinline__ uint32_t* x5() const { return base + H; }
+    __device__ __forceinline__ uint32_t* qkv() const { return base + 2 * H; }
+    __device__ __forceinline__ uint32_t* att() const { return base + 2 * H + qkv_rows; }
+    __device__ __forceinline__ uint32_t* act() const { return base + 2 * H + qkv_rows + qd; }
+};
+__device__ __forceinline__ Slot slot_of(const EngineParams& p, int set, int l)
+{
+    return Slot{p.hs + (size_t(set) * size_t(p.L) + size_t(l)) * size_t(p.hs_layer), p.H, p.qkv_rows,
+                p.heads * 128};
+}
+
+// ---- 64-bit {value, epoch} entries (attention chunk partials) -------------------
 
 __device__ __forceinline__ void ll_store(uint64_t* p, float v, uint32_t epoch)
 {
@@ -249,6 +282,10 @@ __device__ __forceinline__ bool ll_ready(uint64_t v, uint32_t epoch)
 {
     return int32_t(uint32_t(v >> 32) - epoch) >= 0;
 }
+__device__ __forceinline__ uint32_t hs_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kBufSC1);
+}
 
 __device__ __forceinline__ int split_begin(int n, int b, int nb) { return int((long long)n * b / nb); }
 
@@ -269,30 +306,30 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const
 // stores, and fewer watchers measured faster hand-offs (64 watching lanes
 // per block 929 us per launch of all 36 layers, 16 lanes 899 us, 4 lanes
 // 877 us, 1 lane 861 us).
-__device__ __forceinline__ void watch_last(const uint64_t* src, int n, uint32_t epoch, unsigned& budget,
-                                             int32_t* status)
+__device__ __forceinline__ void watch_last(const uint32_t* src, int n, unsigned& budget, int32_t* status)
 {
     if (opaque_tid() == 0 && n > 0) {
         const __amdgpu_buffer_rsrc_t r = buffer_rsrc(src);
-        const uint32_t off = uint32_t(n - 1) * 8u;
-        uint64_t w = ll_load(r, off, 0);
+        const uint32_t off = uint32_t(n - 1) * 4u;
+        uint32_t w = hs_load(r, off, 0);
         unsigned spins = 0;
-        while (!ll_ready(w, epoch) && budget != 0) {
+        while (!hs_ready(w) && budget != 0) {
             __builtin_amdgcn_s_sleep(1);
             if (++spins == kSpinLimit) { budget = 0; atomicOr(status, HQ_STEP_SYNC); }
             compiler_fence();
-            w = ll_load(r, off, 0);
+            w = hs_load(r, off, 0);
         }
     }
 }
 
-// Input thread t polls entries t, t+256, ... of src[0, n) until their epoch is
-// current and returns their values in out[] (0 past n).  All loads are in
+// 64-bit {value, epoch} entries (the attention chunk partials): thread t
+// polls entries t, t+STRIDE, ... of src[0, n) until their epoch is current
+// and returns their values in out[] (0 past n).  All loads are in
 // flight at once; while waiting, a thread re-reads the entries that are not
 // current yet (the caller has watched the vector's last entry first,
 // so the burst rarely needs a second round).
 template <int NPT, int STRIDE = kIThreads>
-__device__ __forceinline__ void poll_into(const uint64_t* src, int n, uint32_t epoch, float (&out)[NPT],
+__device__ __forceinline__ void poll_part_into(const uint64_t* src, int n, uint32_t epoch, float (&out)[NPT],
                                           unsigned& budget, int32_t* status)
 {
     const int t = opaque_tid();
@@ -315,6 +352,37 @@ __device__ __forceinline__ void poll_into(const uint64_t* src, int n, uint32_t e
         });
     }
     static_for<NPT>([&](auto j) { out[j] = bits_f32(uint32_t(v[j])); });   // 0 past n
+}
+
+// Hand-off words: thread t polls words t, t+STRIDE, ... of src[0, n) until
+// they are non-zero and returns their values in out[] (0.0f past n).  All
+// loads are in flight at once; while waiting, a thread re-reads the words
+// that are still empty (the caller has watched the vector's last word first,
+// so the burst rarely needs a second round).
+template <int NPT, int STRIDE = kIThreads>
+__device__ __forceinline__ void poll_into(const uint32_t* src, int n, float (&out)[NPT], unsigned& budget,
+                                          int32_t* status)
+{
+    const int t = opaque_tid();
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(src, n * 4);   // words past n read as 0
+    const uint32_t vo = uint32_t(t) * 4u;
+    uint32_t v[NPT];
+    static_for<NPT>([&](auto j) { v[j] = hs_load(r, vo, j * STRIDE * 4); });
+    unsigned spins = 0;
+    while (budget != 0) {
+        uint64_t pending = 0;
+        static_for<NPT>([&](auto j) {
+            pending |= uint64_t(int(t + STRIDE * j < n) & int(!hs_ready(v[j]))) << j;
+        });
+        if (pending == 0) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins == kSpinLimit) { budget = 0; atomicOr(status, HQ_STEP_SYNC); }
+        compiler_fence();
+        static_for<NPT>([&](auto j) {
+            if ((pending >> j) & 1) v[j] = hs_load(r, vo, j * STRIDE * 4);
+        });
+    }
+    static_for<NPT>([&](auto j) { out[j] = t + STRIDE * j < n ? hs_value(v[j]) : 0.0f; });
 }
 
 // ---- input-wave prologues ---------------------------------------------------------
@@ -428,19 +496,19 @@ __device__ __forceinline__ void load_gamma(const float* g, int n, float (&out)[N
 // weight waves hold only the down rows at this point (their loads have long
 // landed), so their polls do not queue behind weight loads.  Returns the
 // dequant multiplier amax/127 (the same in every wave).
-__device__ float act_phase(const EngineParams& p, int l, uint32_t epoch, unsigned& budget)
+__device__ float act_phase(const EngineParams& p, int l, const uint32_t* act, unsigned& budget)
 {
     const int T = opaque_tid();
     const int w = T / kWave;
     const int I = p.I;
     // Every wave of the block calls this once per layer, so the block
     // barriers below match up across the two roles.
-    if (w == 0) watch_last(p.ll_act, I, epoch, budget, p.status);
+    if (w == 0) watch_last(act, I, budget, p.status);
     __syncthreads();
     if (w == 0) TRACE(l, 12);
     if (w == kIWaves) TRACE(l, 15);
     float a[kActNPT];
-    poll_into<kActNPT, kThreads>(p.ll_act, I, epoch, a, budget, p.status);
+    poll_into<kActNPT, kThreads>(act, I, a, budget, p.status);
     float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < kActNPT; ++j) m = fmaxf(m, fabsf(a[j]));   // 0 past I
@@ -615,10 +683,11 @@ __device__ __forceinline__ void load_window(int e, unsigned& budget, int32_t* st
     if constexpr (kLoadInWindows) wait_lds_geq(&S.hs, kIWaves * (e + 1), budget, status);
 }
 
-__device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, uint32_t epoch_qkv,
-                                unsigned& budget);
+__device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, const Slot& z,
+                                uint32_t epoch_att, unsigned& budget);
 
-__device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int pos, uint32_t base, unsigned& budget)
+__device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int pos, uint32_t base, int set,
+                            unsigned& budget)
 {
     const int H = p.H, I = p.I;
     const int qd = p.heads * kD;
@@ -657,7 +726,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         if (ww == 0) TRACE(l, 17);
         if (ww == kWWaves - 1) TRACE(l, 47);
         // ---- P2: the block's attention items (all waves)
-        attention_phase(p, Ly, l, pos, base + 5u * uint32_t(l) + 1u, budget);
+        attention_phase(p, Ly, l, pos, slot_of(p, set, l), base + 5u * uint32_t(l) + 2u, budget);
         load_window(4 * l + 1, budget, p.status);
         load_pairs<0, kGuEarly>(wg, sg, Ly.gate_up, Ly.gate_up_scales, R.g0, R.g1, I, H, ww);
         // ---- P3: o (the residual add is the input waves')
@@ -704,7 +773,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         // the instruction sequence, and so every dot's wait, is the same on
         // every path)
         // ---- P5: down (the residual add is the input waves')
-        const float act5 = act_phase(p, l, base + 5u * uint32_t(l) + 4u, budget);
+        const float act5 = act_phase(p, l, slot_of(p, set, l).act(), budget);
         load_rows<kQkvLPR, kQkvC, kPaceQkv>(wq, sq, Ln.qkv, Ln.qkv_scales, R.q0, more ? R.q1 : R.q0 + 1,
                                             more ? H : 32, ww);
         if (ww == 0) TRACE(l, 22);
@@ -817,7 +886,7 @@ __device__ __forceinline__ void chunk_softmax(int c, int tn, float& m, float& ex
 // chunks of the head in ascending order as they arrive.  Same arithmetic as
 // attention_kernel's STEP mode (hq_attention.hip).
 __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l, int h, int g, int ng, int nc,
-                               int n, int pos, uint32_t epoch_qkv, uint32_t epoch_att, unsigned& budget)
+                               int n, int pos, const Slot& z, uint32_t epoch_att, unsigned& budget)
 {
     const int w = opaque_tid() / kWave;
     const int lane = lane_id();
@@ -835,40 +904,39 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
         const float kn0 = gmem(Ly.k_norm)[lane], kn1 = gmem(Ly.k_norm)[lane + 64];
         const float cs = gmem(p.rope_cos)[size_t(pos) * (kD / 2) + lane];
         const float sn = gmem(p.rope_sin)[size_t(pos) * (kD / 2) + lane];
-        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(p.ll_qkv);
-        const uint32_t vo = uint32_t(lane) * 8u;
-        const int sq_ = h * kD * 8;
-        const int sk_ = (qd + kvh * kD) * 8;
-        const int sv_ = (qd + (p.kv_heads + kvh) * kD) * 8;
-        const uint64_t done = uint64_t(epoch_qkv) << 32;
-        uint64_t eq0 = ll_load(rq, vo, sq_), eq1 = ll_load(rq, vo, sq_ + 512);
-        uint64_t ek0 = done, ek1 = done, ev0 = done, ev1 = done;
+        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(z.qkv());
+        const uint32_t vo = uint32_t(lane) * 4u;
+        const int sq_ = h * kD * 4;
+        const int sk_ = (qd + kvh * kD) * 4;
+        const int sv_ = (qd + (p.kv_heads + kvh) * kD) * 4;
+        const uint32_t done = 1u;   // any non-zero word: nothing to wait for
+        uint32_t eq0 = hs_load(rq, vo, sq_), eq1 = hs_load(rq, vo, sq_ + 256);
+        uint32_t ek0 = done, ek1 = done, ev0 = done, ev1 = done;
         if (cur) {
-            ek0 = ll_load(rq, vo, sk_);
-            ek1 = ll_load(rq, vo, sk_ + 512);
-            ev0 = ll_load(rq, vo, sv_);
-            ev1 = ll_load(rq, vo, sv_ + 512);
+            ek0 = hs_load(rq, vo, sk_);
+            ek1 = hs_load(rq, vo, sk_ + 256);
+            ev0 = hs_load(rq, vo, sv_);
+            ev1 = hs_load(rq, vo, sv_ + 256);
         }
         unsigned spins = 0;
         while (budget != 0) {
-            const int ready = int(ll_ready(eq0, epoch_qkv)) & int(ll_ready(eq1, epoch_qkv)) &
-                              int(ll_ready(ek0, epoch_qkv)) & int(ll_ready(ek1, epoch_qkv)) &
-                              int(ll_ready(ev0, epoch_qkv)) & int(ll_ready(ev1, epoch_qkv));
+            const int ready = int(hs_ready(eq0)) & int(hs_ready(eq1)) & int(hs_ready(ek0)) & int(hs_ready(ek1)) &
+                              int(hs_ready(ev0)) & int(hs_ready(ev1));
             if (ready) break;
             __builtin_amdgcn_s_sleep(1);
             if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
             compiler_fence();
-            if (!ll_ready(eq0, epoch_qkv)) eq0 = ll_load(rq, vo, sq_);
-            if (!ll_ready(eq1, epoch_qkv)) eq1 = ll_load(rq, vo, sq_ + 512);
-            if (!ll_ready(ek0, epoch_qkv)) ek0 = ll_load(rq, vo, sk_);
-            if (!ll_ready(ek1, epoch_qkv)) ek1 = ll_load(rq, vo, sk_ + 512);
-            if (!ll_ready(ev0, epoch_qkv)) ev0 = ll_load(rq, vo, sv_);
-            if (!ll_ready(ev1, epoch_qkv)) ev1 = ll_load(rq, vo, sv_ + 512);
+            if (!hs_ready(eq0)) eq0 = hs_load(rq, vo, sq_);
+            if (!hs_ready(eq1)) eq1 = hs_load(rq, vo, sq_ + 256);
+            if (!hs_ready(ek0)) ek0 = hs_load(rq, vo, sk_);
+            if (!hs_ready(ek1)) ek1 = hs_load(rq, vo, sk_ + 256);
+            if (!hs_ready(ev0)) ev0 = hs_load(rq, vo, sv_);
+            if (!hs_ready(ev1)) ev1 = hs_load(rq, vo, sv_ + 256);
         }
         if (w == 0) TRACE(l, 25);
         {
             // per-head RMSNorm + RoPE of q (as attention_kernel's STEP prologue)
-            const float x0 = bits_f32(uint32_t(eq0)), x1 = bits_f32(uint32_t(eq1));
+            const float x0 = hs_value(eq0), x1 = hs_value(eq1);
             float s = __builtin_fmaf(x0, x0, 0.0f);
             s = __builtin_fmaf(x1, x1, s);
             const float ss = wave_tree_sum64_all(s);
@@ -881,7 +949,7 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
         if (cur) {
             // k (norm + RoPE) and v of this position, as fp16, into the row
             // of the last chunk; one query head of the group writes the cache
-            const float x0 = bits_f32(uint32_t(ek0)), x1 = bits_f32(uint32_t(ek1));
+            const float x0 = hs_value(ek0), x1 = hs_value(ek1);
             float s = __builtin_fmaf(x0, x0, 0.0f);
             s = __builtin_fmaf(x1, x1, s);
             const float ss = wave_tree_sum64_all(s);
@@ -889,7 +957,7 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             const float y0 = (x0 / r) * kn0;
             const float y1 = (x1 / r) * kn1;
             const uint16_t k0 = f32_to_f16(y0 * cs - y1 * sn), k1 = f32_to_f16(y1 * cs + y0 * sn);
-            const uint16_t v0 = f32_to_f16(bits_f32(uint32_t(ev0))), v1 = f32_to_f16(bits_f32(uint32_t(ev1)));
+            const uint16_t v0 = f32_to_f16(hs_value(ev0)), v1 = f32_to_f16(hs_value(ev1));
             KvBuf& lb = S.kv[ncg - 1];
             const int rr = pos - (nc - 1) * kAttnChunk;
             lb.k[rr * kD + lane] = k0;
@@ -984,7 +1052,7 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             L = __builtin_fmaf(al, S.pl[c], L);
             O = __builtin_fmaf(al, S.po[c][d], O);
         }
-        if (lane < 32) ll_store(p.ll_att + size_t(h) * kD + d, O * (1.0f / L), epoch_att);
+        if (lane < 32) hs_store(z.att() + size_t(h) * kD + d, O * (1.0f / L));
     } else {
         constexpr int pstride = kD + 2;
         uint64_t* hp = p.ll_part + size_t(h) * size_t(p.max_chunks) * pstride;
@@ -1050,7 +1118,7 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
                     }
                 });
             }
-            if (lane < 32) ll_store(p.ll_att + size_t(h) * kD + d, O * (1.0f / L), epoch_att);
+            if (lane < 32) hs_store(z.att() + size_t(h) * kD + d, O * (1.0f / L));
         }
     }
     }
@@ -1092,8 +1160,8 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
         for (int cb = 0; cb < nc; cb += kPartChunks) {
             const int nb = min(kPartChunks, nc - cb);
             float v[kPartNPT];
-            poll_into<kPartNPT, kThreads>(hp + size_t(cb) * pstride, nb * pstride, epoch_att, v, budget,
-                                          p.status);
+            poll_part_into<kPartNPT, kThreads>(hp + size_t(cb) * pstride, nb * pstride, epoch_att, v, budget,
+                                               p.status);
             static_for<kPartNPT>([&](auto j) {
                 const int e = T + kThreads * j;
                 if (e < nb * pstride) part[e] = v[j];
@@ -1113,7 +1181,7 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             }
             __syncthreads();
         }
-        if (T < kD) ll_store(p.ll_att + size_t(h) * kD + T, O * (1.0f / L), epoch_att);
+        if (T < kD) hs_store(z.att() + size_t(h) * kD + T, O * (1.0f / L));
     }
     if (w == 0) TRACE(l, 29);
     // the item's LDS (K/V chunks, q, scores, partials) may be reused once
@@ -1126,8 +1194,8 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
 // barriers).  Items are (query head, group of up to kGroup chunks); the
 // input waves copy each item's K/V chunks, the block's first item's copies
 // having been started in P1.
-__device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, uint32_t epoch_qkv,
-                                unsigned& budget)
+__device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, const Slot& z,
+                                uint32_t epoch_att, unsigned& budget)
 {
     const int n = pos + 1;
     const int nc = (n + kAttnChunk - 1) / kAttnChunk;
@@ -1137,18 +1205,18 @@ __device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l
     for (int it = b; it < items; it += gridDim.x) {
         if (it != b && opaque_tid() < kIThreads)
             prefetch_group(p, l, (it / ng) / p.G, (it % ng) * kGroup, min(kGroup, nc - (it % ng) * kGroup), n, pos);
-        attention_item(p, Ly, l, it / ng, it % ng, ng, nc, n, pos, epoch_qkv, epoch_qkv + 1u, budget);
+        attention_item(p, Ly, l, it / ng, it % ng, ng, nc, n, pos, z, epoch_att, budget);
     }
 }
 
 // Publish the weight waves' results res[0, n) to dst (input threads t < n).
-__device__ __forceinline__ void publish_rows(uint64_t* dst, int n, uint32_t epoch)
+__device__ __forceinline__ void publish_rows(uint32_t* dst, int n)
 {
     const int t = opaque_tid();
-    for (int i = t; i < n; i += kIThreads) ll_store(dst + i, S.res[i], epoch);
+    for (int i = t; i < n; i += kIThreads) hs_store(dst + i, S.res[i]);
 }
 
-__device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32_t base,
+__device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32_t base, int set,
                            unsigned& budget)
 {
     const int t0 = threadIdx.x;
@@ -1169,6 +1237,8 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         const hq_layer& Ly = S.lay[l];
         const uint32_t E = base + 5u * uint32_t(l);
         const int g = 4 * l;   // GEMV phases before this layer
+        const Slot z = slot_of(p, set, l);
+        const uint32_t* x5_prev = slot_of(p, set, l > 0 ? l - 1 : 0).x5();
 
         // ---- P1: RMSNorm(input) -> quant -> (qkv) -------------------------------------
         TRACE(l, 0);
@@ -1180,10 +1250,10 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
 #pragma unroll
                 for (int j = 0; j < kHidNPT; ++j) xin[j] = t + kIThreads * j < H ? p.x[t + kIThreads * j] : 0.0f;
             } else {
-                watch_last(p.ll_x5, H, E, budget, p.status);
+                watch_last(x5_prev, H, budget, p.status);
                 ibar(bseq, budget, p.status);
                 TRACE(l, 1);
-                poll_into<kHidNPT>(p.ll_x5, H, E, xin, budget, p.status);
+                poll_into<kHidNPT>(x5_prev, H, xin, budget, p.status);
             }
             post_hs();
             TRACE(l, 2);
@@ -1196,20 +1266,20 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         if (b < items) prefetch_group(p, l, (b / ng) / p.G, (b % ng) * kGroup, min(kGroup, nc - (b % ng) * kGroup), n, pos);
         wait_lds_geq(&S.done, kWWaves * (g + 1), budget, p.status);
         TRACE(l, 4);
-        publish_rows(p.ll_qkv + R.q0, R.q1 - R.q0, E + 1);
+        publish_rows(z.qkv() + R.q0, R.q1 - R.q0);
 
         // ---- P2: attention ------------------------------------------------------------
-        attention_phase(p, Ly, l, pos, E + 1, budget);
+        attention_phase(p, Ly, l, pos, z, E + 2, budget);
 
         // ---- P3: quant -> (o) -> residual ---------------------------------------------
         float gpost[kHidNPT];
         {
             float att[kAttNPT];
             TRACE(l, 5);
-            watch_last(p.ll_att, qd, E + 2, budget, p.status);
+            watch_last(z.att(), qd, budget, p.status);
             ibar(bseq, budget, p.status);
             TRACE(l, 6);
-            poll_into<kAttNPT>(p.ll_att, qd, E + 2, att, budget, p.status);
+            poll_into<kAttNPT>(z.att(), qd, att, budget, p.status);
             post_hs();
             load_gamma(Ly.post_norm, H, gpost);
             const float act = quantize(att, qd, kOLPR * kOC * 32, bseq, budget, p.status);
@@ -1220,16 +1290,16 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         TRACE(l, 8);
         if (t < nown) {
             xown = xown + S.res[t];
-            ll_store(p.ll_x3 + R.h0 + t, xown, E + 3);
+            hs_store(z.x3() + R.h0 + t, xown);
         }
 
         // ---- P4: RMSNorm(post) -> quant -> (gate_up, SwiGLU) --------------------------
         {
             float xp[kHidNPT];
-            watch_last(p.ll_x3, H, E + 3, budget, p.status);
+            watch_last(z.x3(), H, budget, p.status);
             ibar(bseq, budget, p.status);
             TRACE(l, 9);
-            poll_into<kHidNPT>(p.ll_x3, H, E + 3, xp, budget, p.status);
+            poll_into<kHidNPT>(z.x3(), H, xp, budget, p.status);
             post_hs();
             const float act = rmsnorm_quant(xp, H, gpost, p.eps, kGuLPR * kGuC * 32, bseq, budget, p.status, l, 32);
             post_xq(act);
@@ -1242,18 +1312,27 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         // quantizes it into its own S.xq, so one hand-off carries both the
         // act scale and the down GEMV's input.
         const int na = R.g1 - R.g0;
-        if (t < na) ll_store(p.ll_act + R.g0 + t, S.res[t], E + 4);
+        if (t < na) hs_store(z.act() + R.g0 + t, S.res[t]);
+        // while the SwiGLU hand-off travels: this block's share of layer l's
+        // slot in the other set (written by the previous launch) back to empty
+        {
+            uint32_t* o = slot_of(p, set ^ 1, l).base;
+            const int c0 = split_begin(p.hs_layer, blockIdx.x, gridDim.x);
+            const int c1 = split_begin(p.hs_layer, blockIdx.x + 1, gridDim.x);
+            for (int i = c0 + t; i < c1; i += kIThreads)
+                __hip_atomic_store(o + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
 
         // ---- P5: quant (all waves) -> (down) -> residual --------------------------------
-        act_phase(p, l, E + 4, budget);
+        act_phase(p, l, z.act(), budget);
         post_hs();
         TRACE(l, 13);
         wait_lds_geq(&S.done, kWWaves * (g + 4), budget, p.status);
         TRACE(l, 14);
         if (t < nown) {
             xown = xown + S.res[t];
-            ll_store(p.ll_x5 + R.h0 + t, xown, E + 5);
-            if (l + 1 == p.L) p.x[R.h0 + t] = xown;
+            if (l + 1 < p.L) hs_store(z.x5() + R.h0 + t, xown);
+            else p.x[R.h0 + t] = xown;
         }
     }
 }
@@ -1272,6 +1351,8 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         return;
     }
     const uint32_t base = *p.epoch;
+    // the hand-off set of this launch (launches alternate between two)
+    const int set = int((base / (5u * uint32_t(p.L))) & 1u);
     Rows R;
     R.h0 = split_begin(p.H, b, NB);
     R.h1 = split_begin(p.H, b + 1, NB);
@@ -1300,13 +1381,14 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     for (int i = tid; i < kTraceWords; i += kThreads) S.trace[i] = 0;
     __syncthreads();
 #endif
-    if (wave >= kIWaves) weight_role(p, R, wave - kIWaves, pos, base, budget);
-    else input_role(p, R, pos, base, budget);
+    if (wave >= kIWaves) weight_role(p, R, wave - kIWaves, pos, base, set, budget);
+    else input_role(p, R, pos, base, set, budget);
 #ifdef HQ_ENGINE_TRACE
     __syncthreads();
     for (int i = tid; i < kTraceWords; i += kThreads) p.trace[size_t(b) * kTraceWords + i] = S.trace[i];
 #endif
-    if (b == 0 && tid == 0) *p.epoch = base + 5u * uint32_t(p.L);
+    // (the thread index re-read here: holding it across the layer loop costs a register)
+    if (blockIdx.x == 0 && opaque_tid() == 0) *p.epoch = base + 5u * uint32_t(p.L);
 }
 
 // ---- host ---------------------------------------------------------------------
@@ -1364,14 +1446,19 @@ size_t engine_trace_bytes(const hq_model* m)
 #endif
 }
 
-size_t engine_ll_entries(const hq_model* m)
+static int engine_layer_words(const hq_model* m)
 {
     const int qd = m->heads * m->head_dim;
     const int qrows = qd + 2 * m->kv_heads * m->head_dim;
-    return size_t(2 * m->hidden) + size_t(qrows) + size_t(qd) + size_t(m->intermediate);
+    return 2 * m->hidden + qrows + qd + m->intermediate;
 }
 
-hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, uint32_t* epoch,
+size_t engine_handoff_bytes(const hq_model* m)
+{
+    return size_t(2) * size_t(m->layers) * size_t(engine_layer_words(m)) * 4;
+}
+
+hipError_t launch_engine(const hq_model* m, const hq_state* st, uint32_t* hs, uint32_t* epoch,
                          uint64_t* part, int max_chunks, int nb, uint32_t* trace, hipStream_t s)
 {
     EngineParams p{};
@@ -1395,11 +1482,8 @@ hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, ui
     p.position = st->position;
     p.status = st->status;
     p.x = st->x;
-    p.ll_x3 = ll;
-    p.ll_x5 = p.ll_x3 + m->hidden;
-    p.ll_qkv = p.ll_x5 + m->hidden;
-    p.ll_att = p.ll_qkv + p.qkv_rows;
-    p.ll_act = p.ll_att + qd;
+    p.hs = hs;
+    p.hs_layer = engine_layer_words(m);
     p.epoch = epoch;
     p.ll_part = part;
     p.max_chunks = max_chunks;

@@ -90,9 +90,10 @@ hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s);
 bool engine_fits(const hq_model* m);
 // Grid size on the current device (0: the kernel cannot run there).
 int engine_blocks(const hq_model* m);
-// 64-bit hand-off entries the kernel needs in the workspace.
-size_t engine_ll_entries(const hq_model* m);
-hipError_t launch_engine(const hq_model* m, const hq_state* st, uint64_t* ll, uint32_t* epoch,
+// Bytes of hand-off words the kernel needs in the workspace (zero-filled
+// before the first launch): two sets of one slot per layer.
+size_t engine_handoff_bytes(const hq_model* m);
+hipError_t launch_engine(const hq_model* m, const hq_state* st, uint32_t* hs, uint32_t* epoch,
                          uint64_t* part, int max_chunks, int nb, uint32_t* trace, hipStream_t s);
 // HQ_ENGINE_TRACE builds: bytes of phase timestamps kept after the step
 // workspace proper (0 otherwise).

@@ -64,7 +64,7 @@ static StepLayout step_layout(const hq_model* m, int capacity)
     L.lm_counter_off = L.lm_idx_off + align256(size_t(L.lm_blocks) * 4);
     L.epoch_off = L.lm_counter_off + align256(size_t(ticket_words(L.lm_blocks)) * 4);
     L.ll_off = L.epoch_off + 256;
-    L.eng_part_off = L.ll_off + align256(engine_ll_entries(m) * 8);
+    L.eng_part_off = L.ll_off + align256(engine_handoff_bytes(m));
     L.trace_off = L.eng_part_off + align256(size_t(m->heads) * L.max_chunks * (m->head_dim + 2) * 8);
     L.total = L.trace_off + engine_trace_bytes(m);
     return L;
@@ -143,7 +143,7 @@ static hipError_t enqueue_layers(const hq_model* m, const hq_state* st, hipStrea
     const int nb = (m->device_layer && !(m->flags & HQ_MODEL_PER_LAYER_KERNELS) && engine_fits(m))
                        ? engine_blocks(m) : 0;
     if (nb > 0) {
-        e = launch_engine(m, st, reinterpret_cast<uint64_t*>(ws + Ly.ll_off),
+        e = launch_engine(m, st, reinterpret_cast<uint32_t*>(ws + Ly.ll_off),
                           reinterpret_cast<uint32_t*>(ws + Ly.epoch_off),
                           reinterpret_cast<uint64_t*>(ws + Ly.eng_part_off), Ly.max_chunks, nb,
                           engine_trace_bytes(m) ? reinterpret_cast<uint32_t*>(ws + Ly.trace_off) : nullptr, s);
