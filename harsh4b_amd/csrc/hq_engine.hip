@@ -1313,15 +1313,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         // act scale and the down GEMV's input.
         const int na = R.g1 - R.g0;
         if (t < na) hs_store(z.act() + R.g0 + t, S.res[t]);
-        // while the SwiGLU hand-off travels: this block's share of layer l's
-        // slot in the other set (written by the previous launch) back to empty
-        {
-            uint32_t* o = slot_of(p, set ^ 1, l).base;
-            const int c0 = split_begin(p.hs_layer, blockIdx.x, gridDim.x);
-            const int c1 = split_begin(p.hs_layer, blockIdx.x + 1, gridDim.x);
-            for (int i = c0 + t; i < c1; i += kIThreads)
-                __hip_atomic_store(o + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
 
         // ---- P5: quant (all waves) -> (down) -> residual --------------------------------
         act_phase(p, l, z.act(), budget);
@@ -1367,6 +1358,16 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
         const uint64_t* src = reinterpret_cast<const uint64_t*>(p.layers);
         uint64_t* dst = reinterpret_cast<uint64_t*>(S.lay);
         for (int i = tid; i < p.L * kWords; i += kThreads) dst[i] = src[i];
+    }
+    {
+        // This block's share of the other set (written by the previous
+        // launch, which has finished) back to empty, before any weight load
+        // is issued; the next launch uses that set.
+        const size_t words = size_t(p.L) * size_t(p.hs_layer);
+        uint32_t* o = p.hs + size_t(set ^ 1) * words;
+        const size_t c0 = words * size_t(b) / size_t(NB), c1 = words * size_t(b + 1) / size_t(NB);
+        for (size_t i = c0 + size_t(tid); i < c1; i += kThreads)
+            __hip_atomic_store(o + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (tid == 0) {
         S.xq_seq = 0;
