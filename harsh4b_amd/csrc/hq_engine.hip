@@ -66,6 +66,7 @@ constexpr int kMaxRes = 64;                      // outputs of one GEMV phase pe
 constexpr int kMaxLayers = 64;                   // layer table copy in LDS
 constexpr int kGroup = 4;                         // chunks of 64 positions per attention item
 constexpr unsigned kSpinLimit = 1u << 22;           // rounds one wait may spin
+constexpr int kCopyWave0 = kIWaves, kCopyWaves = 8;  // the waves that copy attention K/V chunks into LDS
 #ifdef HQ_ENGINE_TRACE
 // Timestamps (low 32 bits of the 100 MHz clock) of layers kTraceL0 ..
 // kTraceL0+3: input wave 0 at points 0-15, weight wave 0 at points 16-23,
@@ -89,10 +90,6 @@ constexpr int kDownLPR = 64, kDownC = 5;         // K <= 10240, 1 row per wave
 constexpr int kHidNPT = kMaxHidden / kIThreads;  // 10
 constexpr int kAttNPT = 16;                      // heads*D <= 4096
 constexpr int kActNPT = kMaxVec / kThreads;      // 10: SwiGLU entries per thread (all waves), I <= 10240
-constexpr int kSerialChunks = 16;                // up to this many chunks a head's combine reads its
-                                                 // partials directly (two bursts of eight)
-constexpr int kPartChunks = 62;                  // chunk partials staged in LDS per combine burst
-constexpr int kPartNPT = (kPartChunks * (kD + 2) + kThreads - 1) / kThreads;   // 8 entries per thread
 
 }  // namespace eng
 
@@ -160,6 +157,8 @@ struct Shared {
     alignas(16) float as[kGroup * kAttnChunk];   // attention: the item's scores
     alignas(16) float po[kGroup][kD];   // attention: chunk partials o, m, l
     float pm[kGroup], pl[kGroup];
+    alignas(16) float gq[kG][kD];                   // GQA items: the G normalized, rotated query heads
+    alignas(16) float gs[kG][kGroup * kAttnChunk];  // GQA items: their scores
     hq_layer lay[kMaxLayers];
 #ifdef HQ_ENGINE_TRACE
     uint32_t trace[kTraceWords];
@@ -273,11 +272,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, int
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform_ptr(p)), 0,
                                              __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
-__device__ __forceinline__ uint64_t ll_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
-{
-    const auto q = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kBufSC1);
-    return (uint64_t(q[1]) << 32) | q[0];
-}
 __device__ __forceinline__ bool ll_ready(uint64_t v, uint32_t epoch)
 {
     return int32_t(uint32_t(v >> 32) - epoch) >= 0;
@@ -320,38 +314,6 @@ __device__ __forceinline__ void watch_last(const uint32_t* src, int n, unsigned&
             w = hs_load(r, off, 0);
         }
     }
-}
-
-// 64-bit {value, epoch} entries (the attention chunk partials): thread t
-// polls entries t, t+STRIDE, ... of src[0, n) until their epoch is current
-// and returns their values in out[] (0 past n).  All loads are in
-// flight at once; while waiting, a thread re-reads the entries that are not
-// current yet (the caller has watched the vector's last entry first,
-// so the burst rarely needs a second round).
-template <int NPT, int STRIDE = kIThreads>
-__device__ __forceinline__ void poll_part_into(const uint64_t* src, int n, uint32_t epoch, float (&out)[NPT],
-                                          unsigned& budget, int32_t* status)
-{
-    const int t = opaque_tid();
-    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(src, n * 8);   // entries past n read as 0
-    const uint32_t vo = uint32_t(t) * 8u;
-    uint64_t v[NPT];
-    static_for<NPT>([&](auto j) { v[j] = ll_load(r, vo, j * STRIDE * 8); });
-    unsigned spins = 0;
-    while (budget != 0) {
-        uint64_t pending = 0;
-        static_for<NPT>([&](auto j) {
-            pending |= uint64_t(int(t + STRIDE * j < n) & int(!ll_ready(v[j], epoch))) << j;
-        });
-        if (pending == 0) break;
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins == kSpinLimit) { budget = 0; atomicOr(status, HQ_STEP_SYNC); }
-        compiler_fence();
-        static_for<NPT>([&](auto j) {
-            if ((pending >> j) & 1) v[j] = ll_load(r, vo, j * STRIDE * 8);
-        });
-    }
-    static_for<NPT>([&](auto j) { out[j] = bits_f32(uint32_t(v[j])); });   // 0 past n
 }
 
 // Hand-off words: thread t polls words t, t+STRIDE, ... of src[0, n) until
@@ -685,6 +647,8 @@ __device__ __forceinline__ void load_window(int e, unsigned& budget, int32_t* st
 
 __device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, const Slot& z,
                                 uint32_t epoch_att, unsigned& budget);
+__device__ __forceinline__ bool is_copy_wave(int w);
+__device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l, int pos);
 
 __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int pos, uint32_t base, int set,
                             unsigned& budget)
@@ -712,6 +676,9 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         const bool more = l + 1 < p.L;
         const hq_layer& Ly = S.lay[l];
         const hq_layer& Ln = S.lay[more ? l + 1 : l];
+        // this layer's first attention item: its K/V copies land while the
+        // qkv GEMV and its hand-off run
+        if (is_copy_wave(opaque_tid() / kWave)) prefetch_first_item(p, l, pos);
         // ---- P1: qkv
         wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 1), budget, p.status);
         if (ww == 0) TRACE(l, 16);
@@ -799,23 +766,27 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
 
 // Copies K and V rows [t0, t0 + 64) of kv head kvh into S.kv[kb]: rows
 // before the current position from the cache, rows after it as zeros; the
-// row of the current position is written from the qkv hand-off.  Each input
-// wave handles 16 rows of K and of V: one instruction moves 4 rows of 128
-// halves.
+// row of the current position is written from the qkv hand-off.  The copies
+// are issued by the kCopyWaves copy waves (weight waves 4..11, idle during
+// attention), each handling 8 rows of K and of V: one instruction moves 4
+// rows of 128 halves.  A wave's loads complete in issue order, so copies
+// issued by the input waves would hold back their next hand-off polls.
+__device__ __forceinline__ bool is_copy_wave(int w) { return w >= kCopyWave0 && w < kCopyWave0 + kCopyWaves; }
+
 __device__ __forceinline__ void prefetch_kv(const EngineParams& p, int l, int kvh, int t0, int n, int pos, int kb)
 {
-    const int w = opaque_tid() / kWave;
+    const int w = opaque_tid() / kWave - kCopyWave0;
     const int lane = lane_id();
     const uint16_t* kl = p.keys + size_t(l) * size_t(p.kv_layer);
     const uint16_t* vl = p.values + size_t(l) * size_t(p.kv_layer);
     const uint32_t kdst = lds_addr(S.kv[kb].k), vdst = lds_addr(S.kv[kb].v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = w * 16 + i * 4 + (lane >> 4);            // row within the chunk
+    for (int i = 0; i < 2; ++i) {
+        const int r = w * 8 + i * 4 + (lane >> 4);             // row within the chunk
         const int t = t0 + r;
         const uint32_t off = uint32_t((size_t(min(t, n - 1)) * size_t(p.kv_stride) + size_t(kvh) * kD +
                                        size_t(lane & 15) * 8) * 2);
-        const uint32_t row0 = uint32_t((w * 16 + i * 4) * kD * 2);
+        const uint32_t row0 = uint32_t((w * 8 + i * 4) * kD * 2);
         if (t < pos) {
             dma16(kl, off, kdst + row0);
             dma16(vl, off, vdst + row0);
@@ -828,11 +799,33 @@ __device__ __forceinline__ void prefetch_kv(const EngineParams& p, int l, int kv
     }
 }
 
-// K/V of chunks c0 .. c0+ncg-1 of kv head kvh into S.kv[0 .. ncg).
+// K/V of chunks c0 .. c0+ncg-1 of kv head kvh into S.kv[0 .. ncg) (copy waves).
 __device__ __forceinline__ void prefetch_group(const EngineParams& p, int l, int kvh, int c0, int ncg, int n,
                                                int pos)
 {
     for (int c = 0; c < ncg; ++c) prefetch_kv(p, l, kvh, (c0 + c) * kAttnChunk, n, pos, c);
+}
+
+__device__ __forceinline__ int gqa_group(int nc, int kv_heads, int nb);
+__device__ __forceinline__ int item_slot(int b, int NB, int G);
+
+// The copies of this block's first attention item of layer l (copy waves):
+// issued at the start of the layer, so they land while the qkv GEMV and its
+// hand-off run.  Items as in attention_phase.
+__device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l, int pos)
+{
+    const int n = pos + 1;
+    const int nc = (n + kAttnChunk - 1) / kAttnChunk;
+    const int ng = (nc + kGroup - 1) / kGroup;
+    const int b = blockIdx.x;
+    if (ng > 1) {
+        const int cg = gqa_group(nc, p.kv_heads, gridDim.x);
+        const int ngq = (nc + cg - 1) / cg;
+        if (b < p.kv_heads * ngq) prefetch_group(p, l, b / ngq, (b % ngq) * cg, min(cg, nc - (b % ngq) * cg), n, pos);
+    } else {
+        const int k = item_slot(b, gridDim.x, p.G);   // per-head item: query head k
+        if (k < p.heads) prefetch_group(p, l, k / p.G, 0, nc, n, pos);
+    }
 }
 
 // V accumulation of one or two chains per lane: o[d] = fmaf chain of
@@ -885,17 +878,17 @@ __device__ __forceinline__ void chunk_softmax(int c, int tn, float& m, float& ex
 // its chunks' partials (m, l, o) and the item of the last group combines all
 // chunks of the head in ascending order as they arrive.  Same arithmetic as
 // attention_kernel's STEP mode (hq_attention.hip).
-__device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l, int h, int g, int ng, int nc,
-                               int n, int pos, const Slot& z, uint32_t epoch_att, unsigned& budget)
+__device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l, int h, int nc, int n, int pos,
+                               const Slot& z, unsigned& budget)
 {
     const int w = opaque_tid() / kWave;
     const int lane = lane_id();
     const int G = p.G;
     const int kvh = h / G;
     const int qd = p.heads * kD;
-    const int c0 = g * kGroup;
-    const int ncg = min(kGroup, nc - c0);
-    const bool cur = g == ng - 1;            // the group holding the current position
+    const int ncg = nc;                      // every chunk of the context (nc <= kGroup)
+    constexpr int c0 = 0;
+    constexpr bool cur = true;               // the item holds the current position
 
     if (w == 0) {
         // q of head h (dims lane, lane+64); for the current group also k and
@@ -976,9 +969,9 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             }
         }
     }
-    // the input waves' K/V copies have landed (they issued them), q and the
+    // the copy waves' K/V copies have landed (they issued them), q and the
     // current row are in place
-    if (w < kIWaves) wait_all_memory();
+    if (is_copy_wave(w)) wait_all_memory();
     __syncthreads();
     if (w == 0) TRACE(l, 26);
 
@@ -1038,12 +1031,11 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
     if (w == 0) TRACE(l, 28);
     __syncthreads();
 
-    // combine (input waves): 32 dims per wave
+    // combine (input waves, 32 dims per wave): the head's chunks are all
+    // here: M = max m_c, then L and O over ascending chunks with
+    // a_c = exp(m_c - M)
     if (w < kIWaves) {
-    const int d = 32 * w + (lane & 31);   // combine: 32 dims per wave
-    if (ng == 1) {
-        // the head's chunks are all here: M = max m_c, then L and O over
-        // ascending chunks with a_c = exp(m_c - M)
+        const int d = 32 * w + (lane & 31);
         float M = S.pm[0];
         for (int c = 1; c < ncg; ++c) M = fmaxf(M, S.pm[c]);
         float L = 0.0f, O = 0.0f;
@@ -1053,135 +1045,6 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
             O = __builtin_fmaf(al, S.po[c][d], O);
         }
         if (lane < 32) hs_store(z.att() + size_t(h) * kD + d, O * (1.0f / L));
-    } else {
-        constexpr int pstride = kD + 2;
-        uint64_t* hp = p.ll_part + size_t(h) * size_t(p.max_chunks) * pstride;
-        if (w < ncg) {
-            // wave w publishes chunk w of the group
-            uint64_t* cp = hp + size_t(c0 + w) * pstride;
-            if (lane == 0) {
-                ll_store(cp, S.pm[w], epoch_att);
-                ll_store(cp + 1, S.pl[w], epoch_att);
-            }
-            ll_store(cp + 2 + lane, S.po[w][lane], epoch_att);
-            ll_store(cp + 2 + lane + 64, S.po[w][lane + 64], epoch_att);
-        }
-        if (cur && nc <= kSerialChunks) {
-            // few chunks: the four input waves combine them directly from
-            // the hand-off entries.  M over all chunks: lane i watches chunk
-            // c0 + i of each group of 64
-            const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(hp, nc * pstride * 8);
-            unsigned spins = 0;
-            float M = -__builtin_inff();
-            for (int b0 = 0; b0 < nc; b0 += kWave) {
-                const int cc = min(b0 + lane, nc - 1);
-                uint64_t em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
-                while (budget != 0) {
-                    if (ll_ready(em, epoch_att)) break;
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
-                    compiler_fence();
-                    if (!ll_ready(em, epoch_att)) em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
-                }
-                M = fmaxf(M, bits_f32(uint32_t(em)));
-            }
-            M = wave_max64_all(M);
-            // L and O over ascending chunks, eight chunks' entries in flight
-            // (their m entries have all arrived above)
-            float L = 0.0f, O = 0.0f;
-            for (int b0 = 0; b0 < nc; b0 += 8) {
-                uint64_t em[8], el[8], eo[8];
-                static_for<8>([&](auto j) {
-                    const int cc = min(b0 + j, nc - 1);
-                    em[j] = ll_load(rp, 0u, (cc * pstride) * 8);
-                    el[j] = ll_load(rp, 0u, (cc * pstride + 1) * 8);
-                    eo[j] = ll_load(rp, uint32_t(d) * 8u, (cc * pstride + 2) * 8);
-                });
-                while (budget != 0) {
-                    int ready = 1;
-                    static_for<8>([&](auto j) { ready &= int(ll_ready(el[j], epoch_att)) & int(ll_ready(eo[j], epoch_att)); });
-                    if (ready) break;
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
-                    compiler_fence();
-                    static_for<8>([&](auto j) {
-                        const int cc = min(b0 + j, nc - 1);
-                        if (!ll_ready(el[j], epoch_att)) el[j] = ll_load(rp, 0u, (cc * pstride + 1) * 8);
-                        if (!ll_ready(eo[j], epoch_att)) eo[j] = ll_load(rp, uint32_t(d) * 8u, (cc * pstride + 2) * 8);
-                    });
-                }
-                static_for<8>([&](auto j) {
-                    if (b0 + j < nc) {
-                        const float al = spec_expf(bits_f32(uint32_t(em[j])) - M);
-                        L = __builtin_fmaf(al, bits_f32(uint32_t(el[j])), L);
-                        O = __builtin_fmaf(al, bits_f32(uint32_t(eo[j])), O);
-                    }
-                });
-            }
-            if (lane < 32) hs_store(z.att() + size_t(h) * kD + d, O * (1.0f / L));
-        }
-    }
-    }
-    if (ng > 1 && cur && nc > kSerialChunks) {
-        // The item of the last group combines all nc chunks of head h, in
-        // ascending order: M = max m_c, a_c = exp(m_c - M), L and O fma
-        // chains over c, out = O * (1/L).  Wave 0 waits for every chunk's m
-        // entry (and takes M from them); then the block reads the chunks'
-        // partial entries into LDS (the K/V buffers, free now) in bursts of
-        // kPartChunks chunks, wave 0 writes their a_c, and threads 0..127
-        // carry one dimension's L and O each.
-        constexpr int pstride = kD + 2;
-        static_assert(kPartChunks * pstride * sizeof(float) <= sizeof(S.kv), "partials exceed the K/V buffers");
-        static_assert(kPartChunks <= kGroup * kAttnChunk, "chunk weights exceed the score buffer");
-        const uint64_t* hp = p.ll_part + size_t(h) * size_t(p.max_chunks) * pstride;
-        float* part = reinterpret_cast<float*>(&S.kv[0]);
-        const int T = opaque_tid();
-        if (w == 0) {
-            const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(hp, nc * pstride * 8);
-            unsigned spins = 0;
-            float M = -__builtin_inff();
-            for (int b0 = 0; b0 < nc; b0 += kWave) {
-                const int cc = min(b0 + lane, nc - 1);
-                uint64_t em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
-                while (budget != 0) {
-                    if (ll_ready(em, epoch_att)) break;
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
-                    compiler_fence();
-                    if (!ll_ready(em, epoch_att)) em = ll_load(rp, uint32_t(cc * pstride) * 8u, 0);
-                }
-                M = fmaxf(M, bits_f32(uint32_t(em)));
-            }
-            M = wave_max64_all(M);
-            if (lane == 0) S.pm[0] = M;
-        }
-        __syncthreads();
-        float L = 0.0f, O = 0.0f;
-        for (int cb = 0; cb < nc; cb += kPartChunks) {
-            const int nb = min(kPartChunks, nc - cb);
-            float v[kPartNPT];
-            poll_part_into<kPartNPT, kThreads>(hp + size_t(cb) * pstride, nb * pstride, epoch_att, v, budget,
-                                               p.status);
-            static_for<kPartNPT>([&](auto j) {
-                const int e = T + kThreads * j;
-                if (e < nb * pstride) part[e] = v[j];
-            });
-            __syncthreads();
-            if (w == 0) {
-                const float M = S.pm[0];
-                for (int c = lane; c < nb; c += kWave) S.as[c] = spec_expf(part[c * pstride] - M);
-            }
-            __syncthreads();
-            if (T < kD) {
-                for (int c = 0; c < nb; ++c) {
-                    const float al = S.as[c];
-                    L = __builtin_fmaf(al, part[c * pstride + 1], L);
-                    O = __builtin_fmaf(al, part[c * pstride + 2 + T], O);
-                }
-            }
-            __syncthreads();
-        }
-        if (T < kD) hs_store(z.att() + size_t(h) * kD + T, O * (1.0f / L));
     }
     if (w == 0) TRACE(l, 29);
     // the item's LDS (K/V chunks, q, scores, partials) may be reused once
@@ -1189,23 +1052,364 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
     __syncthreads();
 }
 
+
+// ---- GQA attention items (more than one chunk group per head) ---------------------
+//
+// At contexts of more than kGroup chunks the work item is (kv head, group of
+// cg chunks) and serves the G query heads that share the kv head, so every
+// K/V byte crosses one CU's memory pipe once (an item per query head would
+// move it G times).  Each item publishes its chunks' partials (m, l, o) per
+// query head as 64-bit {value, epoch} entries; afterwards every block
+// combines the partials of its share of the attention output (gqa_combine),
+// so no single block reads all of a head's partials.  Same arithmetic as the
+// per-head items: the chunk terms, then the combine over ascending chunks.
+
+// Chunks per GQA item: the fewest (up to kGroup) that give every item of the
+// layer a block of its own.
+__device__ __forceinline__ int gqa_group(int nc, int kv_heads, int nb)
+{
+    for (int cg = 1; cg < kGroup; ++cg)
+        if (kv_heads * ((nc + cg - 1) / cg) <= nb) return cg;
+    return kGroup;
+}
+
+// Softmax terms of the 64 scores at sc (lane t holds position t).
+__device__ __forceinline__ void scores_softmax(const float* sc, int tn, float& m, float& ex, float& ls)
+{
+    const int lane = lane_id();
+    const float v = sc[lane];
+    m = wave_max64_all(v);
+    ex = (lane < tn) ? spec_expf(v - m) : 0.0f;
+    ls = wave_tree_sum64_all(ex);
+}
+
+__device__ void gqa_item(const EngineParams& p, const hq_layer& Ly, int l, int kvh, int g, int ngq, int cg, int nc,
+                         int n, int pos, const Slot& z, uint32_t epoch_att, unsigned& budget)
+{
+    const int w = opaque_tid() / kWave;
+    const int lane = lane_id();
+    const int G = p.G;
+    const int qd = p.heads * kD;
+    const int c0 = g * cg;
+    const int ncg = min(cg, nc - c0);
+    const bool cur = g == ngq - 1;           // the group holding the current position
+    constexpr int pstride = kD + 2;
+
+    if (w < G) {
+        // wave w: query head kvh*G + w (dims lane, lane+64); wave 0 of the
+        // current group also k and v of the kv head
+        const int h = kvh * G + w;
+        const bool kv = cur && w == 0;
+        const float qn0 = gmem(Ly.q_norm)[lane], qn1 = gmem(Ly.q_norm)[lane + 64];
+        const float kn0 = gmem(Ly.k_norm)[lane], kn1 = gmem(Ly.k_norm)[lane + 64];
+        const float cs = gmem(p.rope_cos)[size_t(pos) * (kD / 2) + lane];
+        const float sn = gmem(p.rope_sin)[size_t(pos) * (kD / 2) + lane];
+        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(z.qkv());
+        const uint32_t vo = uint32_t(lane) * 4u;
+        const int sq_ = h * kD * 4;
+        const int sk_ = (qd + kvh * kD) * 4;
+        const int sv_ = (qd + (p.kv_heads + kvh) * kD) * 4;
+        const uint32_t done = 1u;   // any non-zero word: nothing to wait for
+        uint32_t eq0 = hs_load(rq, vo, sq_), eq1 = hs_load(rq, vo, sq_ + 256);
+        uint32_t ek0 = done, ek1 = done, ev0 = done, ev1 = done;
+        if (kv) {
+            ek0 = hs_load(rq, vo, sk_);
+            ek1 = hs_load(rq, vo, sk_ + 256);
+            ev0 = hs_load(rq, vo, sv_);
+            ev1 = hs_load(rq, vo, sv_ + 256);
+        }
+        unsigned spins = 0;
+        while (budget != 0) {
+            const int ready = int(hs_ready(eq0)) & int(hs_ready(eq1)) & int(hs_ready(ek0)) & int(hs_ready(ek1)) &
+                              int(hs_ready(ev0)) & int(hs_ready(ev1));
+            if (ready) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins == kSpinLimit) { budget = 0; atomicOr(p.status, HQ_STEP_SYNC); }
+            compiler_fence();
+            if (!hs_ready(eq0)) eq0 = hs_load(rq, vo, sq_);
+            if (!hs_ready(eq1)) eq1 = hs_load(rq, vo, sq_ + 256);
+            if (!hs_ready(ek0)) ek0 = hs_load(rq, vo, sk_);
+            if (!hs_ready(ek1)) ek1 = hs_load(rq, vo, sk_ + 256);
+            if (!hs_ready(ev0)) ev0 = hs_load(rq, vo, sv_);
+            if (!hs_ready(ev1)) ev1 = hs_load(rq, vo, sv_ + 256);
+        }
+        {
+            const float x0 = hs_value(eq0), x1 = hs_value(eq1);
+            float s = __builtin_fmaf(x0, x0, 0.0f);
+            s = __builtin_fmaf(x1, x1, s);
+            const float ss = wave_tree_sum64_all(s);
+            const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
+            const float y0 = (x0 / r) * qn0;
+            const float y1 = (x1 / r) * qn1;
+            S.gq[w][lane] = y0 * cs - y1 * sn;
+            S.gq[w][lane + 64] = y1 * cs + y0 * sn;
+        }
+        if (kv) {
+            const float x0 = hs_value(ek0), x1 = hs_value(ek1);
+            float s = __builtin_fmaf(x0, x0, 0.0f);
+            s = __builtin_fmaf(x1, x1, s);
+            const float ss = wave_tree_sum64_all(s);
+            const float r = __builtin_sqrtf(ss / float(kD) + p.eps);
+            const float y0 = (x0 / r) * kn0;
+            const float y1 = (x1 / r) * kn1;
+            const uint16_t k0 = f32_to_f16(y0 * cs - y1 * sn), k1 = f32_to_f16(y1 * cs + y0 * sn);
+            const uint16_t v0 = f32_to_f16(hs_value(ev0)), v1 = f32_to_f16(hs_value(ev1));
+            KvBuf& lb = S.kv[ncg - 1];
+            const int rr = pos - (nc - 1) * kAttnChunk;
+            lb.k[rr * kD + lane] = k0;
+            lb.k[rr * kD + lane + 64] = k1;
+            lb.v[rr * kD + lane] = v0;
+            lb.v[rr * kD + lane + 64] = v1;
+            uint16_t* kl = p.keys + size_t(l) * size_t(p.kv_layer) + size_t(pos) * size_t(p.kv_stride) +
+                           size_t(kvh) * kD;
+            uint16_t* vl = p.values + size_t(l) * size_t(p.kv_layer) + size_t(pos) * size_t(p.kv_stride) +
+                           size_t(kvh) * kD;
+            kl[lane] = k0;
+            kl[lane + 64] = k1;
+            vl[lane] = v0;
+            vl[lane + 64] = v1;
+        }
+    }
+    // the copy waves' K/V copies have landed (they issued them), the query
+    // heads and the current row are in place
+    if (is_copy_wave(w)) wait_all_memory();
+    __syncthreads();
+
+    // scores: wave w takes positions 4w .. 4w+3 of every chunk (16 lanes per
+    // position, 8 dims each) for every query head; the K rows are read once
+    {
+        const float scale = 1.0f / __builtin_sqrtf(float(kD));
+        const int l16 = lane & 15;
+        const int t = w * 4 + (lane >> 4);
+        uint4 kw[kGroup];
+        static_for<kGroup>([&](auto c) {
+            kw[c] = c < ncg ? *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]) : make_uint4(0, 0, 0, 0);
+        });
+        for (int hh = 0; hh < G; ++hh) {
+            float qv[8];
+            const float4 qa = *reinterpret_cast<const float4*>(&S.gq[hh][l16 * 8]);
+            const float4 qb = *reinterpret_cast<const float4*>(&S.gq[hh][l16 * 8 + 4]);
+            qv[0] = qa.x; qv[1] = qa.y; qv[2] = qa.z; qv[3] = qa.w;
+            qv[4] = qb.x; qv[5] = qb.y; qv[6] = qb.z; qv[7] = qb.w;
+            float pp[kGroup];
+            static_for<kGroup>([&](auto c) {
+                const uint32_t kk[4] = {kw[c].x, kw[c].y, kw[c].z, kw[c].w};
+                float a = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
+                    a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
+                }
+                pp[c] = row_tree_sum16(a);
+            });
+            if (l16 == 0)
+                static_for<kGroup>([&](auto c) {
+                    if (c < ncg) {
+                        const int tn = min(kAttnChunk, n - (c0 + c) * kAttnChunk);
+                        S.gs[hh][c * kAttnChunk + t] = t < tn ? pp[c] * scale : -__builtin_inff();
+                    }
+                });
+        }
+    }
+    __syncthreads();
+
+    // chunk partials: task (head hh, chunk c, half of the dims); wave w takes
+    // tasks w, w + 16, ...; each publishes its o values (and m, l) directly
+    {
+        const int ntask = 2 * G * ncg;
+        for (int task = w; task < ntask; task += kWaves) {
+            const int half = task & 1, hc = task >> 1, hh = hc / ncg, c = hc % ncg;
+            const int tn = min(kAttnChunk, n - (c0 + c) * kAttnChunk);
+            float m, ex, ls;
+            scores_softmax(&S.gs[hh][c * kAttnChunk], tn, m, ex, ls);
+            const int d = half * (kD / 2) + lane;
+            float o = 0.0f, unused = 0.0f;
+            v_chains<1>(&S.kv[c].v[d], nullptr, ex, 0.0f, o, unused);
+            uint64_t* cp = p.ll_part + (size_t(kvh * G + hh) * size_t(p.max_chunks) + size_t(c0 + c)) * pstride;
+            if (half == 0 && lane == 0) {
+                ll_store(cp, m, epoch_att);
+                ll_store(cp + 1, ls, epoch_att);
+            }
+            ll_store(cp + 2 + d, o, epoch_att);
+        }
+    }
+    // the item's LDS (K/V chunks, queries, scores) may be reused once every
+    // wave is done
+    __syncthreads();
+}
+
+// Entries i < count (64-bit {value, epoch}, at src_of(i)) into dst[i] as
+// floats, each polled until its epoch is current; input threads, NPT loads
+// in flight per thread.
+template <int NPT, class F>
+__device__ __forceinline__ void gather_entries(int count, F&& src_of, float* dst, uint32_t epoch, unsigned& budget,
+                                               int32_t* status)
+{
+    const int t = opaque_tid();
+    for (int base = 0; base < count; base += NPT * kIThreads) {
+        const uint64_t* a[NPT];
+        uint64_t v[NPT];
+        static_for<NPT>([&](auto j) {
+            a[j] = src_of(min(base + t + j * kIThreads, count - 1));
+            v[j] = __hip_atomic_load(const_cast<uint64_t*>(a[j]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        });
+        unsigned spins = 0;
+        while (budget != 0) {
+            int pending = 0;
+            static_for<NPT>([&](auto j) {
+                pending |= int(base + t + j * kIThreads < count) & int(!ll_ready(v[j], epoch));
+            });
+            if (!pending) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins == kSpinLimit) { budget = 0; atomicOr(status, HQ_STEP_SYNC); }
+            compiler_fence();
+            static_for<NPT>([&](auto j) {
+                if (base + t + j * kIThreads < count && !ll_ready(v[j], epoch))
+                    v[j] = __hip_atomic_load(const_cast<uint64_t*>(a[j]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            });
+        }
+        static_for<NPT>([&](auto j) {
+            const int i = base + t + j * kIThreads;
+            if (i < count) dst[i] = bits_f32(uint32_t(v[j]));
+        });
+    }
+}
+
+// The attention output from the GQA items' chunk partials: block b owns
+// output elements [e0, e0 + ne) of the qd = heads * D outputs (ne <= 256),
+// input thread T element e0 + T (head h, dim d).  For its head: M = max of
+// the chunks' m, a_c = exp(m_c - M), L = fmaf chain of a_c * l_c and O =
+// fmaf chain of a_c * o_c[d] over ascending chunks, out = O * (1 / L).  The
+// partials are staged in LDS (the K/V buffers, free after the items): in one
+// gather when all chunks fit, else in batches after a first pass for M.
+// The maxima are wave reductions and the a_c are computed by all threads;
+// only the L and O chains run per element, as the spec orders them.  The
+// four input waves meet at their barrier.
+constexpr int kCombineChunks = 512;   // chunks per staged batch (at most)
+__device__ void gqa_combine(const EngineParams& p, int nc, const Slot& z, uint32_t epoch_att, int& bseq,
+                            unsigned& budget)
+{
+    constexpr int pstride = kD + 2;
+    constexpr int kStage = int(sizeof(S.kv) / (sizeof(float)));
+    const int t = opaque_tid();
+    const int w = t / kWave;
+    const int qd = p.heads * kD;
+    const int e0 = split_begin(qd, blockIdx.x, gridDim.x);
+    const int ne = split_begin(qd, blockIdx.x + 1, gridDim.x) - e0;
+    if (ne <= 0) return;   // (block-uniform: no input wave of the block takes the barriers below)
+    const int h0 = e0 / kD;
+    const int nh = (e0 + ne - 1) / kD - h0 + 1;        // 1 or 2 heads
+    const int hi = (e0 + t) / kD - h0;                 // this thread's head (t < ne)
+    float* stage = reinterpret_cast<float*>(&S.kv[0]);
+    const uint64_t* part = p.ll_part;
+    const size_t hstride = size_t(p.max_chunks) * pstride;
+    const int cb2 = min(kCombineChunks, kStage / (2 * nh + ne));   // chunks per batch
+    const bool single = nc <= cb2;
+    // stage layout of a batch of nb chunks: m [nh][nb], l [nh][nb], o [ne][nb]
+    auto gather_batch = [&](int cb, int nb, bool with_lo) {
+        const int nm = nh * nb;
+        const int count = with_lo ? (2 * nh + ne) * nb : nm;
+        gather_entries<8>(count, [&](int i) {
+            if (i < 2 * nm) {
+                const int k = i / nb, c = cb + i % nb;       // k < nh: m of head k, else l of head k - nh
+                return part + size_t(h0 + (k < nh ? k : k - nh)) * hstride + size_t(c) * pstride + size_t(k >= nh);
+            }
+            const int j = i - 2 * nm, el = j / nb, c = cb + j % nb;
+            const int e = e0 + el;
+            return part + size_t(e / kD) * hstride + size_t(c) * pstride + 2 + size_t(e % kD);
+        }, stage, epoch_att, budget, p.status);
+    };
+    // M of each head (S.wmax[k]): wave k < nh reduces the m values of head k
+    for (int cb = 0; cb < nc; cb += cb2) {
+        const int nb = min(cb2, nc - cb);
+        gather_batch(cb, nb, single);
+        ibar(bseq, budget, p.status);
+        if (w < nh) {
+            float mm = -__builtin_inff();
+            for (int c = lane_id(); c < nb; c += kWave) mm = fmaxf(mm, stage[w * nb + c]);
+            mm = wave_max64_all(mm);
+            if (lane_id() == 0) S.wmax[w] = fmaxf(cb == 0 ? -__builtin_inff() : S.wmax[w], mm);
+        }
+        ibar(bseq, budget, p.status);
+    }
+    float L = 0.0f, O = 0.0f;
+    for (int cb = 0; cb < nc; cb += cb2) {
+        const int nb = min(cb2, nc - cb);
+        if (!single) {
+            gather_batch(cb, nb, true);
+            ibar(bseq, budget, p.status);
+        }
+        // a_c = exp(m_c - M) in place of the m values (every input thread)
+        for (int i = t; i < nh * nb; i += kIThreads) stage[i] = spec_expf(stage[i] - S.wmax[i / nb]);
+        ibar(bseq, budget, p.status);
+        if (t < ne) {
+            const float* sa = stage + hi * nb;
+            const float* sl = stage + (nh + hi) * nb;
+            const float* so = stage + 2 * nh * nb + t * nb;
+            int c = 0;
+            for (; c + 8 <= nb; c += 8) {
+                float av[8], lv[8], ov[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) { av[j] = sa[c + j]; lv[j] = sl[c + j]; ov[j] = so[c + j]; }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    L = __builtin_fmaf(av[j], lv[j], L);
+                    O = __builtin_fmaf(av[j], ov[j], O);
+                }
+            }
+            for (; c < nb; ++c) {
+                L = __builtin_fmaf(sa[c], sl[c], L);
+                O = __builtin_fmaf(sa[c], so[c], O);
+            }
+        }
+        ibar(bseq, budget, p.status);
+    }
+    if (t < ne) hs_store(z.att() + e0 + t, O * (1.0f / L));
+}
+
+// Per-head attention items (contexts of at most kGroup chunks): item h is
+// query head h, so the G items that read the same K/V chunks are
+// consecutive.  Round r of a layer gives block b item r*NB + k(b).  When
+// G == 4 and NB is a multiple of 32 (blocks go to the 8 XCDs round robin,
+// block b to XCD b % 8), k(b) places the four heads of one kv head on four
+// blocks of one XCD: they run together and read their K/V through that
+// XCD's L2 rather than four times over the fabric.  Otherwise k(b) = b.
+__device__ __forceinline__ int item_slot(int b, int NB, int G)
+{
+    if (G != 4 || (NB & 31) != 0) return b;
+    const int x = b & 7, rest = b >> 3;            // XCD, index within the XCD
+    return (((rest >> 2) << 3) + x) * 4 + (rest & 3);
+}
+
 // All attention items of a layer for this block, run by all sixteen waves
 // (the weight waves join after their qkv dots; every wave executes the same
-// barriers).  Items are (query head, group of up to kGroup chunks); the
-// input waves copy each item's K/V chunks, the block's first item's copies
-// having been started in P1.
+// barriers).  The input waves copy each item's K/V chunks, the block's first
+// item's copies having been started in P1.
 __device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, const Slot& z,
                                 uint32_t epoch_att, unsigned& budget)
 {
     const int n = pos + 1;
     const int nc = (n + kAttnChunk - 1) / kAttnChunk;
     const int ng = (nc + kGroup - 1) / kGroup;
-    const int items = p.heads * ng;
-    const int b = blockIdx.x;
-    for (int it = b; it < items; it += gridDim.x) {
-        if (it != b && opaque_tid() < kIThreads)
-            prefetch_group(p, l, (it / ng) / p.G, (it % ng) * kGroup, min(kGroup, nc - (it % ng) * kGroup), n, pos);
-        attention_item(p, Ly, l, it / ng, it % ng, ng, nc, n, pos, z, epoch_att, budget);
+    if (ng > 1) {
+        // GQA items, then every block combines its share of the output
+        const int cg = gqa_group(nc, p.kv_heads, gridDim.x);
+        const int ngq = (nc + cg - 1) / cg;
+        const int gitems = p.kv_heads * ngq;
+        for (int it = blockIdx.x; it < gitems; it += gridDim.x) {
+            const int kvh = it / ngq, g = it % ngq;
+            if (it != int(blockIdx.x) && is_copy_wave(opaque_tid() / kWave))
+                prefetch_group(p, l, kvh, g * cg, min(cg, nc - g * cg), n, pos);
+            gqa_item(p, Ly, l, kvh, g, ngq, cg, nc, n, pos, z, epoch_att, budget);
+        }
+        // (the input waves then combine the partials: gqa_combine, called
+        // from the input role only, so the weight role's code holds none of it)
+        return;
+    }
+    const int k = item_slot(blockIdx.x, gridDim.x, p.G);
+    for (int h = k; h < p.heads; h += gridDim.x) {
+        if (h != k && is_copy_wave(opaque_tid() / kWave)) prefetch_group(p, l, h / p.G, 0, nc, n, pos);
+        attention_item(p, Ly, l, h, nc, n, pos, z, budget);
     }
 }
 
@@ -1223,11 +1427,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
     const int H = p.H;
     const int qd = p.heads * kD;
     const int nown = R.h1 - R.h0;
-    const int n = pos + 1;
-    const int nc = (n + kAttnChunk - 1) / kAttnChunk;
-    const int ng = (nc + kGroup - 1) / kGroup;   // chunk groups per head
-    const int items = p.heads * ng;              // attention items: (query head, chunk group)
-    const int b = blockIdx.x;
     int bseq = 0;   // input-barrier count
     float xown = t0 < nown ? p.x[R.h0 + t0] : 0.0f;
 
@@ -1261,15 +1460,16 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             post_xq(act);
             TRACE(l, 3);
         }
-        // this layer's attention K/V: copies start now and land while the
-        // qkv hand-off travels
-        if (b < items) prefetch_group(p, l, (b / ng) / p.G, (b % ng) * kGroup, min(kGroup, nc - (b % ng) * kGroup), n, pos);
         wait_lds_geq(&S.done, kWWaves * (g + 1), budget, p.status);
         TRACE(l, 4);
         publish_rows(z.qkv() + R.q0, R.q1 - R.q0);
 
         // ---- P2: attention ------------------------------------------------------------
         attention_phase(p, Ly, l, pos, z, E + 2, budget);
+        {
+            const int nc = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
+            if (nc > kGroup) gqa_combine(p, nc, z, E + 2, bseq, budget);
+        }
 
         // ---- P3: quant -> (o) -> residual ---------------------------------------------
         float gpost[kHidNPT];
@@ -1432,7 +1632,8 @@ int engine_blocks(const hq_model* m)
     auto ceil_div = [](int a, int b) { return (a + b - 1) / b; };
     if (ceil_div(qrows, nb) > kWWaves * (kWave / kQkvLPR) || ceil_div(m->hidden, nb) > kWWaves ||
         ceil_div(m->hidden, nb) > kMaxOwn || 8 * ceil_div(m->intermediate / 8, nb) > kWWaves * 4 ||
-        ceil_div(qrows, nb) > kMaxRes || 8 * ceil_div(m->intermediate / 8, nb) > kMaxRes)
+        ceil_div(qrows, nb) > kMaxRes || 8 * ceil_div(m->intermediate / 8, nb) > kMaxRes ||
+        ceil_div(m->heads * kD, nb) > kIThreads)   // the attention combine's elements per block
         return 0;
     return nb;
 }
