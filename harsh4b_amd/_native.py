@@ -75,6 +75,8 @@ _SIGNATURES = {
     "hq_decode_step": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), vp], c_int),
     "hq_prefill_workspace_bytes": ([ctypes.POINTER(HqModel), c_int], c_size),
     "hq_prefill": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), vp, c_int, c_int, vp, vp], c_int),
+    "hq_decode_batch_workspace_bytes": ([ctypes.POINTER(HqModel), c_int], c_size),
+    "hq_decode_batch": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), c_int, c_int, vp, vp], c_int),
     "hq_step_gemv": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), c_int, c_int, vp], c_int),
     "hq_step_layers": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), vp], c_int),
     "hq_graph_capture": ([ctypes.POINTER(HqModel), ctypes.POINTER(HqState), c_int, vp,

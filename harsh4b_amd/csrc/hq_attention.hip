@@ -42,8 +42,8 @@ struct ChunkTile {
 };
 
 template <int D>
-__device__ __forceinline__ void load_chunk(const AttnParams& a, int t0, int tn, int skip_t,
-                                           size_t kv_off, uint4* kreg, uint4* vreg)
+__device__ __forceinline__ void load_chunk(const AttnParams& a, const uint16_t* keys, const uint16_t* values,
+                                           int t0, int tn, int skip_t, size_t kv_off, uint4* kreg, uint4* vreg)
 {
     using T = ChunkTile<D>;
 #pragma unroll
@@ -53,8 +53,8 @@ __device__ __forceinline__ void load_chunk(const AttnParams& a, int t0, int tn, 
         const int d8 = id % T::kGroupsPerRow;
         const bool ok = id < T::kGroups && t < tn && t != skip_t;
         const size_t off = size_t(t0 + t) * a.time_stride + kv_off + size_t(d8) * 8;
-        kreg[r] = ok ? *reinterpret_cast<const uint4*>(a.keys + off) : make_uint4(0, 0, 0, 0);
-        vreg[r] = ok ? *reinterpret_cast<const uint4*>(a.values + off) : make_uint4(0, 0, 0, 0);
+        kreg[r] = ok ? *reinterpret_cast<const uint4*>(keys + off) : make_uint4(0, 0, 0, 0);
+        vreg[r] = ok ? *reinterpret_cast<const uint4*>(values + off) : make_uint4(0, 0, 0, 0);
     }
 }
 
@@ -105,6 +105,19 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         pos = -1;
         n = a.context + int(blockIdx.z);     // query z of a batch sees z more positions
     }
+    const uint16_t* keys = a.keys;
+    const uint16_t* values = a.values;
+    if (!STEP && a.table) {
+        // batched decode: query z is sequence z at its own position, in its
+        // own cache (its layer slab: capacity * kv_heads * D elements)
+        const int z = blockIdx.z;
+        const int zpos = *a.table->position[z];
+        const int cap = a.table->capacity[z];
+        n = min(max(zpos, 0), cap - 1) + 1;
+        const size_t slab = size_t(cap) * size_t(a.kv_heads) * size_t(D);
+        keys = a.table->keys[z] + size_t(a.layer) * slab;
+        values = a.table->values[z] + size_t(a.layer) * slab;
+    }
     // per-query regions of a batch (blockIdx.z = 0 outside PLAIN batches)
     const size_t zq = size_t(blockIdx.z) * size_t(a.kv_heads) * G * D;
     float* const out = a.out + zq;
@@ -121,7 +134,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     uint4 kreg[T::kPerThread], vreg[T::kPerThread];
     {
         const int t0 = c_begin * C;
-        load_chunk<D>(a, t0, min(C, n - t0), c_begin == cur_chunk ? pos - t0 : -1, kv_off, kreg, vreg);
+        load_chunk<D>(a, keys, values, t0, min(C, n - t0), c_begin == cur_chunk ? pos - t0 : -1, kv_off, kreg, vreg);
     }
     __builtin_amdgcn_sched_barrier(0);   // the chunk loads go out before the query prologue
 
@@ -217,7 +230,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         __syncthreads();
         if (c + 1 < c_end) {
             const int t1 = t0 + C;
-            load_chunk<D>(a, t1, min(C, n - t1), c + 1 == cur_chunk ? pos - t1 : -1, kv_off, kreg,
+            load_chunk<D>(a, keys, values, t1, min(C, n - t1), c + 1 == cur_chunk ? pos - t1 : -1, kv_off, kreg,
                           vreg);
         }
         __builtin_amdgcn_sched_barrier(0);

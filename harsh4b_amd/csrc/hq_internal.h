@@ -44,6 +44,23 @@ hipError_t launch_step_gemv(StepGemv kind, const GemvParams& p, hipStream_t s);
 // ---- attention ---------------------------------------------------------------
 constexpr int kAttnChunk = 64;   // positions per split (the spec's chunk)
 
+// Per-sequence device pointers of a batched decode step (hq_decode_batch):
+// sequence z has its own KV cache, position, token, status, residual and
+// logits.  Lives in the step's workspace (written by a kernel from a launch
+// argument, so a captured graph replays it).
+constexpr int kMaxDecodeBatch = 32;
+struct BatchTable {
+    uint16_t* keys[kMaxDecodeBatch];     // fp16 [layers, capacity, kv_heads, head_dim]
+    uint16_t* values[kMaxDecodeBatch];
+    int32_t* position[kMaxDecodeBatch];
+    int32_t* token[kMaxDecodeBatch];
+    int32_t* status[kMaxDecodeBatch];
+    float* x[kMaxDecodeBatch];
+    float* logits[kMaxDecodeBatch];
+    int32_t capacity[kMaxDecodeBatch];
+    int32_t count;
+};
+
 struct AttnParams {
     // PLAIN mode: q given; STEP mode: raw qkv + norms + rope + KV write
     const float* q;             // PLAIN: [kv*groups, D]
@@ -68,6 +85,11 @@ struct AttnParams {
     float* part;                // [heads, max_chunks, head_dim + 2]
     int32_t* counters;          // [kv_heads], zero between launches
     float* out;                 // [heads, D]
+    // PLAIN batches of a batched decode step (nullable): query z attends the
+    // cache of sequence z (layer `layer`) up to its position, table->position[z]
+    // + 1 positions; keys, values and context above are then unused
+    const BatchTable* table;
+    int layer;
 };
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);

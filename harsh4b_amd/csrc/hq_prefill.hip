@@ -17,6 +17,14 @@
 // Each row kernel restates the decode path's prologue for one token per
 // block (256-lane fmaf partials, tree sum, quantize with the spec rounding)
 // and writes the int8 row de-interleaved, as the GEMM reads it.
+//
+// The batched decode step (hq_decode_batch) runs the same layer sequence for
+// the current token of up to kMaxDecodeBatch independent sequences, each
+// with its own KV cache and position (a per-sequence pointer table in the
+// workspace), then the final RMSNorm, the tied LM head as one GEMM over the
+// batch and a per-sequence argmax that feeds each greedy token back on the
+// device: M forward_token steps (cpu_lightspark.py:424-468) sharing every
+// weight read, bit-identical to them.
 #include <algorithm>
 
 #include "hq_device.h"
@@ -254,6 +262,216 @@ static int run_rows(int mode, RowParams p, int rows, hipStream_t s)
     return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }
 
+
+// ---- batched decode step ----------------------------------------------------------
+
+__global__ void batch_table_kernel(BatchTable t, BatchTable* dst)
+{
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&t);
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+    for (int i = threadIdx.x; i < int(sizeof(BatchTable) / 4); i += blockDim.x) d[i] = src[i];
+}
+
+// Block m: the embedding row of sequence m's current token (a token outside
+// the vocabulary is flagged and replaced by 0, a full cache flagged), as
+// embedding_kernel does for one sequence.
+__global__ __launch_bounds__(kBlock) void batch_embed_kernel(const uint8_t* emb, const float* emb_scales, int vocab,
+                                                             int hidden, const BatchTable* T, float* x)
+{
+    const int m = blockIdx.x;
+    int t = *T->token[m];
+    const int pos = *T->position[m];
+    if (threadIdx.x == 0 && (pos < 0 || pos >= T->capacity[m])) atomicOr(T->status[m], HQ_STEP_FULL);
+    if (t < 0 || t >= vocab) {
+        if (threadIdx.x == 0) atomicOr(T->status[m], HQ_STEP_BAD_TOKEN);
+        t = 0;
+    }
+    const int half = hidden >> 1;
+    const uint8_t* row = emb + size_t(t) * size_t(half);
+    const float s = emb_scales[t];
+    float* xr = x + size_t(m) * hidden;
+    for (int j = threadIdx.x; j < half; j += kBlock) {
+        const uint8_t b = row[j];
+        const int lo = int(int8_t(uint8_t(b << 4))) >> 4;
+        const int hi = int(int8_t(b)) >> 4;
+        xr[2 * j] = float(lo) * s;
+        xr[2 * j + 1] = float(hi) * s;
+    }
+}
+
+// prefill_qk_kernel for the batch: token m is sequence m at its own position,
+// its K/V rows go to its own cache (layer `layer`); a position outside the
+// cache (flagged by the embedding kernel) writes nothing.
+__global__ __launch_bounds__(kBlock) void batch_qk_kernel(QkParams p, const BatchTable* T, int layer)
+{
+    constexpr int D = 128;
+    const int m = blockIdx.x;
+    const int slot = blockIdx.y * (kBlock / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int total = p.heads + 2 * p.kv_heads;
+    if (slot >= total) return;
+    const int cap = T->capacity[m];
+    const int raw = *T->position[m];
+    const bool inside = raw >= 0 && raw < cap;
+    const int pos = min(max(raw, 0), cap - 1);
+    const size_t slab = size_t(cap) * size_t(p.kv_heads) * D;
+    uint16_t* keys = T->keys[m] + size_t(layer) * slab;
+    uint16_t* values = T->values[m] + size_t(layer) * slab;
+    const float* src = p.qkv + size_t(m) * total * D + size_t(slot) * D;
+    const float x0 = src[lane], x1 = src[lane + 64];
+    if (slot >= p.heads + p.kv_heads) {
+        if (inside) {
+            uint16_t* vdst = values + size_t(pos) * p.time_stride + size_t(slot - p.heads - p.kv_heads) * D;
+            vdst[lane] = f32_to_f16(x0);
+            vdst[lane + 64] = f32_to_f16(x1);
+        }
+        return;
+    }
+    const bool is_q = slot < p.heads;
+    const float* w = is_q ? p.q_norm : p.k_norm;
+    float s = __builtin_fmaf(x0, x0, 0.0f);
+    s = __builtin_fmaf(x1, x1, s);
+    const float ss = wave_tree_sum64_all(s);
+    const float r = __builtin_sqrtf(ss / float(D) + p.eps);
+    const float y0 = (x0 / r) * w[lane];
+    const float y1 = (x1 / r) * w[lane + 64];
+    const float c0 = p.rope_cos[size_t(pos) * (D / 2) + lane];
+    const float s0 = p.rope_sin[size_t(pos) * (D / 2) + lane];
+    const float a = y0 * c0 - y1 * s0;
+    const float b = y1 * c0 + y0 * s0;
+    if (is_q) {
+        float* qd = p.q + size_t(m) * p.heads * D + size_t(slot) * D;
+        qd[lane] = a;
+        qd[lane + 64] = b;
+    } else if (inside) {
+        uint16_t* kdst = keys + size_t(pos) * p.time_stride + size_t(slot - p.heads) * D;
+        kdst[lane] = f32_to_f16(a);
+        kdst[lane + 64] = f32_to_f16(b);
+    }
+}
+
+// Block (b, m): logits [b*kArgPer, ...) of sequence m copied to its state's
+// logits and reduced to a (value, index) partial with np.argmax's order; the
+// last block of the row (two-level ticket) writes the greedy token and
+// advances the position, as the single step's LM head does.
+constexpr int kBatchArgPer = kBlock * 16;
+__global__ __launch_bounds__(kBlock) void batch_argmax_kernel(const float* logits, int vocab, const BatchTable* T,
+                                                              float* pval, int32_t* pidx, int32_t* counters)
+{
+    __shared__ float sv[kBlock / kWave];
+    __shared__ int si[kBlock / kWave];
+    __shared__ int last_flag;
+    const int tid = threadIdx.x;
+    const int m = blockIdx.y;
+    const int nb = gridDim.x;
+    const float* row = logits + size_t(m) * size_t(vocab);
+    float* dst = T->logits[m];
+    float v = -__builtin_inff();
+    int idx = 0x7FFFFFFF;
+    const int base = blockIdx.x * kBatchArgPer;
+    for (int i = base + tid; i < min(vocab, base + kBatchArgPer); i += kBlock) {
+        const float x = row[i];
+        dst[i] = x;
+        if (argmax_better(x, i, v, idx)) { v = x; idx = i; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o, kWave);
+        const int oi = __shfl_xor(idx, o, kWave);
+        if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
+    }
+    if ((tid & (kWave - 1)) == 0) { sv[tid / kWave] = v; si[tid / kWave] = idx; }
+    __syncthreads();
+    float* pv = pval + size_t(m) * nb;
+    int32_t* pi = pidx + size_t(m) * nb;
+    if (tid == 0) {
+        for (int w = 1; w < kBlock / kWave; ++w)
+            if (argmax_better(sv[w], si[w], v, idx)) { v = sv[w]; idx = si[w]; }
+        publish_f(pv + blockIdx.x, v);
+        publish_i(pi + blockIdx.x, idx);
+        wait_all_memory();
+        last_flag = last_block_ticket(counters + size_t(m) * ticket_words(nb), blockIdx.x, nb);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    v = -__builtin_inff();
+    idx = 0x7FFFFFFF;
+    for (int b = tid; b < nb; b += kBlock) {
+        const float bv = read_f(pv + b);
+        const int bi = read_i(pi + b);
+        if (argmax_better(bv, bi, v, idx)) { v = bv; idx = bi; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o, kWave);
+        const int oi = __shfl_xor(idx, o, kWave);
+        if (argmax_better(ov, oi, v, idx)) { v = ov; idx = oi; }
+    }
+    __syncthreads();
+    if ((tid & (kWave - 1)) == 0) { sv[tid / kWave] = v; si[tid / kWave] = idx; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kBlock / kWave; ++w)
+            if (argmax_better(sv[w], si[w], v, idx)) { v = sv[w]; idx = si[w]; }
+        *T->token[m] = idx;
+        const int pos = *T->position[m];
+        if (pos >= 0 && pos < T->capacity[m]) *T->position[m] = pos + 1;
+    }
+}
+
+// The batch's residual rows back into each state's x (the single step leaves
+// the final residual there).
+__global__ __launch_bounds__(kBlock) void batch_store_x_kernel(const float* x, int hidden, const BatchTable* T)
+{
+    const int m = blockIdx.x;
+    for (int i = threadIdx.x; i < hidden; i += kBlock) T->x[m][i] = x[size_t(m) * hidden + i];
+}
+
+struct BatchLayout {
+    size_t x, q8, act, qkv, qh, att, proj, gu, gemm, attn_counters, attn_part, logits, pval, pidx, tickets, table,
+        total;
+    int kp, max_chunks, qkv_rows, qd, arg_blocks;
+};
+
+static BatchLayout batch_layout(const hq_model* m, int max_capacity)
+{
+    BatchLayout L{};
+    const int B = kMaxDecodeBatch;
+    const int H = m->hidden, I = m->intermediate, D = m->head_dim, V = m->vocab;
+    L.qd = m->heads * D;
+    L.qkv_rows = L.qd + 2 * m->kv_heads * D;
+    int kmax = H > L.qd ? H : L.qd;
+    if (I > kmax) kmax = I;
+    L.kp = gemm_padded_k(kmax);
+    L.max_chunks = (max_capacity + kAttnChunk - 1) / kAttnChunk;
+    L.arg_blocks = (V + kBatchArgPer - 1) / kBatchArgPer;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t at = off; off += al256p(bytes); return at; };
+    L.x = take(size_t(B) * H * 4);
+    L.q8 = take(size_t(gemm_padded_m(B)) * L.kp);
+    L.act = take(size_t(B) * 4);
+    L.qkv = take(size_t(B) * L.qkv_rows * 4);
+    L.qh = take(size_t(B) * L.qd * 4);
+    L.att = take(size_t(B) * L.qd * 4);
+    L.proj = take(size_t(B) * H * 4);
+    L.gu = take(size_t(B) * 2 * I * 4);
+    size_t g = gemm_scratch_bytes(B, L.qkv_rows, H);
+    g = std::max<size_t>(g, gemm_scratch_bytes(B, H, L.qd));
+    g = std::max<size_t>(g, gemm_scratch_bytes(B, 2 * I, H));
+    g = std::max<size_t>(g, gemm_scratch_bytes(B, H, I));
+    g = std::max<size_t>(g, gemm_scratch_bytes(B, V, H));
+    L.gemm = take(g);
+    L.attn_counters = take(size_t(B) * m->kv_heads * 4);
+    L.attn_part = take(size_t(B) * attention_workspace_floats(m->heads, L.max_chunks, D) * 4);
+    L.logits = take(size_t(B) * V * 4);
+    L.pval = take(size_t(B) * L.arg_blocks * 4);
+    L.pidx = take(size_t(B) * L.arg_blocks * 4);
+    L.tickets = take(size_t(B) * ticket_words(L.arg_blocks) * 4);
+    L.table = take(sizeof(BatchTable));
+    L.total = off;
+    return L;
+}
+
 }  // namespace hq
 
 using namespace hq;
@@ -367,4 +585,138 @@ extern "C" int hq_prefill(const hq_model* m, const hq_state* st, const int32_t* 
     }
     hipLaunchKernelGGL(prefill_position_kernel, dim3(1), dim3(1), 0, s, st->position, start + count);
     return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
+}
+
+extern "C" size_t hq_decode_batch_workspace_bytes(const hq_model* model, int max_capacity)
+{
+    if (!prefill_fits(model) || max_capacity <= 0) return 0;
+    return batch_layout(model, max_capacity).total;
+}
+
+extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int count, int max_capacity,
+                               void* workspace, void* stream)
+{
+    if (!prefill_fits(m) || !states || !workspace || count < 1 || count > kMaxDecodeBatch || max_capacity <= 0)
+        return HQ_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u) return HQ_ERR_ALIGN;
+    if (!m->embedding || !m->embedding_scales || !m->final_norm || !m->rope_cos || !m->rope_sin) return HQ_ERR_ARG;
+    BatchTable t{};
+    t.count = count;
+    for (int i = 0; i < count; ++i) {
+        const hq_state& st = states[i];
+        if (st.capacity <= 0 || st.capacity > max_capacity || st.capacity > m->rope_positions) return HQ_ERR_ARG;
+        if (!st.keys || !st.values || !st.position || !st.token || !st.status || !st.x || !st.logits)
+            return HQ_ERR_ARG;
+        if ((reinterpret_cast<uintptr_t>(st.keys) & 15u) || (reinterpret_cast<uintptr_t>(st.values) & 15u))
+            return HQ_ERR_ALIGN;
+        t.keys[i] = st.keys;
+        t.values[i] = st.values;
+        t.position[i] = st.position;
+        t.token[i] = st.token;
+        t.status[i] = st.status;
+        t.x[i] = st.x;
+        t.logits[i] = st.logits;
+        t.capacity[i] = st.capacity;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const BatchLayout L = batch_layout(m, max_capacity);
+    char* ws = static_cast<char*>(workspace);
+    float* x = reinterpret_cast<float*>(ws + L.x);
+    int8_t* q8 = reinterpret_cast<int8_t*>(ws + L.q8);
+    float* act = reinterpret_cast<float*>(ws + L.act);
+    float* qkv = reinterpret_cast<float*>(ws + L.qkv);
+    float* qh = reinterpret_cast<float*>(ws + L.qh);
+    float* att = reinterpret_cast<float*>(ws + L.att);
+    float* proj = reinterpret_cast<float*>(ws + L.proj);
+    float* gu = reinterpret_cast<float*>(ws + L.gu);
+    float* logits = reinterpret_cast<float*>(ws + L.logits);
+    char* gemm = ws + L.gemm;
+    BatchTable* table = reinterpret_cast<BatchTable*>(ws + L.table);
+    const int H = m->hidden, I = m->intermediate, D = m->head_dim, KV = m->kv_heads, M = count;
+    const long long time_stride = (long long)KV * D;
+    const int slots = (m->heads + 2 * KV + kBlock / kWave - 1) / (kBlock / kWave);
+    auto ok = [] { return hipGetLastError() == hipSuccess; };
+    hipLaunchKernelGGL(batch_table_kernel, dim3(1), dim3(kBlock), 0, s, t, table);
+    hipLaunchKernelGGL(batch_embed_kernel, dim3(M), dim3(kBlock), 0, s, m->embedding, m->embedding_scales, m->vocab,
+                       H, table, x);
+    if (!ok()) return HQ_ERR_LAUNCH;
+    RowParams rp{};
+    rp.eps = m->eps;
+    rp.q = q8;
+    rp.act = act;
+    int e;
+    for (int l = 0; l < m->layers; ++l) {
+        const hq_layer& Ly = m->layer[l];
+        rp.x = x;
+        rp.add = proj;
+        rp.gate_up = nullptr;
+        rp.gamma = Ly.input_norm;
+        rp.k = H;
+        if ((e = run_rows(l == 0 ? ROW_NORM : ROW_RESID_NORM, rp, M, s))) return e;
+        if (gemm_run(q8, act, Ly.qkv, Ly.qkv_scales, qkv, M, L.qkv_rows, H, gemm, s) != hipSuccess)
+            return HQ_ERR_LAUNCH;
+        QkParams qp{};
+        qp.qkv = qkv;
+        qp.q_norm = Ly.q_norm;
+        qp.k_norm = Ly.k_norm;
+        qp.rope_cos = m->rope_cos;
+        qp.rope_sin = m->rope_sin;
+        qp.eps = m->eps;
+        qp.heads = m->heads;
+        qp.kv_heads = KV;
+        qp.time_stride = time_stride;
+        qp.q = qh;
+        hipLaunchKernelGGL(batch_qk_kernel, dim3(M, slots), dim3(kBlock), 0, s, qp, (const BatchTable*)table, l);
+        if (!ok()) return HQ_ERR_LAUNCH;
+        AttnParams a{};
+        a.q = qh;
+        a.time_stride = time_stride;
+        a.context = 1;
+        a.batch = M;
+        a.kv_heads = KV;
+        a.groups = m->heads / KV;
+        a.head_dim = D;
+        a.max_chunks = L.max_chunks;
+        a.counters = reinterpret_cast<int32_t*>(ws + L.attn_counters);
+        a.part = reinterpret_cast<float*>(ws + L.attn_part);
+        a.out = att;
+        a.table = table;
+        a.layer = l;
+        if (launch_attention(a, false, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        rp.x = att;
+        rp.add = nullptr;
+        rp.gamma = nullptr;
+        rp.k = m->heads * D;
+        if ((e = run_rows(ROW_PLAIN, rp, M, s))) return e;
+        if (gemm_run(q8, act, Ly.o, Ly.o_scales, proj, M, H, rp.k, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        rp.x = x;
+        rp.add = proj;
+        rp.gamma = Ly.post_norm;
+        rp.k = H;
+        if ((e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
+        if (gemm_run(q8, act, Ly.gate_up, Ly.gate_up_scales, gu, M, 2 * I, H, gemm, s) != hipSuccess)
+            return HQ_ERR_LAUNCH;
+        rp.x = nullptr;
+        rp.add = nullptr;
+        rp.gate_up = gu;
+        rp.gamma = nullptr;
+        rp.k = I;
+        if ((e = run_rows(ROW_SWIGLU, rp, M, s))) return e;
+        if (gemm_run(q8, act, Ly.down, Ly.down_scales, proj, M, H, I, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
+    }
+    // the last layer's down output into the residual, final RMSNorm, tied LM
+    // head over the batch, per-sequence argmax and position advance
+    rp.x = x;
+    rp.add = proj;
+    rp.gate_up = nullptr;
+    rp.gamma = m->final_norm;
+    rp.k = H;
+    if ((e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
+    if (gemm_run(q8, act, m->embedding, m->embedding_scales, logits, M, m->vocab, H, gemm, s) != hipSuccess)
+        return HQ_ERR_LAUNCH;
+    hipLaunchKernelGGL(batch_argmax_kernel, dim3(L.arg_blocks, M), dim3(kBlock), 0, s, logits, m->vocab,
+                       (const BatchTable*)table, reinterpret_cast<float*>(ws + L.pval),
+                       reinterpret_cast<int32_t*>(ws + L.pidx), reinterpret_cast<int32_t*>(ws + L.tickets));
+    hipLaunchKernelGGL(batch_store_x_kernel, dim3(M), dim3(kBlock), 0, s, x, H, (const BatchTable*)table);
+    return ok() ? HQ_OK : HQ_ERR_LAUNCH;
 }

@@ -131,6 +131,11 @@ class QwenDecodeState:
     keeps fp32; the benchmark configurations specify fp16).  Position and the
     current token also live on the device so a captured HIP graph of a step is
     valid at every position; ``position`` here is the host's mirror of it.
+
+    ``stream`` is the model's stream, shared by every state of the model: a
+    step's persistent layer kernel needs every CU of the GPU at once, so the
+    steps of different sequences run one after another, never side by side
+    (concurrent launches would starve each other's waits, HQ_STEP_SYNC).
     """
 
     def __init__(self, model: "LiteSparkQwen", capacity: int):
@@ -168,7 +173,7 @@ class QwenDecodeState:
         if nbytes == 0:
             raise ValueError("model shape is not supported by the decode step")
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-        self.stream = torch.cuda.Stream(device=dev)
+        self.stream = model.stream
         self.stream.wait_stream(torch.cuda.current_stream(dev))
         s = HqState()
         s.capacity = capacity
@@ -263,6 +268,11 @@ class LiteSparkQwen:
         m.device_layer = self._layer_table.data_ptr()
         m.flags = 0
         self.struct = m
+        self._batch_workspaces: dict[int, torch.Tensor] = {}
+        self._batch_graph = None   # (key, graph, states) of the last captured batched step
+        # every decode state of the model enqueues on this one stream (see
+        # QwenDecodeState), and so does the batched step
+        self.stream = torch.cuda.Stream(device=self.device)
 
     @property
     def layer_kernel_blocks(self) -> int:
@@ -376,6 +386,101 @@ class LiteSparkQwen:
         state.position += steps
         if check_status:
             state.check_status()
+
+    # -- batched decode (M independent sequences) -------------------------------
+    MAX_BATCH = 32
+
+    def _batch_setup(self, states):
+        m = len(states)
+        if not 1 <= m <= self.MAX_BATCH:
+            raise ValueError(f"a batched step takes 1 to {self.MAX_BATCH} decode states")
+        if len({id(st) for st in states}) != m:
+            raise ValueError("a decode state appears twice in the batch")
+        for st in states:
+            if st.model is not self:
+                raise ValueError("a decode state belongs to another model")
+        cap = max(st.capacity for st in states)
+        ws = self._batch_workspaces.get(cap)
+        if ws is None:
+            nbytes = _native.lib().hq_decode_batch_workspace_bytes(ctypes.byref(self.struct), cap)
+            if nbytes == 0:
+                raise ValueError("model shape is not supported by the batched decode step")
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+            self._batch_workspaces[cap] = ws
+        table = (HqState * m)(*[st.struct for st in states])
+        stream = self.stream
+        stream.wait_stream(torch.cuda.current_stream(self.device))   # the workspace's zero fill
+        for st in states:
+            stream.wait_stream(st.stream)
+        return table, cap, ws, stream
+
+    def _batch_release(self, states, stream) -> None:
+        for st in states:
+            st.stream.wait_stream(stream)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+
+    def forward_tokens(self, token_ids, states) -> list[torch.Tensor]:
+        """One decode step for each (token, state) pair of a batch of up to 32
+        independent sequences: the reference's forward_token
+        (cpu_lightspark.py:424-468) applied to each pair, with the same bits,
+        in one hq_decode_batch call that reads every weight once for the
+        whole batch.  Returns each state's logits (device tensors); each
+        greedy token is left in its ``state.token``."""
+        states = list(states)
+        ids = [int(t) for t in token_ids]
+        if len(ids) != len(states):
+            raise ValueError("one token per decode state")
+        for t, st in zip(ids, states):
+            self._check_token(t, st)
+        table, cap, ws, stream = self._batch_setup(states)
+        with torch.cuda.stream(stream):
+            for t, st in zip(ids, states):
+                st.token.fill_(t)
+        check(_native.lib().hq_decode_batch(ctypes.byref(self.struct), table, len(states), cap, ws.data_ptr(),
+                                            stream.cuda_stream), "hq_decode_batch")
+        for st in states:
+            st.position += 1
+        self._batch_release(states, stream)
+        return [st.logits for st in states]
+
+    def decode_greedy_batch(self, states, steps: int, use_graph: bool = True, check_status: bool = True) -> None:
+        """`steps` batched greedy steps over the states, each feeding its
+        argmax token back on the device (the tokens already in the states'
+        ``token`` are consumed first), replayed from one captured HIP graph
+        of the batched step.  With `check_status` the call waits and raises
+        on any state's device status."""
+        states = list(states)
+        for st in states:
+            if st.position + steps > st.capacity:
+                raise ValueError("decode state capacity exhausted")
+        table, cap, ws, stream = self._batch_setup(states)
+        lib = _native.lib()
+        if use_graph:
+            # the graph holds the states' device pointers: it is kept with the
+            # states themselves (so they outlive it) and only for this batch
+            key = (tuple(bytes(st.struct) for st in states), cap)
+            if self._batch_graph is None or self._batch_graph[0] != key:
+                graph = torch.cuda.CUDAGraph()
+                err = 0
+                with torch.cuda.graph(graph, stream=stream):
+                    err = lib.hq_decode_batch(ctypes.byref(self.struct), table, len(states), cap, ws.data_ptr(),
+                                              stream.cuda_stream)
+                check(err, "hq_decode_batch (graph capture)")
+                self._batch_graph = (key, graph, states)
+            graph = self._batch_graph[1]
+            with torch.cuda.stream(stream):
+                for _ in range(steps):
+                    graph.replay()
+        else:
+            for _ in range(steps):
+                check(lib.hq_decode_batch(ctypes.byref(self.struct), table, len(states), cap, ws.data_ptr(),
+                                          stream.cuda_stream), "hq_decode_batch")
+        for st in states:
+            st.position += steps
+        self._batch_release(states, stream)
+        if check_status:
+            for st in states:
+                st.check_status()
 
     def decode_sampled(self, state: QwenDecodeState, steps: int, args, generator, generated) -> list[int]:
         """`steps` iterations of the reference's stochastic decode loop

@@ -249,6 +249,26 @@ size_t hq_prefill_workspace_bytes(const hq_model* model, int capacity);
 int hq_prefill(const hq_model* model, const hq_state* state, const int32_t* tokens, int count, int start,
                void* workspace, void* stream);
 
+/* Batched decode: one decode step for each of `count` (1..32) independent
+ * sequences, each with its own hq_state (KV cache, position, token, status,
+ * residual, logits), as `count` hq_decode_step calls would run them and with
+ * the same bits, but sharing every weight read: per layer the body
+ * projections are int8 MFMA GEMMs over the batch, attention runs over each
+ * sequence's own cache and context, and the tied LM head is one GEMM over
+ * the batch followed by a per-sequence argmax that writes each greedy token
+ * to *state->token and advances *state->position.  No reference
+ * counterpart (forward_token is batch 1, cpu_lightspark.py:424-468; the
+ * reference runtime keeps one session per request, inference_runtime.py:
+ * 177-184): the contract is M forward_token steps.  `states` is a HOST array
+ * of count structs; every state's capacity must be <= max_capacity, the
+ * capacity the workspace was sized for: hq_decode_batch_workspace_bytes(
+ * model, max_capacity) bytes, 256-byte aligned, zero-filled before first use
+ * (its counters are left at zero by every call).  A full cache sets
+ * HQ_STEP_FULL and a bad token HQ_STEP_BAD_TOKEN in that state's status. */
+size_t hq_decode_batch_workspace_bytes(const hq_model* model, int max_capacity);
+int hq_decode_batch(const hq_model* model, const hq_state* states, int count, int max_capacity,
+                    void* workspace, void* stream);
+
 /* Launch one body GEMV of the step (the kernel the step launches) for one
  * layer on the state's buffers, so a kernel can be timed in isolation.
  * kind: 0 = RMSNorm+qkv, 1 = o + residual, 2 = RMSNorm+gate_up+SwiGLU,

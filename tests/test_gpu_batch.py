@@ -1,0 +1,132 @@
+"""GPU parity of the batched decode step (hq_decode_batch): M independent
+sequences stepped together must give, for every sequence, the bits M
+separate forward_token steps give (cpu_lightspark.py:424-468 in the
+reference repository, applied to each sequence): logits, greedy tokens, the
+K/V rows written, the residual and the position; and the oracle's logits."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.gpu_util import assert_bits_equal, to_host
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+KEYS = ("qkv", "qkv_scales", "o", "o_scales", "gate_up", "gate_up_scales", "down",
+        "down_scales", "input_norm", "post_norm", "q_norm", "k_norm")
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[gpu] {request.node.nodeid}", flush=True)
+    yield
+    torch.cuda.synchronize()
+
+
+def golden_model(g):
+    from harsh4b_amd.synthetic import model_from_arrays
+    arrays = {k: [np.ascontiguousarray(a) for a in g[k]] for k in KEYS}
+    for k in ("embedding", "embedding_scales", "final_norm"):
+        arrays[k] = np.ascontiguousarray(g[k])
+    return model_from_arrays(g["config"], arrays)
+
+
+def _compare(model, batched, single, tag):
+    """Batched states against single-step states: positions, tokens, logits,
+    residual and every K/V row written so far, bit for bit."""
+    for i, (a, b) in enumerate(zip(batched, single)):
+        assert a.position == b.position, (tag, i)
+        assert int(a.device_position.item()) == int(b.device_position.item()) == a.position, (tag, i)
+        assert model.greedy_token(a) == model.greedy_token(b), (tag, i)
+        assert_bits_equal(to_host(a.logits), to_host(b.logits), f"{tag} logits {i}")
+        assert_bits_equal(to_host(a.x), to_host(b.x), f"{tag} residual {i}")
+        n = a.position
+        assert_bits_equal(to_host(a.keys)[:, :n].view(np.uint16), to_host(b.keys)[:, :n].view(np.uint16),
+                          f"{tag} keys {i}")
+        assert_bits_equal(to_host(a.values)[:, :n].view(np.uint16), to_host(b.values)[:, :n].view(np.uint16),
+                          f"{tag} values {i}")
+        a.check_status()
+        b.check_status()
+
+
+def test_tiny_model_batch_matches_single_steps_and_oracle(forward_golden):
+    g = forward_golden
+    model = golden_model(g)
+    toks = [int(t) for t in g["tokens"]]
+    histories = [[], toks[:1], toks[:3], toks[:6]]
+    nxt = [toks[0], toks[2], toks[4], toks[1]]
+    cap = 12
+    A = [model.new_state(cap) for _ in histories]
+    B = [model.new_state(cap) for _ in histories]
+    for st_a, st_b, h in zip(A, B, histories):
+        for t in h:
+            model.forward_token(t, st_a)
+            model.forward_token(t, st_b)
+    model.forward_tokens(nxt, A)
+    for t, st in zip(nxt, B):
+        model.forward_token(t, st)
+    _compare(model, A, B, "tiny step")
+    # the oracle, sequence by sequence
+    from harsh4b_amd.synthetic import host_arrays
+    ref = oracle.OracleModel(model.config, host_arrays(model))
+    for i, (h, t) in enumerate(zip(histories, nxt)):
+        rs = ref.new_state(cap)
+        for u in h + [t]:
+            ref.forward_token(u, rs)
+        assert_bits_equal(to_host(A[i].logits), rs.logits, f"oracle logits {i}")
+    # then three batched greedy steps from a captured graph against
+    # decode_greedy on each single state
+    model.decode_greedy_batch(A, 3)
+    for st in B:
+        model.decode_greedy(st, 3)
+    _compare(model, A, B, "tiny greedy")
+
+
+def test_batch_rejects_bad_input(forward_golden):
+    g = forward_golden
+    model = golden_model(g)
+    st = model.new_state(2)
+    with pytest.raises(ValueError, match="one token per"):
+        model.forward_tokens([1, 2], [st])
+    with pytest.raises(ValueError, match="twice"):
+        model.forward_tokens([1, 2], [st, st])
+    with pytest.raises(ValueError, match="outside the vocabulary"):
+        model.forward_tokens([int(g["config"]["vocab_size"])], [st])
+    with pytest.raises(ValueError, match="1 to 32"):
+        model.forward_tokens([], [])
+
+
+@pytest.fixture(scope="module")
+def qwen():
+    from harsh4b_amd.config import QWEN3_4B
+    from harsh4b_amd.synthetic import random_model
+    model = random_model(QWEN3_4B, seed=11)
+    torch.cuda.synchronize()
+    return model
+
+
+@pytest.mark.parametrize("m", [8, 32])
+def test_qwen3_4b_batch_matches_single_steps(qwen, m):
+    # M sequences with histories of 1 .. 300 positions (one to five chunks
+    # of attention, one to two chunk groups), stepped together and alone
+    model = qwen
+    rng = np.random.default_rng(100 + m)
+    lengths = [int(v) for v in rng.integers(1, 300, m)]
+    lengths[0], lengths[-1] = 1, 300
+    prompts = [[int(t) for t in rng.integers(0, 151936, n)] for n in lengths]
+    A, B = [], []
+    for pr in prompts:
+        for group in (A, B):
+            st = model.new_state(len(pr) + 4)
+            model.prefill(pr, st)
+            group.append(st)
+    nxt = [int(t) for t in rng.integers(0, 151936, m)]
+    model.forward_tokens(nxt, A)
+    for t, st in zip(nxt, B):
+        model.forward_token(t, st)
+    _compare(model, A, B, f"M={m} step")
+    model.decode_greedy_batch(A, 2)
+    for st in B:
+        model.decode_greedy(st, 2)
+    _compare(model, A, B, f"M={m} greedy")
