@@ -261,96 +261,132 @@ def bench_gemv(args):
     print(json.dumps(result), flush=True)
 
 
+def batched_step_bytes(config, m, context):
+    """Algorithmic bytes of one batched decode step of m sequences at
+    `context` positions each: every weight once (packed body, row scales,
+    norm weights, the tied int4 LM head and its scales), each sequence's
+    K/V rows (fp16, context - 1 read + 1 written per layer), its embedding
+    row, RoPE rows and logits."""
+    from harsh4b_amd.config import body_bytes, shapes
+    L = int(config["num_hidden_layers"])
+    h = int(config["hidden_size"])
+    d = int(config["head_dim"])
+    kvh = int(config["num_key_value_heads"])
+    v = int(config["vocab_size"])
+    weights = body_bytes(config) + 4 * L * sum(r for r, _ in shapes(config).values()) + 4 * L * (2 * h + 2 * d)
+    lm_head = v * h // 2 + 4 * v + 4 * h
+    per_seq = L * 2 * kvh * d * 2 * context + h // 2 + 4 + 4 * L * d + 4 * v
+    return weights + lm_head + m * per_seq
+
+
 def bench_batched(args):
-    """the body GEMMs of one decode step for M = 8, 16 and 32
-    concurrent sequences (fused per-sequence quant + int4 x int8 GEMM on MFMA,
-    hq_quant_int4_gemm), 36 layers x (qkv, o, gate_up, down) with distinct
-    weights, against the same work as M batch-1 fused GEMVs (hq_quant_int4_gemv)
-    per sequence.  Each GEMM reads a layer's weights once for all M
-    sequences; value = sequences x steps per second of the body GEMMs at
-    M = 32 (the GEMM's roofline is HBM: weights once per step)."""
+    """batched greedy decode of M = 8, 16 and 32 independent
+    sequences at context 256 (each prefilled with its own random 256-token
+    prompt), one hq_decode_batch step per token of every sequence, replayed
+    from a HIP graph.  value = sequence-tokens/s at M = 32; per M the step
+    time, tok/s, the step's HBM bytes over its time (weights once per step +
+    M K/V caches), and the speedup over M batch-1 decode steps of the same
+    model at the same context."""
+    import numpy as np
     import torch
-    from harsh4b_amd.config import QWEN3_4B, body_bytes, shapes
-    from harsh4b_amd.lightspark import quant_int4_gemm, quant_int4_gemv
+    from harsh4b_amd.config import QWEN3_4B
     from harsh4b_amd.synthetic import random_model
     cfg = QWEN3_4B
-    dev = torch.device("cuda", 0)
+    ctx = args.ctx if args.ctx is not None else 256
+    steps, warmup = max(1, min(args.steps, 64)), max(1, min(args.warmup, 8))
     print(f"# building random Qwen3-4B int4 model (seed {args.seed})", file=sys.stderr, flush=True)
     model = random_model(cfg, seed=args.seed)
-    sh = shapes(cfg)
-    L = int(cfg["num_hidden_layers"])
-    wbytes = body_bytes(cfg) + 4 * L * sum(r for r, _ in sh.values())
-    macs = L * sum(r * w for r, w in sh.values())
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(4)
-    s = torch.cuda.Stream(dev)
-    s.wait_stream(torch.cuda.current_stream(dev))
-    reps = max(2, min(args.gemv_reps, 20))
+    vocab = int(cfg["vocab_size"])
+    cap = ctx + warmup + steps + 4
+
+    def prompt(i):
+        return [int(t) for t in np.random.default_rng(4 + i).integers(0, vocab, ctx)]
 
     def timed(fn):
-        with torch.cuda.stream(s):
-            fn()
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            fn()
-        with torch.cuda.stream(s):
-            g.replay()
-            torch.cuda.synchronize()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            for _ in range(reps):
-                g.replay()
-            e1.record(s)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(model.stream)
+        fn()
+        e1.record(model.stream)
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
+        return e0.elapsed_time(e1) / 1e3
 
+    # batch 1 at the same context: the rate M independent steps would have
+    one = model.new_state(cap)
+    model.prefill(prompt(0), one)
+    model.decode_greedy(one, warmup)
+    t1 = timed(lambda: model.decode_greedy(one, steps, check_status=False))
+    one.check_status()
+    del one
+    tok1 = steps / t1
+    print(f"# batch 1 at context {ctx}: {tok1:.1f} tok/s", file=sys.stderr, flush=True)
     per_m = {}
     for m in (8, 16, 32):
-        xs = {name: torch.randn((m, w), generator=gen, device=dev, dtype=torch.float32)
-              for name, (r, w) in sh.items()}
-        outs = {name: torch.empty((m, r), device=dev, dtype=torch.float32) for name, (r, w) in sh.items()}
-
-        def gemm_body():
-            for layer in model.layers:
-                for name in sh:
-                    quant_int4_gemm(xs[name], getattr(layer, name), out=outs[name], stream=s)
-
-        ms = timed(gemm_body)
-        gbs = wbytes / (ms * 1e-3) / 1e9
-        tops = 2 * m * macs / (ms * 1e-3) / 1e12
-        per_m[m] = {"us_per_step": round(ms * 1e3, 1), "seq_steps_per_s": round(m / (ms * 1e-3), 1),
-                    "weight_GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                    "int8_TOP/s": round(tops, 2), "mfma_frac": round(tops / 5000.0, 5)}
-        print(f"# M={m}: body GEMMs {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s of weights, {tops:.1f} TOP/s",
-              file=sys.stderr, flush=True)
-    # the GEMV alternative: one sequence's body GEMVs (M sequences cost M times this)
-    xv = {name: torch.randn(w, generator=gen, device=dev, dtype=torch.float32) for name, (r, w) in sh.items()}
-    ov = {name: torch.empty(r, device=dev, dtype=torch.float32) for name, (r, w) in sh.items()}
-
-    def gemv_body():
-        for layer in model.layers:
-            for name in sh:
-                quant_int4_gemv(xv[name], getattr(layer, name), out=ov[name], stream=s)
-
-    gemv_ms = timed(gemv_body)
-    print(f"# M=1 GEMVs: {gemv_ms * 1e3:.1f} us/step", file=sys.stderr, flush=True)
-    for m in per_m:
-        per_m[m]["gemv_us_per_step_for_M"] = round(m * gemv_ms * 1e3, 1)
-        per_m[m]["speedup_vs_M_gemvs"] = round(m * gemv_ms * 1e3 / per_m[m]["us_per_step"], 2)
+        states = []
+        for i in range(m):
+            st = model.new_state(cap)
+            model.prefill(prompt(i), st)
+            states.append(st)
+        model.decode_greedy_batch(states, warmup)          # captures the batched step
+        t = timed(lambda: model.decode_greedy_batch(states, steps, check_status=False))
+        for st in states:
+            st.check_status()
+        ms = t * 1e3 / steps
+        nbytes = batched_step_bytes(cfg, m, ctx + warmup + steps // 2)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        per_m[m] = {"ms_per_step": round(ms, 3), "tok_s": round(m * steps / t, 1),
+                    "speedup_vs_batch1": round(m * steps / t / tok1, 2),
+                    "step_vs_batch1_step": round(ms / (1e3 / tok1), 2),
+                    "achieved_GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "bytes_per_step": nbytes}
+        print(f"# M={m}: {ms:.3f} ms/step, {m * steps / t:.1f} tok/s, {gbs:.0f} GB/s "
+              f"({ms / (1e3 / tok1):.2f}x the batch-1 step)", file=sys.stderr, flush=True)
+        model._batch_graph = None
+        del states
     top = per_m[32]
-    result = {"metric": "batched body GEMM sequence-steps/s (configs[3], M=32)", "value": top["seq_steps_per_s"],
-              "unit": "sequence-steps/s", "n_gpus": 1, "steps": reps, "warmup": 1,
-              "ms_per_step": round(top["us_per_step"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
-              "vs_baseline": None, "dtype": "int8", "data": "synthetic: random-init int4 weights, N(0,1) inputs",
-              "config": {"workload": "configs[3]: body GEMMs (36 layers x qkv, o, gate_up, down) of one decode "
-                                     "step for M = 8/16/32 sequences, int8 MFMA vs M batch-1 GEMVs"},
-              "roofline": {"kernel": "gemm_mfma_kernel (M=32)", "bound": "hbm", "achieved": top["weight_GB/s"],
-                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": top["hbm_frac"], "traffic": None,
-                           "algorithmic_bytes": wbytes},
-              "per_m": per_m, "gemv_m1_us_per_step": round(gemv_ms * 1e3, 1)}
+    result = {"metric": "batched greedy decode sequence-tokens/s (configs[3], M=32, context 256)",
+              "value": top["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+              "ms_per_step": top["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+              "vs_baseline": None, "dtype": "int8",
+              "data": "synthetic: random-init int4 weights, random 256-token prompts (seeds 4+i)",
+              "config": {"workload": f"configs[3]: batched decode of M = 8/16/32 sequences at context {ctx}, "
+                                     "each with its own fp16 KV cache, greedy",
+                         "global_batch": 32, "seq_len": ctx, "parallelism": "none (1 GPU)"},
+              "roofline": {"kernel": "whole batched step (hq_decode_batch), M=32", "bound": "hbm",
+                           "achieved": top["achieved_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": top["hbm_frac"], "traffic": None, "algorithmic_bytes": top["bytes_per_step"]},
+              "batch1_tok_s": round(tok1, 1), "per_m": per_m}
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_batched(model, ctx, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_batched(model, ctx, seconds):
+    """The oracle decoding sequences one step at a time (the reference has no
+    batching: M sequences cost M steps), from a cache of `ctx` positions."""
+    import numpy as np
+    import oracle
+    from harsh4b_amd.synthetic import host_arrays
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    ref = oracle.OracleModel(model.config, host_arrays(model))
+    rs = ref.new_state(ctx + 64)
+    rng = np.random.default_rng(4)
+    for name in ("keys", "values"):
+        getattr(rs, name)[:, :ctx] = rng.standard_normal(getattr(rs, name)[:, :ctx].shape).astype(
+            np.float16).view(np.uint16)
+    rs.position = ctx
+    token = ref.forward_token(1000, rs)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        token = ref.forward_token(token, rs)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 2) or rs.position >= rs.struct.capacity:
+            break
+    return {"value": round(n / el, 2), "unit": "sequence-tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps of one sequence at context {ctx}+ ({el:.1f} s; M sequences take M "
+                      f"times as long), OpenMP over GEMV rows (oracle/hq_oracle.c)"}
 
 
 def bench_sample(args):

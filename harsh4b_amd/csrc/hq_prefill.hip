@@ -76,63 +76,77 @@ struct RowParams {
     float* act;             // [batch]
 };
 
-template <int MODE>
-__device__ __forceinline__ float row_value(const RowParams& p, int m, int i, float r)
-{
-    if constexpr (MODE == ROW_SWIGLU) {
-        const float g = p.gate_up[size_t(m) * 2 * p.k + i];
-        const float u = p.gate_up[size_t(m) * 2 * p.k + p.k + i];
-        const float t = 1.0f + spec_expf(-g);
-        return (g / t) * u;
-    } else if constexpr (MODE == ROW_PLAIN) {
-        return p.x[size_t(m) * p.k + i];
-    } else {
-        return (p.x[size_t(m) * p.k + i] / r) * p.gamma[i];
-    }
-}
-
-// One token (block) per row: the prologue of the step's GEMVs.
-template <int MODE>
+// One token (block) per row: the prologue of the step's GEMVs.  Thread t
+// holds elements t, t+256, ... of the row in registers (NPT of them, all
+// loaded at once), so the row is read from memory once: RMSNorm's partial t
+// is the fmaf chain over them in ascending order and the partials meet in
+// the spec's halving tree, then the row is normalized, its absolute maximum
+// taken and every element quantized from the registers.
+template <int MODE, int NPT>
 __global__ __launch_bounds__(kBlock) void prefill_rows_kernel(RowParams p)
 {
     __shared__ float red[kBlock];
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
-    float r = 1.0f;
-    if constexpr (MODE == ROW_NORM || MODE == ROW_RESID_NORM) {
-        float* xr = p.x + size_t(m) * p.k;
-        float ss = 0.0f;
-        for (int i = tid; i < p.k; i += kBlock) {
-            float v = xr[i];
-            if constexpr (MODE == ROW_RESID_NORM) {
-                v = v + p.add[size_t(m) * p.k + i];
-                xr[i] = v;
-            }
-            ss = __builtin_fmaf(v, v, ss);
-        }
-        const float total = block_tree_sum256(ss, red);
-        r = __builtin_sqrtf(total / float(p.k) + p.eps);
-    }
-    int8_t* qr = p.q + size_t(m) * p.kp;
-    float amax = 0.0f;
+    const int k = p.k;
+    float v[NPT];
     if constexpr (MODE == ROW_SWIGLU) {
-        // the SwiGLU values (one exp each) are kept in LDS for the quant pass
-        __shared__ float vals[kPrefillMaxWidth];
-        for (int i = tid; i < p.k; i += kBlock) {
-            const float v = row_value<MODE>(p, m, i, r);
-            vals[i] = v;
-            amax = fmaxf(amax, fabsf(v));
+        const float* g = p.gate_up + size_t(m) * 2 * k;
+        float gv[NPT], uv[NPT];
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const int i = tid + kBlock * j;
+            gv[j] = i < k ? g[i] : 0.0f;
+            uv[j] = i < k ? g[k + i] : 0.0f;
         }
-        amax = block_max_nonneg(amax, red);
-        amax = fmaxf(amax, 1e-5f);
-        const float inv = 127.0f / amax;
-        for (int i = tid; i < p.k; i += kBlock) qr[deint_offset(i)] = quant_i8(vals[i], inv);
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const float t = 1.0f + spec_expf(-gv[j]);
+            v[j] = (gv[j] / t) * uv[j];
+        }
     } else {
-        for (int i = tid; i < p.k; i += kBlock) amax = fmaxf(amax, fabsf(row_value<MODE>(p, m, i, r)));
-        amax = block_max_nonneg(amax, red);
-        amax = fmaxf(amax, 1e-5f);
-        const float inv = 127.0f / amax;
-        for (int i = tid; i < p.k; i += kBlock) qr[deint_offset(i)] = quant_i8(row_value<MODE>(p, m, i, r), inv);
+        float* xr = p.x + size_t(m) * k;
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const int i = tid + kBlock * j;
+            v[j] = i < k ? xr[i] : 0.0f;
+        }
+        if constexpr (MODE == ROW_RESID_NORM) {
+            const float* ar = p.add + size_t(m) * k;
+#pragma unroll
+            for (int j = 0; j < NPT; ++j) {
+                const int i = tid + kBlock * j;
+                if (i < k) {
+                    v[j] = v[j] + ar[i];
+                    xr[i] = v[j];
+                }
+            }
+        }
+        if constexpr (MODE == ROW_NORM || MODE == ROW_RESID_NORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NPT; ++j)
+                if (tid + kBlock * j < k) ss = __builtin_fmaf(v[j], v[j], ss);
+            const float total = block_tree_sum256(ss, red);
+            const float r = __builtin_sqrtf(total / float(k) + p.eps);
+#pragma unroll
+            for (int j = 0; j < NPT; ++j) {
+                const int i = tid + kBlock * j;
+                v[j] = i < k ? (v[j] / r) * p.gamma[i] : 0.0f;
+            }
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) amax = fmaxf(amax, fabsf(v[j]));   // 0 past k
+    amax = block_max_nonneg(amax, red);
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+    int8_t* qr = p.q + size_t(m) * p.kp;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+        const int i = tid + kBlock * j;
+        if (i < k) qr[deint_offset(i)] = quant_i8(v[j], inv);
     }
     if (tid == 0) p.act[m] = amax / 127.0f;
 }
@@ -247,17 +261,28 @@ static bool prefill_fits(const hq_model* m)
 }
 
 // The GEMM reads row m of its activations at m * gemm_padded_k(width): the
-// row stride follows each projection's own width.
+// row stride follows each projection's own width.  Rows of up to 2560, 4096
+// and 10240 values take 10, 16 and 40 registers per thread.
+template <int MODE>
+static void launch_rows(const RowParams& p, int rows, hipStream_t s)
+{
+    if (p.k <= kBlock * 10)
+        hipLaunchKernelGGL((prefill_rows_kernel<MODE, 10>), dim3(rows), dim3(kBlock), 0, s, p);
+    else if (p.k <= kBlock * 16)
+        hipLaunchKernelGGL((prefill_rows_kernel<MODE, 16>), dim3(rows), dim3(kBlock), 0, s, p);
+    else
+        hipLaunchKernelGGL((prefill_rows_kernel<MODE, 40>), dim3(rows), dim3(kBlock), 0, s, p);
+}
+
 static int run_rows(int mode, RowParams p, int rows, hipStream_t s)
 {
+    if (p.k > kBlock * 40) return HQ_ERR_ARG;
     p.kp = gemm_padded_k(p.k);
     switch (mode) {
-    case ROW_NORM: hipLaunchKernelGGL(prefill_rows_kernel<ROW_NORM>, dim3(rows), dim3(kBlock), 0, s, p); break;
-    case ROW_RESID_NORM:
-        hipLaunchKernelGGL(prefill_rows_kernel<ROW_RESID_NORM>, dim3(rows), dim3(kBlock), 0, s, p);
-        break;
-    case ROW_PLAIN: hipLaunchKernelGGL(prefill_rows_kernel<ROW_PLAIN>, dim3(rows), dim3(kBlock), 0, s, p); break;
-    default: hipLaunchKernelGGL(prefill_rows_kernel<ROW_SWIGLU>, dim3(rows), dim3(kBlock), 0, s, p); break;
+    case ROW_NORM: launch_rows<ROW_NORM>(p, rows, s); break;
+    case ROW_RESID_NORM: launch_rows<ROW_RESID_NORM>(p, rows, s); break;
+    case ROW_PLAIN: launch_rows<ROW_PLAIN>(p, rows, s); break;
+    default: launch_rows<ROW_SWIGLU>(p, rows, s); break;
     }
     return hipGetLastError() == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }
