@@ -80,11 +80,6 @@ constexpr int kTraceWords = 4 * kTracePoints;
 constexpr int kQkvLPR = 32, kQkvC = 3;           // K <= 3072, 2 rows per wave
 constexpr int kOLPR = 64, kOC = 2;               // K <= 4096, 1 row per wave
 constexpr int kGuLPR = 8, kGuC = 10;             // K <= 2560, 4 gate/up pairs per wave
-// gate_up chunks a weight wave loads before its o dot; the rest follow the
-// dot.  Issuing all ten first held the last waves' o dots behind their own
-// load issue (all 36 layers: 854 us per launch with 10 early, 847 with 3,
-// 856 with 2, 881 with none early).
-constexpr int kGuEarly = 3;
 constexpr int kDownLPR = 64, kDownC = 5;         // K <= 10240, 1 row per wave
 // Phase inputs held in registers by the input threads.
 constexpr int kHidNPT = kMaxHidden / kIThreads;  // 10
@@ -189,6 +184,21 @@ __device__ __forceinline__ int lds_load(const int* p)
 // written after this is seen after the data written before it).
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+__device__ __forceinline__ float lane_f(float v, int lane)
+{
+    return bits_f32(__builtin_amdgcn_readlane(f32_bits(v), lane));
+}
+
+// Block barrier for LDS data: this wave's LDS operations complete, then
+// s_barrier.  Unlike __syncthreads it does not wait for the wave's global
+// memory operations, so weight loads in flight stay in flight.
+__device__ __forceinline__ void block_sync()
+{
+    lds_drain();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+}
 
 // Wait until *p >= target (LDS), bounded.
 __device__ __forceinline__ void wait_lds_geq(const int* p, int target, unsigned& budget, int32_t* status)
@@ -476,21 +486,25 @@ __device__ float act_phase(const EngineParams& p, int l, const uint32_t* act, un
     for (int j = 0; j < kActNPT; ++j) m = fmaxf(m, fabsf(a[j]));   // 0 past I
     m = wave_max64_all(m);
     if (lane_id() == 0) S.amx[w] = m;
-    __syncthreads();
+    block_sync();
     if (w == 0) TRACE(l, 42);
     if (w == kIWaves) TRACE(l, 30);
-    float amax = S.amx[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; ++i) amax = fmaxf(amax, S.amx[i]);
-    amax = fmaxf(amax, 1e-5f);
+    // the sixteen wave maxima in lanes 0-15 of each row, folded by the row's
+    // DPP shifts into its lane 0 (maxima of non-negative values: order-free)
+    static_assert(kWaves == 16, "one wave maximum per row lane");
+    float amax = S.amx[lane_id() & 15];
+    amax = fmaxf(amax, dpp_f<kRowShl8>(amax));
+    amax = fmaxf(amax, dpp_f<kRowShl4>(amax));
+    amax = fmaxf(amax, dpp_f<kRowShl2>(amax));
+    amax = fmaxf(amax, dpp_f<kRowShl1>(amax));
+    amax = fmaxf(lane_f(amax, 0), 1e-5f);
     const float inv = 127.0f / amax;
+    // every element of the down GEMV's span, I included: a[j] is 0 past I,
+    // which quantizes to the zero padding
+    static_assert(kActNPT * kThreads == kDownLPR * kDownC * 32, "quantized span = the down rows' span");
 #pragma unroll
-    for (int j = 0; j < kActNPT; ++j) {
-        const int e = T + kThreads * j;
-        if (e < I) S.xq[xq_offset(e)] = uint8_t(quant_i8(a[j], inv));
-    }
-    for (int i = I + T; i < kDownLPR * kDownC * 32; i += kThreads) S.xq[i] = 0;
-    __syncthreads();
+    for (int j = 0; j < kActNPT; ++j) S.xq[xq_offset(T + kThreads * j)] = uint8_t(quant_i8(a[j], inv));
+    block_sync();
     if (w == 0) TRACE(l, 44);
     if (w == kIWaves) TRACE(l, 31);
     return amax / 127.0f;
@@ -619,10 +633,6 @@ __device__ __forceinline__ int rows_acc(int part)
     return acc;
 }
 
-__device__ __forceinline__ float lane_f(float v, int lane)
-{
-    return bits_f32(__builtin_amdgcn_readlane(f32_bits(v), lane));
-}
 
 // Post this wave's results: its LDS writes complete, then the count.
 __device__ __forceinline__ void post_done()
@@ -650,6 +660,8 @@ __device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l
 __device__ __forceinline__ bool is_copy_wave(int w);
 __device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l, int pos);
 
+__device__ __forceinline__ bool block_has_item(const EngineParams& p, int pos);
+
 __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int pos, uint32_t base, int set,
                             unsigned& budget)
 {
@@ -661,13 +673,22 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
     // its own weight loads on every path
     const bool has_o = R.h0 + ww < R.h1;
     // Loads are issued in the order the phases use them, each after the dot
-    // that frees its registers and once the input waves hold the next
-    // hand-off: gate_up once the attention output is in, down once the
+    // that frees its registers and, mostly, once the input waves hold the
+    // next hand-off: gate_up after the attention phase, down once the
     // attention residual is in, the next layer's qkv once the down input is
     // in and its o once the layer output is in.  Every GEMV's weights so
     // have one to two hand-offs of lead time while a wave holds at most
-    // about two phases of weights.
+    // about two phases of weights.  A block without attention items issues
+    // its gate_up loads as soon as it leaves the attention phase: they land
+    // while the attention runs elsewhere, and none is in flight when the
+    // attention residual's hand-off is read (a wave's memory operations
+    // complete in issue order, so loads issued ahead of a hand-off read
+    // delay it).  Blocks with items wait for the attention output first.
+    // (36 layers at context 64: 835 us per launch against 841 with every
+    // block loading three chunks after the attention output and seven after
+    // its o dot; 987 against 1012 us at context 1024.)
     uint4 wq[kQkvC] = {}, wo[kOC] = {}, wg[kGuC] = {}, wd[kDownC] = {};
+    const bool att_blk = block_has_item(p, pos);
     float sq = 0.0f, so = 0.0f, sg = 0.0f, sd = 0.0f;
     load_rows<kQkvLPR, kQkvC, pace(0, 0)>(wq, sq, S.lay[0].qkv, S.lay[0].qkv_scales, R.q0, R.q1, H, ww);
     load_rows<kOLPR, kOC, pace(0, 0)>(wo, so, S.lay[0].o, S.lay[0].o_scales, R.h0, R.h1, qd, ww);
@@ -694,8 +715,8 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         if (ww == kWWaves - 1) TRACE(l, 47);
         // ---- P2: the block's attention items (all waves)
         attention_phase(p, Ly, l, pos, slot_of(p, set, l), base + 5u * uint32_t(l) + 2u, budget);
-        load_window(4 * l + 1, budget, p.status);
-        load_pairs<0, kGuEarly>(wg, sg, Ly.gate_up, Ly.gate_up_scales, R.g0, R.g1, I, H, ww);
+        if (att_blk) load_window(4 * l + 1, budget, p.status);
+        load_pairs<0, kGuC>(wg, sg, Ly.gate_up, Ly.gate_up_scales, R.g0, R.g1, I, H, ww);
         // ---- P3: o (the residual add is the input waves')
         wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 2), budget, p.status);
         if (ww == 0) TRACE(l, 18);
@@ -708,7 +729,6 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         post_done();
         if (ww == 0) TRACE(l, 19);
         if (ww == kWWaves - 1) TRACE(l, 46);
-        load_pairs<kGuEarly, kGuC>(wg, sg, Ly.gate_up, Ly.gate_up_scales, R.g0, R.g1, I, H, ww);
         load_window(4 * l + 2, budget, p.status);
         load_rows<kDownLPR, kDownC, kPaceDown>(wd, sd, Ly.down, Ly.down_scales, R.h0, R.h1, I, ww);
         // ---- P4: gate_up + SwiGLU
@@ -826,6 +846,19 @@ __device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l
         const int k = item_slot(b, gridDim.x, p.G);   // per-head item: query head k
         if (k < p.heads) prefetch_group(p, l, k / p.G, 0, nc, n, pos);
     }
+}
+
+// Whether this block runs an attention item of every layer at position pos
+// (the item assignment of attention_phase).
+__device__ __forceinline__ bool block_has_item(const EngineParams& p, int pos)
+{
+    const int n = pos + 1;
+    const int nc = (n + kAttnChunk - 1) / kAttnChunk;
+    if ((nc + kGroup - 1) / kGroup > 1) {
+        const int cg = gqa_group(nc, p.kv_heads, gridDim.x);
+        return int(blockIdx.x) < p.kv_heads * ((nc + cg - 1) / cg);
+    }
+    return item_slot(blockIdx.x, gridDim.x, p.G) < p.heads;
 }
 
 // V accumulation of one or two chains per lane: o[d] = fmaf chain of
