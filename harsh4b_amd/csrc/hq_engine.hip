@@ -143,7 +143,6 @@ struct Shared {
     float wmax[kIWaves];
     float act;                          // dequant multiplier of xq
     int xq_seq;                         // input-wave xq posts, 4 per GEMV input of P1/P3/P4 (input -> weight)
-    int done;                           // weight-wave completions (weight -> input)
     int ibar;                           // input-wave barrier arrivals
     int hs;                             // hand-offs received by the input waves, 4 per phase
     float amx[kWaves];                  // P5: each wave's max |SwiGLU output| of its entries
@@ -192,7 +191,13 @@ __device__ __forceinline__ float lane_f(float v, int lane)
 
 // Block barrier for LDS data: this wave's LDS operations complete, then
 // s_barrier.  Unlike __syncthreads it does not wait for the wave's global
-// memory operations, so weight loads in flight stay in flight.
+// memory operations, so weight loads in flight stay in flight.  The weight
+// waves hand each GEMV's results to the input waves through it (the input
+// waves are idle then, and the barrier releases them sooner than a polled
+// LDS count: 36 layers at context 64 went from 810 to 750 us per launch).
+// The input waves hand the quantized phase input on through the xq_seq count
+// instead: as a barrier it would hold their prologue until the weight waves
+// had issued their next loads (765 us).
 __device__ __forceinline__ void block_sync()
 {
     lds_drain();
@@ -218,7 +223,11 @@ __device__ __forceinline__ void ibar(int& seq, unsigned& budget, int32_t* status
     seq += kIWaves;
     lds_drain();
     if (lane_id() == 0) __hip_atomic_fetch_add(&S.ibar, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    wait_lds_geq(&S.ibar, seq, budget, status);
+    // (spun without s_sleep: the four input waves arrive within a few
+    // hundred clocks of each other)
+    unsigned spins = 0;
+    while (lds_load(&S.ibar) < seq && budget != 0)
+        if (++spins == kSpinLimit) { budget = 0; atomicOr(status, HQ_STEP_SYNC); }
 }
 
 #ifdef HQ_ENGINE_TRACE
@@ -634,12 +643,6 @@ __device__ __forceinline__ int rows_acc(int part)
 }
 
 
-// Post this wave's results: its LDS writes complete, then the count.
-__device__ __forceinline__ void post_done()
-{
-    lds_drain();
-    if (lane_id() == 0) __hip_atomic_fetch_add(&S.done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
 
 struct Rows {
     int h0, h1, q0, q1, g0, g1;
@@ -710,7 +713,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
             const float sc = lane == 0 ? lane_f(sq, 0) : lane_f(sq, kQkvLPR);
             if (lane < 2 && row < R.q1) S.res[row - R.q0] = (float(acc) * act) * sc;
         }
-        post_done();
+        block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 17);
         if (ww == kWWaves - 1) TRACE(l, 47);
         // ---- P2: the block's attention items (all waves)
@@ -726,7 +729,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
             const int acc = rows_acc<kOLPR, 0, 1>(reg_dot<kOLPR, kOC>(wo, S.xq));
             if (has_o && lane == 0) S.res[ww] = (float(acc) * act) * so;
         }
-        post_done();
+        block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 19);
         if (ww == kWWaves - 1) TRACE(l, 46);
         load_window(4 * l + 2, budget, p.status);
@@ -754,7 +757,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
                 S.res[pair - R.g0] = (g / t) * u;
             }
         }
-        post_done();
+        block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 21);
         // (after the last layer the same loads, all of one 16-byte block:
         // the instruction sequence, and so every dot's wait, is the same on
@@ -769,7 +772,7 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
             const int acc = rows_acc<kDownLPR, 0, 1>(reg_dot<kDownLPR, kDownC>(wd, S.xq));
             if (has_o && lane == 0) S.res[ww] = (float(acc) * act) * sd;
         }
-        post_done();
+        block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 23);
         if (more) load_window(4 * (l + 1), budget, p.status);
         load_rows<kOLPR, kOC, kPaceO>(wo, so, Ln.o, Ln.o_scales, R.h0, more ? R.h1 : R.h0 + 1, more ? qd : 32, ww);
@@ -1468,7 +1471,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         const int t = opaque_tid();   // (addresses from it are not hoisted out of the loop)
         const hq_layer& Ly = S.lay[l];
         const uint32_t E = base + 5u * uint32_t(l);
-        const int g = 4 * l;   // GEMV phases before this layer
         const Slot z = slot_of(p, set, l);
         const uint32_t* x5_prev = slot_of(p, set, l > 0 ? l - 1 : 0).x5();
 
@@ -1493,7 +1495,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             post_xq(act);
             TRACE(l, 3);
         }
-        wait_lds_geq(&S.done, kWWaves * (g + 1), budget, p.status);
+        block_sync();   // the weight waves' results in S.res
         TRACE(l, 4);
         publish_rows(z.qkv() + R.q0, R.q1 - R.q0);
 
@@ -1519,7 +1521,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             post_xq(act);
             TRACE(l, 7);
         }
-        wait_lds_geq(&S.done, kWWaves * (g + 2), budget, p.status);
+        block_sync();   // the weight waves' results in S.res
         TRACE(l, 8);
         if (t < nown) {
             xown = xown + S.res[t];
@@ -1538,7 +1540,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             post_xq(act);
             TRACE(l, 10);
         }
-        wait_lds_geq(&S.done, kWWaves * (g + 3), budget, p.status);
+        block_sync();   // the weight waves' results in S.res
         TRACE(l, 11);
         // The SwiGLU output is handed on as fp32 values: every block reads
         // the whole vector, takes its maximum |value| (order-free) and
@@ -1551,7 +1553,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         act_phase(p, l, z.act(), budget);
         post_hs();
         TRACE(l, 13);
-        wait_lds_geq(&S.done, kWWaves * (g + 4), budget, p.status);
+        block_sync();   // the weight waves' results in S.res
         TRACE(l, 14);
         if (t < nown) {
             xown = xown + S.res[t];
@@ -1604,7 +1606,6 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     }
     if (tid == 0) {
         S.xq_seq = 0;
-        S.done = 0;
         S.ibar = 0;
         S.hs = 0;
     }
