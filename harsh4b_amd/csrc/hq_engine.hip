@@ -311,17 +311,19 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const
     return (const __attribute__((address_space(1))) T*)p;
 }
 
-// One lane of input wave 0 waits until the last entry of src[0, n) is
-// current; the waves then read the whole vector in one burst (poll_into
-// re-reads the few entries that are not current yet).  Every block polls
-// the same entry, so the wait costs one load per block per round: the
-// polls of the 256 blocks share the memory channels with the producers'
-// stores, and fewer watchers measured faster hand-offs (64 watching lanes
-// per block 929 us per launch of all 36 layers, 16 lanes 899 us, 4 lanes
-// 877 us, 1 lane 861 us).
+// Lane 0 of the calling wave waits until the last entry of src[0, n) is
+// current; the wave then reads its part of the vector in one burst
+// (poll_into re-reads the few entries that are not current yet).  Every
+// block polls the same entry, so the wait costs a load per watching wave
+// and round: the polls of the 256 blocks share the memory channels with the
+// producers' stores, and few watchers measured faster hand-offs (64
+// watching lanes per block 929 us per launch of all 36 layers, 16 lanes 899
+// us, 4 lanes 877 us, 1 lane 861 us, in a build where the other input waves
+// then met wave 0 at a barrier).  Each input wave watches for itself: that
+// costs fewer than the barrier after one wave's watch (746 -> 739 us).
 __device__ __forceinline__ void watch_last(const uint32_t* src, int n, unsigned& budget, int32_t* status)
 {
-    if (opaque_tid() == 0 && n > 0) {
+    if (lane_id() == 0 && n > 0) {
         const __amdgpu_buffer_rsrc_t r = buffer_rsrc(src);
         const uint32_t off = uint32_t(n - 1) * 4u;
         uint32_t w = hs_load(r, off, 0);
@@ -1485,7 +1487,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
                 for (int j = 0; j < kHidNPT; ++j) xin[j] = t + kIThreads * j < H ? p.x[t + kIThreads * j] : 0.0f;
             } else {
                 watch_last(x5_prev, H, budget, p.status);
-                ibar(bseq, budget, p.status);
                 TRACE(l, 1);
                 poll_into<kHidNPT>(x5_prev, H, xin, budget, p.status);
             }
@@ -1512,7 +1513,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
             float att[kAttNPT];
             TRACE(l, 5);
             watch_last(z.att(), qd, budget, p.status);
-            ibar(bseq, budget, p.status);
             TRACE(l, 6);
             poll_into<kAttNPT>(z.att(), qd, att, budget, p.status);
             post_hs();
@@ -1532,7 +1532,6 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         {
             float xp[kHidNPT];
             watch_last(z.x3(), H, budget, p.status);
-            ibar(bseq, budget, p.status);
             TRACE(l, 9);
             poll_into<kHidNPT>(z.x3(), H, xp, budget, p.status);
             post_hs();
