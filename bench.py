@@ -10,15 +10,23 @@ greedy token fed back on the device.
 
 Printed as one JSON line: tok/s (value); the HBM roofline of the dominant
 kernel, the persistent layer kernel that runs all 36 decoder layers of a step
-in one launch (about 96 % of the step time), timed live with HIP events on
-its launch stream; the body-weight bandwidth of that launch; the standalone
-GEMV kernels of the five-kernels-per-layer form; and the CPU oracle's tok/s
-on this host's cores for the same model and context (cpu_baseline, a
-bounded sample).  `roofline.traffic` is the HBM bytes per launch of the
-layer kernel from the committed PMC profile
-(profiles/decode_traffic_pmc.json: FETCH_SIZE and WRITE_SIZE scaled by a copy
-kernel's reading), or null when the profile is absent.
+in one launch (about 95 % of the step time), timed live with HIP events on
+its launch stream; the body-weight bandwidth of that launch; and, under
+"configs", the other BASELINE configurations measured in the same run, each
+with its own roofline and CPU baseline: configs[0] (one fused quant + int4
+GEMV 2560 -> 9728 over rotating weight copies), configs[1] (one decoder
+layer's body GEMVs: the standalone GEMV kernels and the layer kernel's
+per-layer share) and configs[4] (the same decode at context 4096, with the
+attention's KV bandwidth).  cpu_baseline is the CPU oracle (this repository's
+C restatement of the reference path; AVX-512 VNNI GEMVs where the host has
+them) decoding the same model on this host, on all available cores and on
+the reference's default 6 threads, with the CPU model and core counts.
+`roofline.traffic` is the layer kernel's HBM bytes per launch at the line's
+own context from the committed PMC profile (profiles/engine_traffic_pmc.json,
+made with --workload layers under rocprofv3 --pmc and --pmc-summary), or null
+when no profile holds that context.
 """
+
 from __future__ import annotations
 
 import argparse
@@ -33,7 +41,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_PROFILE = ROOT / "profiles" / "decode_traffic_pmc.json"
+TRAFFIC_PROFILE = ROOT / "profiles" / "engine_traffic_pmc.json"
+REFERENCE_THREADS = 6          # the reference runner's default (cpu_lightspark.py:34, 38-42)
 METRIC = "decode tok/s @ Qwen3-4B batch 1; body-GEMV HBM GB/s as % of peak"
 # The reference's published decode rates for this model at batch 1, 256
 # tokens (README.md:139-144 of the reference repository, Apple M4 CPU, 6
@@ -52,9 +61,16 @@ def parse():
                     help="context before the timed decode (default 64; 4096 for --workload long)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--gemv-reps", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="CPU time of each decode baseline run (the GEMV runs take a quarter of it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("decode", "sampled", "sample", "long", "batched", "gemv", "copy"),
+    ap.add_argument("--no-configs", action="store_true",
+                    help="decode: skip the configs[0]/[1]/[4] measurements folded into the line")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
+                    help="print the traffic summary of rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE output "
+                         "directories of --workload layers and --workload copy runs")
+    ap.add_argument("--workload", choices=("decode", "sampled", "sample", "long", "batched", "gemv", "copy",
+                                           "layers"),
                     default="decode",
                     help="decode: configs[2] (the reported line); sampled: the same decode with the "
                          "reference runner's default stochastic sampler (temperature 0.7, top-k 40, "
@@ -64,7 +80,9 @@ def parse():
                          "body GEMMs of M = 8/16/32 sequences on int8 MFMA against M GEMVs; gemv: "
                          "configs[0], one fused quant + int4 GEMV 2560 -> 9728 over rotating weight "
                          "copies; copy: a plain 256 MiB device-to-device copy, the calibration kernel "
-                         "of the PMC traffic counters")
+                         "of the PMC traffic counters; layers: the layer kernel alone, launched "
+                         "--steps times at the default line's context (or --ctx with the long workload's "
+                         "N(0,1) cache), for rocprofv3 --pmc")
     return ap.parse_args()
 
 
@@ -107,13 +125,18 @@ def layer_kernel_bytes(config, context):
     return body_bytes(config) + scales + norms + kv + rope + 2 * 4 * h
 
 
-def measured_traffic(kind):
-    """HBM bytes per launch of one kernel kind from the PMC profile."""
+def traffic_at(context):
+    """HBM bytes per launch of the layer kernel at `context` from the PMC
+    profile (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel's reading), or
+    None when the profile holds no run at exactly that context."""
     try:
         prof = json.loads(TRAFFIC_PROFILE.read_text())
-        return int(prof["kernels"][kind]["traffic_bytes"])
-    except (OSError, KeyError, ValueError):
+    except (OSError, ValueError):
         return None
+    for run in prof.get("runs", []):
+        if int(run.get("context", -1)) == int(context):
+            return int(run["traffic_bytes"])
+    return None
 
 
 def time_graph(lib, model, state, launches, reps, torch):
@@ -169,42 +192,99 @@ def time_layers(lib, model, state, launches, reps, torch):
     return e0.elapsed_time(e1) / (reps * launches)
 
 
-def cpu_baseline(model, state, ctx, seconds):
-    """The CPU oracle (C restatement of the reference path, OpenMP) decoding
-    from the same model and KV cache on this host."""
-    import numpy as np
+def cpu_info():
+    """CPU model, logical CPUs this process may run on, and the host's
+    physical cores (distinct physical id / core id pairs)."""
+    model, cores, phys = None, set(), None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and model is None:
+                    model = val
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    cores.add((phys, val))
+    except OSError:
+        pass
+    return {"cpu_model": model, "logical_cpus_available": len(os.sched_getaffinity(0)),
+            "physical_cores_host": len(cores) or None}
+
+
+def all_threads():
+    """The cores this process has: its CPU affinity, capped by OMP_NUM_THREADS
+    where that is set (the GPU box sets it to the job's CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
+
+
+def cpu_runs(run, seconds, unit, sample, kind="port"):
+    """`run(seconds)` -> (value, detail) on all available cores and on the
+    reference's 6 threads; the all-core run is the reported baseline."""
     import oracle
-    from harsh4b_amd.synthetic import host_arrays
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    ref = oracle.OracleModel(model.config, host_arrays(model))
-    rs = ref.new_state(state.capacity)
+    out = {}
+    for name, threads in (("all_cores", all_threads()), ("reference_threads", REFERENCE_THREADS)):
+        oracle.set_threads(threads)
+        value, detail = run(seconds)
+        out[name] = {"threads": threads, "value": round(value, 3), "sample": detail}
+    oracle.set_threads(all_threads())
+    top = out["all_cores"]
+    return {"value": top["value"], "unit": unit, "cores": top["threads"], "kind": kind,
+            "sample": sample + "; " + top["sample"], "runs": out, "simd": "avx512-vnni" if oracle.simd_active()
+            else "scalar", **cpu_info()}
+
+
+def oracle_decode_rate(ref, state, ctx, seconds, token=1000):
+    """tok/s of the oracle decoding from a cache of `ctx` positions (the
+    position is reset before the run, so every run sees the same context)."""
+    state.position = ctx
+    token = ref.forward_token(token, state)      # warm-up step (page-in, thread spin-up)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        token = ref.forward_token(token, state)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 2) or state.position >= state.struct.capacity:
+            break
+    return n / el, f"{n} steps in {el:.1f} s"
+
+
+def cpu_baseline(ref, state, ctx, seconds):
+    """The CPU oracle (C restatement of the reference path) decoding from the
+    same model and KV cache on this host."""
+    def run(sec):
+        return oracle_decode_rate(ref, state, ctx, sec)
+    return cpu_runs(run, seconds, "tok/s", f"decode steps of the same 36-layer model at context {ctx}+, "
+                                          "OpenMP over GEMV rows (oracle/hq_oracle.c)")
+
+
+def oracle_state_from(ref, state, ctx, capacity):
+    """An oracle state holding the first ctx cache positions of a device state."""
+    import numpy as np
+    rs = ref.new_state(capacity)
     rs.keys[:, :ctx] = state.keys[:, :ctx].cpu().numpy().view(np.uint16)
     rs.values[:, :ctx] = state.values[:, :ctx].cpu().numpy().view(np.uint16)
     rs.position = ctx
-    token = 1000
-    token = ref.forward_token(token, rs)      # warm-up step (page-in, thread spin-up)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        token = ref.forward_token(token, rs)
-        n += 1
-        el = time.perf_counter() - t0
-        if (el >= seconds and n >= 2) or rs.position >= rs.struct.capacity:
-            break
-    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps of the same 36-layer model at context {ctx}+, "
-                      f"{el:.1f} s, OpenMP over GEMV rows (oracle/hq_oracle.c)"}
+    return rs
 
 
-def bench_gemv(args):
+GEMV_ROWS, GEMV_WIDTH, GEMV_COPIES = 9728, 2560, 48
+
+
+def gemv_case(args, cpu_seconds):
     """fused per-token quant + int4 GEMV, K=2560 -> N=9728, with
     48 distinct weight copies (598 MB, above the 256 MB Infinity Cache)
-    cycled so every launch streams its weights from HBM."""
+    cycled so every launch streams its weights from HBM; timed from a graph
+    of the 48 launches with HIP events on their stream.  The CPU baseline is
+    the oracle's fused quant + GEMV over the same copies."""
     import numpy as np
     import torch
-    from harsh4b_amd import _native
     from harsh4b_amd.lightspark import LiteSparkProjection, quant_int4_gemv
     from harsh4b_amd.synthetic import random_packed
-    rows, width, copies = 9728, 2560, 48
+    rows, width, copies = GEMV_ROWS, GEMV_WIDTH, GEMV_COPIES
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
@@ -223,7 +303,7 @@ def bench_gemv(args):
     with torch.cuda.graph(g, stream=s):
         for p in projs:
             quant_int4_gemv(x, p, out=out, stream=s)
-    reps = max(1, args.steps // copies)
+    reps = max(2, args.gemv_reps)
     with torch.cuda.stream(s):
         g.replay()
         torch.cuda.synchronize()
@@ -237,27 +317,43 @@ def bench_gemv(args):
     us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
     nbytes = rows * width // 2 + 4 * rows + 4 * width + 4 * rows
     gbs = nbytes / (us * 1e-6) / 1e9
-    result = {"metric": "single fused quant + int4 GEMV (configs[0]) HBM GB/s", "value": round(gbs, 1),
-              "unit": "GB/s", "n_gpus": 1, "steps": reps * copies, "warmup": copies,
-              "us_per_call": round(us, 3), "higher_is_better": True, "dtype": "int8",
-              "data": "synthetic", "config": {"workload": "configs[0]: K=2560 -> N=9728, 48 rotating copies"},
-              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
-    if not args.no_cpu_baseline:
+    result = {"workload": "configs[0]: fused quant + int4 GEMV, K=2560 -> N=9728, 48 rotating weight copies",
+              "us_per_call": round(us, 3), "calls": reps * copies, "algorithmic_bytes": nbytes,
+              "roofline": {"kernel": "gemv_kernel (hq_quant_int4_gemv)", "bound": "hbm", "achieved": round(gbs, 1),
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                           "traffic": None}}
+    del g
+    if cpu_seconds:
         import oracle
         hw = w_all.cpu().numpy()
         hs = s_all.cpu().numpy()
         hx = x.cpu().numpy()
         oracle.quant_int4_gemv(hx, hw[0], hs[0])
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds or n < 10:
-            i = n % copies
-            oracle.quant_int4_gemv(hx, hw[i], hs[i])
-            n += 1
-        el = time.perf_counter() - t0
-        result["cpu_baseline"] = {"value": round(n * nbytes / el / 1e9, 2), "unit": "GB/s",
-                                  "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
-                                  "kind": "port", "sample": f"{n} calls over 48 rotating copies, {el:.1f} s"}
+
+        def run(sec):
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < sec or n < 10:
+                i = n % copies
+                oracle.quant_int4_gemv(hx, hw[i], hs[i])
+                n += 1
+            el = time.perf_counter() - t0
+            return n * nbytes / el / 1e9, f"{n} calls in {el:.1f} s"
+        result["cpu_baseline"] = cpu_runs(run, cpu_seconds, "GB/s", "fused quant + GEMV calls over the 48 copies")
+    del projs, w_all, s_all
+    torch.cuda.empty_cache()
+    return result
+
+
+def bench_gemv(args):
+    """configs[0] alone, as its own JSON line."""
+    res = gemv_case(args, 0 if args.no_cpu_baseline else max(2.0, args.cpu_seconds / 2))
+    gbs = res["roofline"]["achieved"]
+    result = {"metric": "single fused quant + int4 GEMV (configs[0]) HBM GB/s", "value": gbs,
+              "unit": "GB/s", "n_gpus": 1, "steps": res["calls"], "warmup": GEMV_COPIES,
+              "us_per_call": res["us_per_call"], "higher_is_better": True, "dtype": "int8",
+              "data": "synthetic", "config": {"workload": res["workload"]}, "roofline": res["roofline"]}
+    if "cpu_baseline" in res:
+        result["cpu_baseline"] = res["cpu_baseline"]
     print(json.dumps(result), flush=True)
 
 
@@ -464,12 +560,264 @@ def bench_copy(args):
                       "config": {"workload": "copy 256 MiB"}}), flush=True)
 
 
+def fill_long(state, ctx, torch):
+    """the first ctx positions of every layer's cache hold N(0,1)
+    keys and values (fp16); decoding starts at position ctx."""
+    gen = torch.Generator(device=state.keys.device)
+    gen.manual_seed(5)
+    for cache in (state.keys, state.values):
+        cache[:, :ctx].normal_(generator=gen)
+    state.device_position.fill_(ctx)
+    state.position = ctx
+    state.token.fill_(1000)
+    torch.cuda.synchronize()
+
+
+def kv_read_bytes(config, context):
+    """fp16 K/V bytes the attention of one step reads at `context` positions
+    (the context - 1 cached rows of every layer)."""
+    L = int(config["num_hidden_layers"])
+    row = 2 * int(config["num_key_value_heads"]) * int(config["head_dim"]) * 2
+    return L * row * (context - 1)
+
+
+def layer_case(cfg, per_kind_ms, layers_ms, ref_arrays, cpu_seconds):
+    """one decoder layer's body GEMVs at batch 1 with fused
+    activation quant (and the RMSNorms in the qkv and gate_up kernels): the
+    sum of the four standalone GEMV kernels (timed from graphs of each kind's
+    36 launches), and the layer kernel's per-layer share (its attention and
+    hand-offs included).  CPU: the oracle's fused quant + GEMV over layer 0's
+    four matrices."""
+    L = int(cfg["num_hidden_layers"])
+    alg = algorithmic_bytes(cfg)
+    nbytes = sum(alg.values())
+    us = sum(per_kind_ms.values()) * 1e3
+    gbs = nbytes / (us * 1e-6) / 1e9
+    eng_us = layers_ms * 1e3 / L
+    eng_bytes = layer_kernel_bytes(cfg, 1) // L
+    res = {"workload": "configs[1]: one Qwen3-4B decoder layer's body GEMVs at batch 1 with fused quant",
+           "us_per_layer": round(us, 3), "algorithmic_bytes": nbytes,
+           "roofline": {"kernel": "gemv_kernel x4 (qkv, o, gate_up, down; five-kernels-per-layer form)",
+                        "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+           "layer_kernel_share": {"us_per_layer": round(eng_us, 3),
+                                  "GB/s": round(eng_bytes / (eng_us * 1e-6) / 1e9, 1),
+                                  "note": "layer kernel time / 36 (attention, norms and hand-offs included)"}}
+    if cpu_seconds and ref_arrays is not None:
+        import numpy as np
+        import oracle
+        rng = np.random.default_rng(7)
+        mats = []
+        for name in ("qkv", "o", "gate_up", "down"):
+            w, s = ref_arrays[name][0], ref_arrays[name + "_scales"][0]
+            mats.append((rng.standard_normal(2 * w.shape[1]).astype(np.float32), w, s))
+
+        def run(sec):
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < sec or n < 4:
+                for x, w, s in mats:
+                    oracle.quant_int4_gemv(x, w, s)
+                n += 1
+            el = time.perf_counter() - t0
+            return n * nbytes / el / 1e9, f"{n} layers in {el:.1f} s ({el / n * 1e3:.2f} ms per layer)"
+        res["cpu_baseline"] = cpu_runs(run, cpu_seconds, "GB/s", "fused quant + GEMV of the four body matrices "
+                                                                   "of layer 0")
+    return res
+
+
+def attention_case(args, torch, context=4096):
+    """The standalone fused GQA decode kernel (hq_gqa_decode) at one layer's
+    shape: 32 query / 8 kv heads x 128, fp16 N(0,1) K/V of `context`
+    positions; timed from a graph of 36 calls (one per layer, each on its own
+    cache slab, so the K/V stream from HBM and not from the last call's
+    cache)."""
+    from harsh4b_amd.lightspark import gqa_decode
+    dev = torch.device("cuda", 0)
+    L, kv, g, d = 36, 8, 4, 128
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    keys = torch.randn((L, context, kv, d), generator=gen, device=dev).half()
+    values = torch.randn((L, context, kv, d), generator=gen, device=dev).half()
+    q = torch.randn((kv * g * d,), generator=gen, device=dev)
+    out = torch.empty_like(q)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for layer in range(L):
+            gqa_decode(q, keys[layer], values[layer], out, context, kv, g, d, stream=s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for layer in range(L):
+            gqa_decode(q, keys[layer], values[layer], out, context, kv, g, d, stream=s)
+    reps = max(2, args.gemv_reps)
+    with torch.cuda.stream(s):
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * L)
+    nbytes = 2 * context * kv * d * 2 + 2 * 4 * kv * g * d
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del graph, keys, values
+    torch.cuda.empty_cache()
+    return {"kernel": "attention_kernel (hq_gqa_decode)", "context": context, "us_per_call": round(us, 3),
+            "algorithmic_bytes": nbytes, "achieved": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def long_case(args, model, lib, cfg, ref, cpu_seconds, short):
+    """the batch-1 decode at context 4096 over an N(0,1) fp16 KV
+    cache: the layer kernel at the line's context (roofline with the K/V
+    bytes), the decode rate, and the attention's marginal KV bandwidth
+    against the short-context launch `short` = (context, ms)."""
+    import torch
+    ctx, warm, steps = 4096, 16, 64
+    state = model.new_state(ctx + warm + steps + 4)
+    fill_long(state, ctx, torch)
+    model.decode_greedy(state, warm)
+    state.synchronize()
+    context = int(state.device_position.item()) + 1
+    layers_ms = time_layers(lib, model, state, 4, args.gemv_reps, torch)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(state.stream)
+    model.decode_greedy(state, steps, check_status=False)
+    e1.record(state.stream)
+    torch.cuda.synchronize()
+    state.check_status()
+    tok_s = steps / (e0.elapsed_time(e1) / 1e3)
+    eng_bytes = layer_kernel_bytes(cfg, context)
+    gbs = eng_bytes / (layers_ms * 1e-3) / 1e9
+    kv_extra = kv_read_bytes(cfg, context) - kv_read_bytes(cfg, short[0])
+    marginal = kv_extra / ((layers_ms - short[1]) * 1e-3) / 1e9
+    print(f"# configs[4]: layer kernel {layers_ms * 1e3:.1f} us at context {context}, decode {tok_s:.1f} tok/s, "
+          f"attention marginal {marginal:.0f} GB/s", file=sys.stderr, flush=True)
+    res = {"workload": f"configs[4]: the same decode at context {ctx} (N(0,1) fp16 KV cache), greedy",
+           "tok_s": round(tok_s, 2), "steps": steps, "warmup": warm,
+           "roofline": {"kernel": "engine_kernel (persistent layer kernel: 36 decoder layers)", "bound": "hbm",
+                        "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_at(context),
+                        "algorithmic_bytes": eng_bytes, "context": context,
+                        "us_per_launch": round(layers_ms * 1e3, 2)},
+           "attention_marginal": {"kv_bytes": kv_extra, "us": round((layers_ms - short[1]) * 1e3, 2),
+                                  "GB/s": round(marginal, 1), "frac": round(marginal / HBM_PEAK_GBS, 4),
+                                  "note": f"extra K/V bytes read at context {context} over context {short[0]} "
+                                          "/ the extra layer-kernel time"}}
+    if cpu_seconds and ref is not None:
+        rs = oracle_state_from(ref, state, context - 1, context + 64)
+        res["cpu_baseline"] = cpu_runs(lambda sec: oracle_decode_rate(ref, rs, context - 1, sec), cpu_seconds,
+                                       "tok/s", f"decode steps of the same model at context {context}, "
+                                                "OpenMP over GEMV rows (oracle/hq_oracle.c)")
+        del rs
+    del state
+    torch.cuda.empty_cache()
+    return res
+
+
+def layers_context(args):
+    """Context of the layer-kernel launches of --workload layers: the default
+    line's (a 64-token prompt and --warmup decode steps) or, for --ctx of
+    1024 and more, the long workload's (an N(0,1) cache of ctx positions and
+    --warmup decode steps)."""
+    ctx = args.ctx if args.ctx is not None else 64
+    return ctx + args.warmup + 1
+
+
+def bench_layers(args):
+    """The layer kernel alone, launched --steps times at the context of
+    layers_context(args), for rocprofv3 --pmc (one launch = one step's 36
+    decoder layers; the position does not advance between launches)."""
+    import numpy as np
+    import torch
+    from harsh4b_amd import _native
+    from harsh4b_amd.config import QWEN3_4B
+    from harsh4b_amd.synthetic import random_model
+    cfg = QWEN3_4B
+    lib = _native.lib()
+    ctx = args.ctx if args.ctx is not None else 64
+    model = random_model(cfg, seed=args.seed)
+    state = model.new_state(ctx + args.warmup + 8)
+    if ctx >= 1024:
+        fill_long(state, ctx, torch)
+    else:
+        model.prefill([int(t) for t in np.random.default_rng(3).integers(0, int(cfg["vocab_size"]), ctx)], state)
+    model.decode_greedy(state, args.warmup)
+    state.synchronize()
+    context = int(state.device_position.item()) + 1
+    assert context == layers_context(args), (context, layers_context(args))
+    s = state.stream
+    for _ in range(args.steps):
+        _native.check(lib.hq_step_layers(ctypes.byref(model.struct), ctypes.byref(state.struct), s.cuda_stream),
+                      "hq_step_layers")
+    torch.cuda.synchronize()
+    state.check_status()
+    print(json.dumps({"workload": "layers", "context": context, "launches": args.steps}), flush=True)
+
+
+def pmc_counter(directory, counter):
+    """Mean Counter_Value per dispatch of each kernel in a rocprofv3 CSV
+    output directory -> {kernel: (dispatches, mean)}."""
+    import csv
+    rows = {}
+    for f in Path(directory).rglob("*counter_collection.csv"):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Counter_Name") != counter:
+                    continue
+                rows.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return {k: (len(v), sum(v) / len(v)) for k, v in rows.items()}
+
+
+def pmc_summary(args):
+    """HBM traffic per launch of the layer kernel from two rocprofv3 --pmc
+    runs of --workload layers (FETCH_SIZE, then WRITE_SIZE; KiB per
+    dispatch) scaled by what the same counters read for the 256 MiB copy of
+    --workload copy."""
+    from harsh4b_amd.config import QWEN3_4B
+    fetch_dir, write_dir, cfetch_dir, cwrite_dir = args.pmc_summary
+    copy_bytes = 256 << 20
+
+    def copy_kib(d, counter):
+        for k, (_, v) in pmc_counter(d, counter).items():
+            if "copyBuffer" in k or "copy" in k.lower():
+                return v
+        raise SystemExit(f"no copy kernel in {d}")
+    cf, cw = copy_kib(cfetch_dir, "FETCH_SIZE"), copy_kib(cwrite_dir, "WRITE_SIZE")
+    ff, wf = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+    fetch, write = pmc_counter(fetch_dir, "FETCH_SIZE"), pmc_counter(write_dir, "WRITE_SIZE")
+    name = next(k for k in fetch if "engine_kernel" in k)
+    n, fk = fetch[name]
+    wk = write[name][1]
+    context = layers_context(args)
+    traffic = int(fk * 1024 * ff + wk * 1024 * wf)
+    alg = layer_kernel_bytes(QWEN3_4B, context)
+    print(json.dumps({"calibration": {"copy_kernel_bytes_read": copy_bytes, "copy_kernel_bytes_written": copy_bytes,
+                                      "copy_fetch_kib": round(cf, 1), "copy_write_kib": round(cw, 1),
+                                      "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+                      "runs": [{"kernel": name, "context": context, "dispatches": n, "fetch_kib": round(fk, 1),
+                                "write_kib": round(wk, 1), "traffic_bytes": traffic, "algorithmic_bytes": alg,
+                                "ratio": round(traffic / alg, 4)}]}, indent=1), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the path runs on one GPU's share; sharding across GPUs is not built)", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_summary:
+        pmc_summary(args)
+        return
+    if args.workload == "layers":
+        bench_layers(args)
+        return
     if args.workload == "gemv":
         bench_gemv(args)
         return
@@ -498,16 +846,7 @@ def main():
     cap = args.ctx + args.warmup + args.steps + 4
     state = model.new_state(cap)
     if long_ctx:
-        # the first ctx positions of every layer's cache hold
-        # N(0,1) keys and values (fp16); decoding starts at position ctx
-        gen = torch.Generator(device=state.keys.device)
-        gen.manual_seed(5)
-        for cache in (state.keys, state.values):
-            cache[:, :args.ctx].normal_(generator=gen)
-        state.device_position.fill_(args.ctx)
-        state.position = args.ctx
-        state.token.fill_(1000)
-        torch.cuda.synchronize()
+        fill_long(state, args.ctx, torch)
         print(f"# filled {args.ctx} cache positions with N(0,1)", file=sys.stderr, flush=True)
     else:
         prompt = [int(t) for t in np.random.default_rng(3).integers(0, int(cfg["vocab_size"]), args.ctx)]
@@ -611,7 +950,7 @@ def main():
                    "global_batch": 1, "seq_len": args.ctx, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "engine_kernel (persistent layer kernel: 36 decoder layers)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("engine"),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_at(context),
                      "algorithmic_bytes": eng_bytes, "context": context,
                      "us_per_launch": round(layers_ms * 1e3, 2)},
         "body_gemv": {"bytes_per_token": body_bytes(cfg), "us_per_token": round(layers_ms * 1e3, 2),
@@ -625,9 +964,28 @@ def main():
     }
     if prefill_info:
         result["prefill"] = prefill_info
+    ref = arrays = None
     if not args.no_cpu_baseline:
+        import oracle
+        from harsh4b_amd.synthetic import host_arrays
+        arrays = host_arrays(model)
+        ref = oracle.OracleModel(model.config, arrays)
+    cpu_s = 0 if args.no_cpu_baseline else args.cpu_seconds
+    if args.workload == "decode" and not args.no_configs:
+        print("# configs[0], [1] and [4]", file=sys.stderr, flush=True)
+        configs = {"configs[0]": gemv_case(args, cpu_s / 4),
+                   "configs[1]": layer_case(cfg, per_kind_ms, layers_ms, arrays, cpu_s / 4),
+                   "configs[4]": long_case(args, model, lib, cfg, ref, cpu_s, (context, layers_ms))}
+        result["configs"] = configs
+        att = attention_case(args, torch)
+        print(f"# hq_gqa_decode at context 4096: {att['us_per_call']:.2f} us, {att['achieved']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+        result["attention"] = {"standalone_ctx4096": att,
+                               "layer_kernel_marginal_ctx4096": configs["configs[4]"]["attention_marginal"]}
+    if ref is not None:
         print("# timing the CPU oracle baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(model, state, args.ctx, args.cpu_seconds)
+        rs = oracle_state_from(ref, state, args.ctx, state.capacity)
+        result["cpu_baseline"] = cpu_baseline(ref, rs, args.ctx, cpu_s)
     print(json.dumps(result), flush=True)
 
 

@@ -96,6 +96,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.or_rope.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
     L.or_int4_i8_gemv.argtypes = [vp, vp, vp, ctypes.c_float, vp, ctypes.c_int, ctypes.c_int]
     L.or_int4_i8_gemv_acc.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp]
+    L.or_set_simd.argtypes = [ctypes.c_int]
+    L.or_set_simd.restype = None
+    L.or_simd_active.argtypes = []
+    L.or_set_threads.argtypes = [ctypes.c_int]
+    L.or_set_threads.restype = None
+    L.or_max_threads.argtypes = []
     L.or_int4_i8_gemm_acc.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
     L.or_quant_int4_gemv.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, vp]
     L.or_quant_int4_gemv.restype = ctypes.c_float
@@ -404,4 +410,19 @@ def _ptr(a: np.ndarray, ctype):
 
 
 def threads() -> int:
-    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    """OpenMP threads the oracle's GEMVs run on."""
+    return int(lib().or_max_threads())
+
+
+def set_threads(n: int) -> None:
+    lib().or_set_threads(int(n))
+
+
+def set_simd(on: bool) -> None:
+    """Use the AVX-512 VNNI GEMV path where the CPU has it (default), or
+    force the scalar loop (the same integers)."""
+    lib().or_set_simd(int(bool(on)))
+
+
+def simd_active() -> bool:
+    return bool(lib().or_simd_active())

@@ -17,6 +17,10 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <omp.h>
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
 
 /* ------------------------------------------------------------------------ */
 /* bit helpers                                                               */
@@ -255,9 +259,39 @@ void or_rope(float* x, int heads, int head_dim, const float* cos_row, const floa
  * litespark_int4.cpp:22-76.  acc = sum_k W[n,k] * x[k] in int32 (the NEON
  * body and the scalar tail compute the same integer), then
  * out = ((float)acc * activation_scale) * scale[n] (:73-74).
+ *
+ * Two implementations of the same integer: the scalar loop, and on x86 CPUs
+ * with AVX-512 VNNI an SDOT-like path (the reference's NEON SDOT role, done
+ * with vpdpbusd): the activations are split once per call into even and
+ * odd elements (the low and high nibbles' partners); each 64-byte block of
+ * a row gives its 64 low and 64 high nibbles as unsigned u = w + 8 in
+ * [0, 15], vpdpbusd accumulates u * x in int32, and
+ * sum(w * x) = sum(u * x) - 8 * sum(x) exactly (no term can overflow:
+ * |u * x| <= 15 * 128).  or_set_simd(0) forces the scalar loop, which
+ * tests compare with the vector path.
  */
-void or_int4_i8_gemv_acc(const int8_t* x, const uint8_t* weights, int rows, int width,
-                         int32_t* acc)
+static int g_simd = 1;
+
+void or_set_simd(int on) { g_simd = on != 0; }
+
+int or_simd_active(void)
+{
+#if defined(__x86_64__)
+    return g_simd && __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+           __builtin_cpu_supports("avx512vnni");
+#else
+    return 0;
+#endif
+}
+
+void or_set_threads(int n)
+{
+    if (n > 0) omp_set_num_threads(n);
+}
+
+int or_max_threads(void) { return omp_get_max_threads(); }
+
+static void gemv_acc_scalar(const int8_t* x, const uint8_t* weights, int rows, int width, int32_t* acc)
 {
     const int half = width >> 1;
 #pragma omp parallel for schedule(static) if (rows >= 64)
@@ -270,6 +304,57 @@ void or_int4_i8_gemv_acc(const int8_t* x, const uint8_t* weights, int rows, int 
         }
         acc[r] = s;
     }
+}
+
+#if defined(__x86_64__)
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+static void gemv_acc_vnni(const int8_t* x, const uint8_t* weights, int rows, int width, int32_t* acc)
+{
+    const int half = width >> 1;
+    const int body = half & ~63;          /* packed bytes in whole 64-byte blocks */
+    int8_t* xe = (int8_t*)malloc((size_t)(half > 0 ? half : 1));
+    int8_t* xo = (int8_t*)malloc((size_t)(half > 0 ? half : 1));
+    int32_t xsum = 0;                      /* sum of the activations the blocks cover */
+    for (int j = 0; j < half; ++j) {
+        xe[j] = x[2 * j];
+        xo[j] = x[2 * j + 1];
+        if (j < body) xsum += (int32_t)x[2 * j] + (int32_t)x[2 * j + 1];
+    }
+    const __m512i lo_mask = _mm512_set1_epi8(0x0F);
+    const __m512i bias = _mm512_set1_epi8(0x08);
+#pragma omp parallel for schedule(static) if (rows >= 64)
+    for (int r = 0; r < rows; ++r) {
+        const uint8_t* row = weights + (int64_t)r * half;
+        __m512i a0 = _mm512_setzero_si512(), a1 = _mm512_setzero_si512();
+        for (int j = 0; j < body; j += 64) {
+            const __m512i w = _mm512_loadu_si512((const void*)(row + j));
+            const __m512i lo = _mm512_xor_si512(_mm512_and_si512(w, lo_mask), bias);
+            const __m512i hi = _mm512_xor_si512(_mm512_and_si512(_mm512_srli_epi16(w, 4), lo_mask), bias);
+            a0 = _mm512_dpbusd_epi32(a0, lo, _mm512_loadu_si512((const void*)(xe + j)));
+            a1 = _mm512_dpbusd_epi32(a1, hi, _mm512_loadu_si512((const void*)(xo + j)));
+        }
+        int32_t s = _mm512_reduce_add_epi32(_mm512_add_epi32(a0, a1)) - 8 * xsum;
+        for (int j = body; j < half; ++j) {
+            const uint8_t b = row[j];
+            s += nib_lo(b) * (int32_t)xe[j] + nib_hi(b) * (int32_t)xo[j];
+        }
+        acc[r] = s;
+    }
+    free(xe);
+    free(xo);
+}
+#endif
+
+void or_int4_i8_gemv_acc(const int8_t* x, const uint8_t* weights, int rows, int width,
+                         int32_t* acc)
+{
+#if defined(__x86_64__)
+    if (or_simd_active()) {
+        gemv_acc_vnni(x, weights, rows, width, acc);
+        return;
+    }
+#endif
+    gemv_acc_scalar(x, weights, rows, width, acc);
 }
 
 void or_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const float* scales,
@@ -391,13 +476,15 @@ static void gqa_split_impl(const float* query, const void* keys, const void* val
     const float scale = 1.0f / sqrtf((float)head_dim);
     const int nchunks = (context + chunk - 1) / chunk;
     const int dpl = head_dim / 16;
-    float* m = (float*)malloc(sizeof(float) * (size_t)nchunks);
-    float* l = (float*)malloc(sizeof(float) * (size_t)nchunks);
-    float* o = (float*)malloc(sizeof(float) * (size_t)nchunks * (size_t)head_dim);
-    float s[256], e[256], tree[256], kf[256];
-    for (int g = 0; g < kv_heads; ++g) {
-        for (int h = 0; h < groups; ++h) {
-            const int qh = g * groups + h;
+    /* query heads are independent: one OpenMP thread per head at a time */
+#pragma omp parallel for schedule(dynamic, 1) if (context >= 256)
+    for (int qh = 0; qh < kv_heads * groups; ++qh) {
+        {
+            const int g = qh / groups;
+            float* m = (float*)malloc(sizeof(float) * (size_t)nchunks);
+            float* l = (float*)malloc(sizeof(float) * (size_t)nchunks);
+            float* o = (float*)malloc(sizeof(float) * (size_t)nchunks * (size_t)head_dim);
+            float s[256], e[256], tree[256], kf[256];
             const float* q = query + (int64_t)qh * head_dim;
             for (int c = 0; c < nchunks; ++c) {
                 float mc = -INFINITY;
@@ -454,9 +541,9 @@ static void gqa_split_impl(const float* query, const void* keys, const void* val
             }
             const float inv = 1.0f / L;
             for (int d = 0; d < head_dim; ++d) out[d] = out[d] * inv;
+            free(m); free(l); free(o);
         }
     }
-    free(m); free(l); free(o);
 }
 
 void or_gqa_decode_split(const float* query, const uint16_t* keys, const uint16_t* values,

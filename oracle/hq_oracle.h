@@ -55,6 +55,12 @@ void or_rope(float* x, int heads, int head_dim, const float* cos_row, const floa
 /* ---- GEMV ---- */
 void or_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const float* scales,
                      float activation_scale, float* output, int rows, int width);
+/* Vector path control (AVX-512 VNNI where the CPU has it; same integers)
+ * and OpenMP thread count of the GEMVs. */
+void or_set_simd(int on);
+int or_simd_active(void);
+void or_set_threads(int n);
+int or_max_threads(void);
 void or_int4_i8_gemv_acc(const int8_t* x, const uint8_t* weights, int rows, int width,
                          int32_t* acc);
 void or_int4_i8_gemm_acc(const int8_t* x, const uint8_t* weights, int m, int rows,

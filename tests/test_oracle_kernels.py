@@ -281,3 +281,33 @@ def test_argmax_golden_ties_and_nan(kat):
     assert oracle.argmax(y) == int(np.argmax(y)) == 1
     z = np.array([-0.0, 0.0], dtype=np.float32)
     assert oracle.argmax(z) == int(np.argmax(z)) == 0
+
+
+# ----------------------------------------------------------------- GEMV vector path
+@pytest.mark.parametrize("rows,width", [(1, 2), (3, 126), (5, 128), (7, 130), (64, 2560), (33, 4162),
+                                        (17, 9728)])
+def test_gemv_vector_path_equals_scalar(rows, width):
+    """The AVX-512 VNNI path (used where the CPU has it) and the scalar loop
+    give the same int32 accumulators: random bytes (every nibble value, -8
+    included), int8 activations over the whole range, and the extremes."""
+    rng = np.random.default_rng(rows * 1000 + width)
+    cases = [(rng.integers(0, 256, (rows, width // 2), dtype=np.uint8),
+              rng.integers(-128, 128, width, dtype=np.int8)),
+             (np.full((rows, width // 2), 0x88, np.uint8), np.full(width, -128, np.int8)),
+             (np.full((rows, width // 2), 0x77, np.uint8), np.full(width, 127, np.int8))]
+    try:
+        for w, x in cases:
+            oracle.set_simd(False)
+            ref = oracle.int4_i8_gemv_acc(x, w, rows, width)
+            oracle.set_simd(True)
+            got = oracle.int4_i8_gemv_acc(x, w, rows, width)
+            np.testing.assert_array_equal(got, ref)
+            # and the closed form on the unpacked values (int64)
+            lo = (w & 0xF).astype(np.int64)
+            hi = (w >> 4).astype(np.int64)
+            full = np.empty((rows, width), np.int64)
+            full[:, 0::2] = np.where(lo > 7, lo - 16, lo)
+            full[:, 1::2] = np.where(hi > 7, hi - 16, hi)
+            np.testing.assert_array_equal(ref, full @ x.astype(np.int64))
+    finally:
+        oracle.set_simd(True)
