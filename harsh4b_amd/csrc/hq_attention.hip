@@ -8,9 +8,9 @@
 // At batch 1 there are only kv_heads (8) independent heads, so the time axis
 // is split into chunks of 64 positions: block (kv_head, chunk) handles the
 // `groups` query heads that share one K/V stream (each K/V byte is read
-// once), computes its chunk's max, exp-sum and partial V accumulation, and
-// the last block of a kv head to arrive (an atomic ticket, no waiting)
-// combines the chunk partials.  In STEP mode the kernel also applies the
+// once), computes its chunk's max, exp-sum and partial V accumulation and
+// publishes them; a second kernel (attention_combine_kernel) combines the
+// chunk partials of every (query head, dim) in parallel.  In STEP mode the kernel also applies the
 // per-head RMSNorm (cpu_lightspark.py:435-436) and RoPE (:437-438) to the raw
 // q/k projection and writes the fp16 k/v of the current position into the
 // cache (:439-440), so no separate kernel runs between the qkv GEMV and the
@@ -60,10 +60,9 @@ __device__ __forceinline__ void load_chunk(const AttnParams& a, const uint16_t* 
 
 // Block (kv_head, split) walks chunks [split*CPB, split*CPB + CPB) of the
 // context.  With a single split (context <= CPB*64) it combines its chunk
-// partials itself; otherwise the partials go to the workspace and the last
-// split of the kv head to arrive combines all of them.  Either way the
-// combine runs over ascending chunks, so the result is the same bits.
-constexpr int kCmbFloats = 2048;   // combine staging: 2 * G * (chunks per batch)
+// partials itself; otherwise the partials go to the workspace and
+// attention_combine_kernel combines them.  Either way the combine runs over
+// ascending chunks, so the result is the same bits.
 
 template <int D, int GMAX, bool STEP, int CPB>
 __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
@@ -82,9 +81,6 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     __shared__ float m_s[GMAX][CPB];
     __shared__ float l_s[GMAX][CPB];
     __shared__ float o_s[CPB][GMAX][D];   // per-chunk V partials
-    __shared__ int last_flag;
-    __shared__ float cmb_s[kCmbFloats];   // the last split's combine: staged a_c and l_c
-    __shared__ float mh_s[GMAX];
 
     const int g = blockIdx.x;
     const int split = blockIdx.y;
@@ -122,7 +118,6 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     const size_t zq = size_t(blockIdx.z) * size_t(a.kv_heads) * G * D;
     float* const out = a.out + zq;
     float* const part = a.part + size_t(blockIdx.z) * size_t(a.kv_heads) * G * a.max_chunks * (D + 2);
-    int32_t* const counters = a.counters + size_t(blockIdx.z) * a.kv_heads;
     const int nc = (n + C - 1) / C;
     const int nsplit = (nc + CPB - 1) / CPB;
     if (split >= nsplit) return;
@@ -346,81 +341,95 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
             if (d == 0) { publish_f(pp, m_s[h][ci]); publish_f(pp + 1, l_s[h][ci]); }
         }
     }
-    wait_all_memory();
-    __syncthreads();
-    if (tid == 0) {
-        const int ticket = atomicAdd(counters + g, 1);
-        last_flag = (ticket == nsplit - 1);
+    // (attention_combine_kernel, launched next on the stream, combines them)
+}
+
+// Combine of the chunk partials when a context spans several chunks: thread
+// (blockIdx.x * kBlock + tid) is output element (query head hh, dim d) of
+// query z = blockIdx.y.  Same arithmetic as the single-chunk combine above:
+// M = max_c m_c; a_c = exp(m_c - M); L and O as fmaf chains over ascending
+// c; out = O * (1 / L).  The block's heads' m_c and l_c are staged in LDS
+// (batches of CB chunks), the a_c computed once per chunk in place of m_c,
+// and the o values read 64 chunks at a time (coalesced over d).
+template <int D, bool STEP>
+__global__ __launch_bounds__(kBlock) void attention_combine_kernel(AttnParams a)
+{
+    constexpr int C = kAttnChunk;
+    constexpr int HPB = kBlock / D;           // query heads per block
+    constexpr int CB = 4096 / HPB;            // chunks per staged batch
+    constexpr int OB = 64;                    // o values in flight per thread
+    __shared__ float m_s[HPB][CB];
+    __shared__ float l_s[HPB][CB];
+    __shared__ float red_s[kBlock];
+    const int z = blockIdx.y;
+    int n;
+    if constexpr (STEP) {
+        const int pos = *a.position;
+        if (pos < 0 || pos >= a.capacity) return;   // (flagged by attention_kernel)
+        n = pos + 1;
+    } else if (a.table) {
+        const int zpos = *a.table->position[z];
+        n = min(max(zpos, 0), a.table->capacity[z] - 1) + 1;
+    } else {
+        n = a.context + z;
     }
-    __syncthreads();
-    if (!last_flag) return;
-    // The last split of the kv head combines all nc chunks of its G heads:
-    // M_h = max_c m_c, a_c = exp(m_c - M_h), L and O as fmaf chains over
-    // ascending c, out = O * (1 / L).  The m and l values are staged in LDS
-    // by all threads (batches of cb chunks), the maxima are wave
-    // reductions, the a_c are computed in parallel in place of the m values,
-    // and each thread then runs the chains of its (head, dim) pairs with the
-    // o values of 16 chunks in flight (staging o in LDS as well measured
-    // slower: 30.3 against 25.9 us at context 4096).
-    {
-        const int cb = kCmbFloats / (2 * G);          // chunks per staged batch
-        for (int h = wave; h < G; h += kBlock / kWave) if (lane == 0) mh_s[h] = -__builtin_inff();
-        for (int c0 = 0; c0 < nc; c0 += cb) {         // M (one batch in the common case)
-            const int nb = min(cb, nc - c0);
-            __syncthreads();
-#pragma unroll 4
-            for (int i = tid; i < G * nb; i += kBlock)
-                cmb_s[i] = read_f(part + (size_t(g * G + i / nb) * a.max_chunks + c0 + i % nb) * pstride);
-            __syncthreads();
-            for (int h = wave; h < G; h += kBlock / kWave) {
-                float mm = -__builtin_inff();
-                for (int c = lane; c < nb; c += kWave) mm = fmaxf(mm, cmb_s[h * nb + c]);
-                mm = wave_max64_all(mm);
-                if (lane == 0) mh_s[h] = fmaxf(mh_s[h], mm);
-            }
+    const int nc = (n + C - 1) / C;
+    if (nc <= 1) return;                       // attention_kernel combined it in-block
+    const int heads = a.kv_heads * a.groups;
+    const int tid = threadIdx.x;
+    const int hl = tid / D, d = tid % D;
+    const int hh = blockIdx.x * HPB + hl;
+    const bool live = hh < heads;
+    constexpr int pstride = D + 2;
+    const float* part = a.part + size_t(z) * size_t(heads) * a.max_chunks * pstride;
+    const float* ph = part + size_t(min(hh, heads - 1)) * a.max_chunks * pstride;
+
+    float M = -__builtin_inff();
+    if (nc > CB) {
+        // M from every chunk first (several staged batches follow)
+        float mm = -__builtin_inff();
+        for (int c = d; c < nc; c += D) mm = fmaxf(mm, read_f(ph + size_t(c) * pstride));
+        red_s[tid] = mm;
+        __syncthreads();
+        for (int i = 0; i < D; ++i) M = fmaxf(M, red_s[hl * D + i]);
+    }
+    float L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += CB) {
+        const int nb = min(CB, nc - c0);
+        __syncthreads();
+        // the first OB o values go out with the m, l loads
+        float ov[OB];
+#pragma unroll
+        for (int j = 0; j < OB; ++j) ov[j] = j < nb ? read_f(ph + size_t(c0 + j) * pstride + 2 + d) : 0.0f;
+        for (int i = tid; i < HPB * nb; i += kBlock) {
+            const int h2 = min(blockIdx.x * HPB + i / nb, heads - 1);
+            const float* pp = part + (size_t(h2) * a.max_chunks + c0 + i % nb) * pstride;
+            m_s[i / nb][i % nb] = read_f(pp);
+            l_s[i / nb][i % nb] = read_f(pp + 1);
         }
-        float L[PAIRS], O[PAIRS];
+        __syncthreads();
+        if (nc <= CB)
+            for (int c = 0; c < nb; ++c) M = fmaxf(M, m_s[hl][c]);
+        __syncthreads();
+        // a_c in place of m_c: thread d of head hl takes chunks d, d + D, ...
+        for (int c = d; c < nb; c += D) m_s[hl][c] = spec_expf(m_s[hl][c] - M);
+        __syncthreads();
+        for (int cb = 0; cb < nb; cb += OB) {
+            if (cb > 0) {
 #pragma unroll
-        for (int r = 0; r < PAIRS; ++r) { L[r] = 0.0f; O[r] = 0.0f; }
-        for (int c0 = 0; c0 < nc; c0 += cb) {
-            const int nb = min(cb, nc - c0);
-            __syncthreads();
-            // a_c of head h at [h*nb + c], l_c at [(G + h)*nb + c]
-#pragma unroll 4
-            for (int i = tid; i < 2 * G * nb; i += kBlock) {
-                const int k = i / nb, c = c0 + i % nb;
-                const int h = k < G ? k : k - G;
-                const float v = read_f(part + (size_t(g * G + h) * a.max_chunks + c) * pstride + (k < G ? 0 : 1));
-                cmb_s[i] = k < G ? spec_expf(v - mh_s[h]) : v;
+                for (int j = 0; j < OB; ++j)
+                    ov[j] = cb + j < nb ? read_f(ph + size_t(c0 + cb + j) * pstride + 2 + d) : 0.0f;
             }
-            __syncthreads();
 #pragma unroll
-            for (int r = 0; r < PAIRS; ++r) {
-                const int h = h0 + HSTEP * r;
-                if (h >= G) continue;
-                const float* src = part + size_t(g * G + h) * a.max_chunks * pstride + 2 + d;
-                const float* sa = cmb_s + h * nb;
-                const float* sl = cmb_s + (G + h) * nb;
-                for (int c = 0; c < nb; c += 16) {
-                    float ov[16];
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) ov[j] = c + j < nb ? read_f(src + size_t(c0 + c + j) * pstride) : 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 16; ++j)
-                        if (c + j < nb) {
-                            L[r] = __builtin_fmaf(sa[c + j], sl[c + j], L[r]);
-                            O[r] = __builtin_fmaf(sa[c + j], ov[j], O[r]);
-                        }
+            for (int j = 0; j < OB; ++j)
+                if (cb + j < nb) {
+                    const float al = m_s[hl][cb + j];
+                    L = __builtin_fmaf(al, l_s[hl][cb + j], L);
+                    O = __builtin_fmaf(al, ov[j], O);
                 }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < PAIRS; ++r) {
-            const int h = h0 + HSTEP * r;
-            if (h < G) out[size_t(g * G + h) * D + d] = O[r] * (1.0f / L[r]);
         }
     }
-    if (tid == 0) publish_i(counters + g, 0);
+    if (live) a.out[size_t(z) * size_t(heads) * D + size_t(hh) * D + d] = O * (1.0f / L);
 }
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim)
@@ -445,6 +454,12 @@ static hipError_t launch_attn(const AttnParams& a, hipStream_t s)
     const int batch = (!STEP && a.batch > 1) ? a.batch : 1;
     hipLaunchKernelGGL((attention_kernel<D, GMAX, STEP, kChunksPerBlock>), dim3(a.kv_heads, splits, batch),
                        dim3(kBlock), 0, s, a);
+    if (a.max_chunks > 1) {
+        constexpr int hpb = kBlock / D;
+        const int heads = a.kv_heads * a.groups;
+        hipLaunchKernelGGL((attention_combine_kernel<D, STEP>), dim3((heads + hpb - 1) / hpb, batch), dim3(kBlock),
+                           0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -458,7 +473,10 @@ hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s)
     case 16: return launch_attn<16, 8, false>(a, s);
     case 32: return launch_attn<32, 8, false>(a, s);
     case 64: return launch_attn<64, 8, false>(a, s);
-    case 128: return launch_attn<128, 8, false>(a, s);
+    case 128:
+        // up to four query heads per kv head (Qwen3-4B's 32/8): the V
+        // accumulation then runs two (head, dim) pairs per thread, not four
+        return a.groups <= 4 ? launch_attn<128, 4, false>(a, s) : launch_attn<128, 8, false>(a, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -471,9 +489,8 @@ extern "C" size_t hq_gqa_workspace_bytes(int score_stride, int kv_heads, int gro
 {
     if (score_stride <= 0 || kv_heads <= 0 || groups <= 0 || head_dim <= 0) return 0;
     const int nc = (score_stride + kAttnChunk - 1) / kAttnChunk;
-    // arrival counters in the first 256 bytes (a fixed place, so one zeroed
-    // workspace serves every context up to score_stride), then the chunk
-    // partials
+    // a 256-byte header (reserved), then the chunk partials: one workspace
+    // serves every context up to score_stride
     return 256 + attention_workspace_floats(kv_heads * groups, nc, head_dim) * 4;
 }
 
@@ -485,7 +502,7 @@ static int gqa_check(const float* query, const uint16_t* keys, const uint16_t* v
     if (context <= 0 || kv_heads <= 0 || groups <= 0 || groups > 8) return HQ_ERR_ARG;
     if (score_stride < context) return HQ_ERR_ARG;
     if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128) return HQ_ERR_ARG;
-    if (kv_heads * 256 > 256 * 64) return HQ_ERR_ARG;   // counters fit in 256 bytes
+    if (kv_heads > 64) return HQ_ERR_ARG;
     if ((reinterpret_cast<uintptr_t>(keys) & 15u) != 0 || (reinterpret_cast<uintptr_t>(values) & 15u) != 0)
         return HQ_ERR_ALIGN;
     return HQ_OK;
@@ -505,7 +522,6 @@ static int gqa_launch(const float* query, const uint16_t* keys, const uint16_t* 
     a.groups = groups;
     a.head_dim = head_dim;
     a.max_chunks = nc;
-    a.counters = static_cast<int32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
     a.out = output;
     const hipError_t e = launch_attention(a, false, stream);
@@ -558,14 +574,6 @@ static void* scratch_address(int dev)
     return g_scratch_ptr[dev];
 }
 
-// Zero the arrival counters: a kernel, not hipMemsetAsync, so the call can
-// be captured into a graph.  The attention kernel leaves them at zero again,
-// so this only matters after an overlapping call left them inconsistent.
-__global__ void zero_counters_kernel(int32_t* c, int n)
-{
-    if (int(threadIdx.x) < n) c[threadIdx.x] = 0;
-}
-
 extern "C" int hq_gqa_decode_noalloc(const float* query, const uint16_t* keys, const uint16_t* values,
                                      float* output, int context, int kv_heads, int groups, int head_dim,
                                      int score_stride, void* stream)
@@ -580,7 +588,5 @@ extern "C" int hq_gqa_decode_noalloc(const float* query, const uint16_t* keys, c
     void* ws = scratch_address(dev);
     if (ws == nullptr) return HQ_ERR_DEVICE;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(zero_counters_kernel, dim3(1), dim3(64), 0, s, static_cast<int32_t*>(ws), 64);
-    if (hipGetLastError() != hipSuccess) return HQ_ERR_LAUNCH;
     return gqa_launch(query, keys, values, ws, output, context, kv_heads, groups, head_dim, s);
 }

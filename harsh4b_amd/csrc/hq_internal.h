@@ -79,11 +79,10 @@ struct AttnParams {
     int context;                // PLAIN: positions of query 0
     int batch;                  // PLAIN: queries (grid z); query z sees context + z positions,
                                 // reads q + z*heads*D, writes out + z*heads*D and uses its own
-                                // part / counters regions (max_chunks and kv_heads apart)
+                                // part region (max_chunks apart)
     int kv_heads, groups, head_dim;
     int max_chunks;             // grid.y
     float* part;                // [heads, max_chunks, head_dim + 2]
-    int32_t* counters;          // [kv_heads], zero between launches
     float* out;                 // [heads, D]
     // PLAIN batches of a batched decode step (nullable): query z attends the
     // cache of sequence z (layer `layer`) up to its position, table->position[z]

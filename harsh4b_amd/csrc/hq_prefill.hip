@@ -214,7 +214,7 @@ __global__ void prefill_position_kernel(int32_t* position, int value) { *positio
 
 // Workspace layout for a model and KV capacity.
 struct PrefillLayout {
-    size_t x, q8, act, qkv, qh, att, proj, gu, gemm, attn_counters, attn_part, total;
+    size_t x, q8, act, qkv, qh, att, proj, gu, gemm, attn_part, total;
     int kp, max_chunks, qkv_rows, qd;
 };
 
@@ -246,7 +246,6 @@ static PrefillLayout prefill_layout(const hq_model* m, int capacity)
     g = std::max<size_t>(g, gemm_scratch_bytes(B, 2 * I, H));
     g = std::max<size_t>(g, gemm_scratch_bytes(B, H, I));
     L.gemm = take(g);
-    L.attn_counters = take(size_t(B) * m->kv_heads * 4);
     L.attn_part = take(size_t(B) * attention_workspace_floats(m->heads, L.max_chunks, D) * 4);
     L.total = off;
     return L;
@@ -453,7 +452,7 @@ __global__ __launch_bounds__(kBlock) void batch_store_x_kernel(const float* x, i
 }
 
 struct BatchLayout {
-    size_t x, q8, act, qkv, qh, att, proj, gu, gemm, attn_counters, attn_part, logits, pval, pidx, tickets, table,
+    size_t x, q8, act, qkv, qh, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, table,
         total;
     int kp, max_chunks, qkv_rows, qd, arg_blocks;
 };
@@ -486,7 +485,6 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     g = std::max<size_t>(g, gemm_scratch_bytes(B, H, I));
     g = std::max<size_t>(g, gemm_scratch_bytes(B, V, H));
     L.gemm = take(g);
-    L.attn_counters = take(size_t(B) * m->kv_heads * 4);
     L.attn_part = take(size_t(B) * attention_workspace_floats(m->heads, L.max_chunks, D) * 4);
     L.logits = take(size_t(B) * V * 4);
     L.pval = take(size_t(B) * L.arg_blocks * 4);
@@ -578,7 +576,6 @@ extern "C" int hq_prefill(const hq_model* m, const hq_state* st, const int32_t* 
             a.groups = m->heads / KV;
             a.head_dim = D;
             a.max_chunks = L.max_chunks;
-            a.counters = reinterpret_cast<int32_t*>(ws + L.attn_counters);
             a.part = reinterpret_cast<float*>(ws + L.attn_part);
             a.out = att;
             if (launch_attention(a, false, s) != hipSuccess) return HQ_ERR_LAUNCH;
@@ -702,7 +699,6 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         a.groups = m->heads / KV;
         a.head_dim = D;
         a.max_chunks = L.max_chunks;
-        a.counters = reinterpret_cast<int32_t*>(ws + L.attn_counters);
         a.part = reinterpret_cast<float*>(ws + L.attn_part);
         a.out = att;
         a.table = table;

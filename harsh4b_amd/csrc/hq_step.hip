@@ -43,7 +43,7 @@ __global__ __launch_bounds__(kBlock) void embedding_kernel(
 
 struct StepLayout {
     int q_size, kv_size, groups, max_chunks, lm_blocks;
-    size_t attn_part_bytes, attn_counter_off, lm_val_off, lm_idx_off, lm_counter_off;
+    size_t attn_part_bytes, lm_val_off, lm_idx_off, lm_counter_off;
     size_t epoch_off, ll_off, eng_part_off, trace_off, total;
 };
 
@@ -58,8 +58,7 @@ static StepLayout step_layout(const hq_model* m, int capacity)
     L.max_chunks = (capacity + kAttnChunk - 1) / kAttnChunk;
     L.lm_blocks = step_gemv_blocks(StepGemv::LmHead, m->vocab, 0, m->hidden);
     L.attn_part_bytes = align256(attention_workspace_floats(m->heads, L.max_chunks, m->head_dim) * 4);
-    L.attn_counter_off = L.attn_part_bytes;
-    L.lm_val_off = L.attn_counter_off + align256(size_t(m->heads > m->kv_heads ? m->heads : m->kv_heads) * 4);
+    L.lm_val_off = L.attn_part_bytes;
     L.lm_idx_off = L.lm_val_off + align256(size_t(L.lm_blocks) * 4);
     L.lm_counter_off = L.lm_idx_off + align256(size_t(L.lm_blocks) * 4);
     L.epoch_off = L.lm_counter_off + align256(size_t(ticket_words(L.lm_blocks)) * 4);
@@ -163,7 +162,6 @@ static hipError_t enqueue_layers(const hq_model* m, const hq_state* st, hipStrea
         a.kv_heads = m->kv_heads; a.groups = Ly.groups; a.head_dim = m->head_dim;
         a.max_chunks = Ly.max_chunks;
         a.part = reinterpret_cast<float*>(ws);
-        a.counters = reinterpret_cast<int32_t*>(ws + Ly.attn_counter_off);
         a.out = st->attended;
         if ((e = launch_attention(a, true, s)) != hipSuccess) return e;
 

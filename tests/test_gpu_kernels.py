@@ -183,7 +183,8 @@ def test_gqa_other_head_shapes(d, g):
 
 
 def test_gqa_repeated_calls_reuse_workspace():
-    # the arrival counters must be back at zero after every call
+    # one workspace serves every later call, longer or shorter (it holds
+    # partials of earlier calls: each call writes every partial it reads)
     ls = lightspark()
     rng = np.random.default_rng(77)
     kv, g, d = 8, 4, 128
