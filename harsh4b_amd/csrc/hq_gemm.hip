@@ -11,26 +11,34 @@
 // A lane of the A operand carries 16 K values of one weight row; the nibbles
 // of a packed dword become signed bytes (w << 4) & 0xF0F0F0F0 (16 * even
 // columns) and w & 0xF0F0F0F0 (16 * odd columns), so the MFMA accumulates
-// 16 * acc exactly.  The B operand is the activation slice stored in LDS with
-// the same per-8-column even/odd order, so A and B agree on the K order: a
-// prologue kernel writes the int8 activations once into the workspace in
-// that order, rows padded to whole 256-column slices with zeros, and each
-// GEMM block copies its columns into LDS with global->LDS loads.
-// K is split across blocks so that small row counts still fill the chip;
-// split partial sums meet in an int32 workspace through atomic adds, and the
-// last split to arrive at a row tile writes the epilogue and re-zeroes its
-// part of the workspace (no waiting anywhere).
+// 16 * acc exactly.  The B operand is the activations in the same per-8-column
+// even/odd order (the quantizing kernels write them so, rows padded with
+// zeros to whole 256-column slices), read straight from global memory (L2):
+// lane group q of a "double step" of 128 columns holds columns [32q, 32q+32)
+// as two 16-column MFMA operands, for A from one 16-byte load of the packed
+// row and for B from two 16-byte loads of the activation row.
+//
+// A block owns RG groups of 16 rows over the whole K; its W waves split K
+// (each a contiguous range of double steps, all of its loads in flight at
+// once) and their int32 partial tiles meet in LDS, so no split of K crosses
+// blocks: no atomics, no arrival tickets, no zeroed workspace.
 #include "hq_device.h"
 #include "hq_internal.h"
 
 namespace hq {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kTileRows = 64;     // 4 waves x 16 rows
-constexpr int kSlice = 256;       // K columns staged per iteration
+// 16-byte load that streams past the caches (the weights are read once)
+__device__ __forceinline__ uint4 load16_nt(const uint8_t* p)
+{
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+constexpr int kSlice = 256;       // activation rows are padded to whole slices of 256 columns
 constexpr int kMaxBatch = 32;     // sequences per launch (two 16-wide B tiles)
-constexpr int kMaxSlices = 10;    // K slices one block covers (its weights in flight at once)
 
 struct GemmParams {
     const int8_t* x;          // [m, kp] de-interleaved per 8 columns, zero past K
@@ -39,11 +47,7 @@ struct GemmParams {
     const float* ws;          // [N]
     float* out;               // [m, N]
     int32_t* acc_out;         // nullable [m, N]
-    int32_t* acc;             // workspace [m, N] (zero between calls)
-    int32_t* counters;        // workspace [tiles]
     int m, n, k, kp;          // kp: padded row stride of x (a multiple of kSlice)
-    int slices_per_split;
-    int splits;
 };
 
 // De-interleave 8 int8 columns (a, b = the two little-endian dwords) into
@@ -54,135 +58,100 @@ __device__ __forceinline__ void deinterleave8(uint32_t a, uint32_t b, uint32_t& 
     od = ((a >> 8) & 0xFFu) | ((a >> 16) & 0xFF00u) | ((b & 0xFF00u) << 8) | (b & 0xFF000000u);
 }
 
-// A block covers one 64-row tile over a range of at most kMaxSlices K
-// slices.  Every lane issues all of its weight loads for the range first
-// (32 bytes of its row per slice), so a block keeps up to 64 KB of weights in
-// flight; the activation columns of the range are staged in LDS (de-interleaved,
-// once per block) while those loads travel, and the MFMAs then run from
-// registers and LDS without further barriers.
-template <int BT>
-__global__ __launch_bounds__(kBlock) void gemm_mfma_kernel(GemmParams p)
+template <int RG, int W, int BT, int DS>
+__global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
 {
-    constexpr int MP = 16 * BT;                 // padded batch
-    __shared__ __align__(16) uint8_t xs[MP * kSlice * kMaxSlices];
-    __shared__ int last_flag;
-
+    __shared__ int32_t red[W][RG * BT * 4][kWave];
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid & (kWave - 1);
-    const int tile = blockIdx.x;
-    const int split = blockIdx.y;
-    const int row0 = tile * kTileRows + wave * 16;
-    const int arow = row0 + (lane & 15);        // A row of this lane
-    const int kb = lane >> 4;                   // 0..3: 64-column quarter of a slice
-    const bool arow_ok = arow < p.n;
-    const int half = p.k >> 1;
-    const uint8_t* wrow = p.w + size_t(arow_ok ? arow : 0) * size_t(half);
-    const int nslices = (p.k + kSlice - 1) / kSlice;
-    const int s_begin = split * p.slices_per_split;
-    const int ns = min(nslices, s_begin + p.slices_per_split) - s_begin;   // 1 .. kMaxSlices
-
-    // A: 32 packed bytes (64 columns) of row `arow` per lane and slice: the
-    // four lanes of a row read its slice bytes [16kb, 16kb+16) (wa) and
-    // [64+16kb, 64+16kb+16) (wb), so each load instruction reads 64
-    // contiguous bytes of each of its 16 rows
-    uint4 wa[kMaxSlices], wb[kMaxSlices];
+    const int q = lane >> 4;                    // lane group: columns [32q, 32q + 32) of a double step
+    const int r16 = lane & 15;                  // A: row within a group; B: sequence within a tile
+    const int row0 = blockIdx.x * 16 * RG;
+    const int half = p.k >> 1;                  // packed bytes per row (a multiple of 16)
+    const int nds = (p.k + 127) >> 7;           // double steps of 128 columns
+    const int ds0 = nds * wave / W, ds1 = nds * (wave + 1) / W;
+    const uint8_t* arow[RG];
+    bool aok[RG];
 #pragma unroll
-    for (int j = 0; j < kMaxSlices; ++j) {
-        wa[j] = make_uint4(0, 0, 0, 0);
-        wb[j] = make_uint4(0, 0, 0, 0);
-        const int ca = (s_begin + j) * kSlice + 32 * kb;        // first column of wa
-        const int cb = ca + 128;                                 // first column of wb
-        if (j < ns && arow_ok && ca < p.k) wa[j] = *reinterpret_cast<const uint4*>(wrow + (ca >> 1));
-        if (j < ns && arow_ok && cb < p.k) wb[j] = *reinterpret_cast<const uint4*>(wrow + (cb >> 1));
+    for (int rg = 0; rg < RG; ++rg) {
+        const int row = row0 + 16 * rg + r16;
+        aok[rg] = row < p.n;
+        arow[rg] = p.w + size_t(aok[rg] ? row : 0) * size_t(half);
     }
+    const int8_t* brow[BT];
+#pragma unroll
+    for (int b = 0; b < BT; ++b) brow[b] = p.x + size_t(min(16 * b + r16, p.m - 1)) * size_t(p.kp);
 
-    // stage x[:, range] (already de-interleaved, zero past K and in rows
-    // m .. MP-1 of the workspace) into LDS, rows of ns*kSlice bytes
-    const int rowb = ns * kSlice;
-    const int chunks = MP * rowb / 16;
-    const int k0 = s_begin * kSlice;
-    const uint32_t xs0 = lds_addr(xs);
-    for (int q0 = wave * kWave; q0 < chunks; q0 += kBlock) {
-        const int q = q0 + lane;
-        const int mm = q / (rowb / 16);
-        const int c = (q % (rowb / 16)) * 16;
-        if (q < chunks) dma16(p.x, uint32_t(mm * p.kp + k0 + c), xs0 + uint32_t(q0) * 16u);
-    }
-    wait_all_memory();
-    __syncthreads();
-
-    i32x4 acc[BT];
+    i32x4 acc[RG][BT];
 #pragma unroll
-    for (int b = 0; b < BT; ++b) acc[b] = i32x4{0, 0, 0, 0};
+    for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-    for (int sl = 0; sl < kMaxSlices; ++sl) {
-        if (sl < ns) {
-            const uint32_t wd[8] = {wa[sl].x, wa[sl].y, wa[sl].z, wa[sl].w, wb[sl].x, wb[sl].y, wb[sl].z, wb[sl].w};
+        for (int b = 0; b < BT; ++b) acc[rg][b] = i32x4{0, 0, 0, 0};
+    constexpr uint32_t m4 = 0xF0F0F0F0u;
+    for (int d0 = ds0; d0 < ds1; d0 += DS) {
+        const int nd = min(DS, ds1 - d0);
+        uint4 wa[DS][RG], xb[DS][BT][2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t m4 = 0xF0F0F0F0u;
-                const i32x4 a = {int((wd[2 * j] << 4) & m4), int(wd[2 * j] & m4),
-                                 int((wd[2 * j + 1] << 4) & m4), int(wd[2 * j + 1] & m4)};
-                // columns of chunk j: wa holds [32kb, 32kb+32), wb [128+32kb, 128+32kb+32)
-                const int cofs = sl * kSlice + (j >> 1) * 128 + 32 * kb + 16 * (j & 1);
+        for (int j = 0; j < DS; ++j) {
+            const int pb = (d0 + j) * 64 + 16 * q;          // this lane's 16 packed bytes
 #pragma unroll
-                for (int b = 0; b < BT; ++b) {
-                    const uint4 xv = *reinterpret_cast<const uint4*>(xs + (16 * b + (lane & 15)) * rowb + cofs);
-                    const i32x4 bv = {int(xv.x), int(xv.y), int(xv.z), int(xv.w)};
-                    acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bv, acc[b], 0, 0, 0);
+            for (int rg = 0; rg < RG; ++rg)
+                wa[j][rg] = (j < nd && aok[rg] && pb < half)
+                                ? load16_nt(arow[rg] + pb)
+                                : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < BT; ++b) {
+                const int8_t* xp = brow[b] + 2 * pb;             // columns 2pb .. 2pb + 32 (zero past K)
+                xb[j][b][0] = j < nd ? *reinterpret_cast<const uint4*>(xp) : make_uint4(0, 0, 0, 0);
+                xb[j][b][1] = j < nd ? *reinterpret_cast<const uint4*>(xp + 16) : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < DS; ++j) {
+            if (j < nd) {
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg) {
+                    const uint4 w = wa[j][rg];
+                    const i32x4 a0 = {int((w.x << 4) & m4), int(w.x & m4), int((w.y << 4) & m4), int(w.y & m4)};
+                    const i32x4 a1 = {int((w.z << 4) & m4), int(w.z & m4), int((w.w << 4) & m4), int(w.w & m4)};
+#pragma unroll
+                    for (int b = 0; b < BT; ++b) {
+                        const uint4 x0 = xb[j][b][0], x1 = xb[j][b][1];
+                        acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            a0, i32x4{int(x0.x), int(x0.y), int(x0.z), int(x0.w)}, acc[rg][b], 0, 0, 0);
+                        acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            a1, i32x4{int(x1.x), int(x1.y), int(x1.z), int(x1.w)}, acc[rg][b], 0, 0, 0);
+                    }
                 }
             }
         }
     }
-
-    // D layout: lane holds rows 4*(lane/16) + r, column lane % 16.
-    const int col_m = lane & 15;
-    const int rbase = row0 + 4 * (lane >> 4);
-    if (p.splits == 1) {
+    // D layout: lane holds rows 4 * (lane / 16) + r, column lane % 16
 #pragma unroll
-        for (int b = 0; b < BT; ++b) {
-            const int mm = 16 * b + col_m;
+    for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int n = rbase + r;
-                if (mm < p.m && n < p.n) {
-                    const int a = acc[b][r] >> 4;
-                    p.out[size_t(mm) * p.n + n] = (float(a) * p.act[mm]) * p.ws[n];
-                    if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
-                }
-            }
-        }
-        return;
-    }
+        for (int b = 0; b < BT; ++b)
 #pragma unroll
-    for (int b = 0; b < BT; ++b) {
-        const int mm = 16 * b + col_m;
+            for (int r = 0; r < 4; ++r) red[wave][(rg * BT + b) * 4 + r][lane] = acc[rg][b][r];
+    __syncthreads();
+    // element e of the block's (16 RG rows) x (16 BT sequences) tile: rows
+    // fastest, so the stores of one sequence are contiguous
+    constexpr int NR = 16 * RG;
+    for (int e = tid; e < NR * 16 * BT; e += kWave * W) {
+        const int rl = e % NR, ml = e / NR;
+        const int rg = rl >> 4, rr = rl & 15, b = ml >> 4, col = ml & 15;
+        const int src = col + 16 * (rr >> 2), reg = (rg * BT + b) * 4 + (rr & 3);
+        int32_t sum = 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int n = rbase + r;
-            if (mm < p.m && n < p.n) atomicAdd(p.acc + size_t(mm) * p.n + n, acc[b][r] >> 4);
+        for (int w2 = 0; w2 < W; ++w2) sum += red[w2][reg][src];
+        const int mm = 16 * b + col, n = row0 + rl;
+        if (mm < p.m && n < p.n) {
+            const int a = sum >> 4;
+            p.out[size_t(mm) * p.n + n] = (float(a) * p.act[mm]) * p.ws[n];
+            if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
         }
     }
-    wait_all_memory();   // this thread's atomic adds have been performed
-    __syncthreads();
-    if (tid == 0) {
-        const int ticket = atomicAdd(p.counters + tile, 1);
-        last_flag = (ticket == p.splits - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    const int trows = min(kTileRows, p.n - tile * kTileRows);
-    for (int e = tid; e < p.m * trows; e += kBlock) {
-        const int mm = e / trows;
-        const int n = tile * kTileRows + e % trows;
-        int32_t* cell = p.acc + size_t(mm) * p.n + n;
-        const int a = read_i(cell);
-        p.out[size_t(mm) * p.n + n] = (float(a) * p.act[mm]) * p.ws[n];
-        if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
-        publish_i(cell, 0);
-    }
-    if (tid == 0) publish_i(p.counters + tile, 0);
 }
 
 // Per-sequence spec quantization: block m quantizes row m into q (row
@@ -250,7 +219,7 @@ __global__ __launch_bounds__(kBlock) void batch_deinterleave_kernel(const int8_t
 }
 
 struct GemmLayout {
-    size_t acc_off, counter_off, q_off, act_off, total;
+    size_t q_off, act_off, total;
 };
 
 static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -258,38 +227,39 @@ static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 static int padded_k(int k) { return (k + kSlice - 1) / kSlice * kSlice; }
 static int padded_m(int m) { return (m + kMaxBatch - 1) / kMaxBatch * kMaxBatch; }
 
+// The standalone entries' workspace: the de-interleaved padded activations
+// (padded_m(m) rows of padded_k(k) bytes; padding bytes are never written,
+// zero from the initial fill), then the activation scales.
 static GemmLayout gemm_layout(int m, int n, int k)
 {
-    const int mb = m < kMaxBatch ? m : kMaxBatch;
+    (void)n;
     GemmLayout L{};
-    L.acc_off = 0;
-    L.counter_off = al256(size_t(mb) * size_t(n) * 4);
-    L.q_off = L.counter_off + al256(size_t((n + kTileRows - 1) / kTileRows) * 4);
-    // de-interleaved activations, padded_m(m) rows of padded_k(k) bytes;
-    // padding bytes are never written (zero from the initial fill)
-    L.act_off = L.q_off + al256(size_t(padded_m(m)) * size_t(padded_k(k)));
+    L.q_off = 0;
+    L.act_off = al256(size_t(padded_m(m)) * size_t(padded_k(k)));
     L.total = L.act_off + al256(size_t(m) * 4);
     return L;
 }
 
-// x: the de-interleaved padded activations in the workspace.
-static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, const float* ws,
-                           float* out, int m, int n, int k, int32_t* acc_out, char* workspace,
-                           hipStream_t s)
+template <int RG, int W, int BT>
+static void launch_gemm(const GemmParams& p, hipStream_t s)
 {
-    const GemmLayout L = gemm_layout(m, n, k);
+    // double steps one wave keeps in flight: all of its range up to K =
+    // W * DS * 128 (a 1024-thread block holds fewer registers per lane, the
+    // more so with two sequence tiles)
+    constexpr int DS = W == 16 ? (BT == 2 ? 4 : 5) : 6;
+    hipLaunchKernelGGL((gemm_kernel<RG, W, BT, DS>), dim3((p.n + 16 * RG - 1) / (16 * RG)), dim3(kWave * W), 0, s,
+                       p);
+}
+
+// x: the de-interleaved padded activations.  Waves per block: the fewest of
+// 4, 8, 16 whose K ranges fit one round of loads; rows per block: 32 when
+// that still leaves 512 blocks or more (one sequence tile), else 16.
+static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, const float* ws,
+                           float* out, int m, int n, int k, int32_t* acc_out, hipStream_t s)
+{
     const int kp = padded_k(k);
-    const int tiles = (n + kTileRows - 1) / kTileRows;
-    const int nslices = (k + kSlice - 1) / kSlice;
-    // about one block per CU, each covering at most kMaxSlices slices; a
-    // split K costs a round of atomic adds and a ticket, so shapes with
-    // enough row tiles to fill half the chip are not split
-    int want = tiles >= 128 ? 1 : (256 + tiles - 1) / tiles;
-    if (want < 1) want = 1;
-    if (want > nslices) want = nslices;
-    int per = (nslices + want - 1) / want;
-    if (per > kMaxSlices) per = kMaxSlices;
-    const int splits = (nslices + per - 1) / per;
+    const int nds = (k + 127) / 128;
+    const int waves = nds <= 4 * 6 ? 4 : nds <= 8 * 6 ? 8 : 16;
     for (int m0 = 0; m0 < m; m0 += kMaxBatch) {
         GemmParams p{};
         p.m = m - m0 < kMaxBatch ? m - m0 : kMaxBatch;
@@ -298,15 +268,21 @@ static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, 
         p.w = w; p.ws = ws;
         p.out = out + size_t(m0) * n;
         p.acc_out = acc_out ? acc_out + size_t(m0) * n : nullptr;
-        p.acc = reinterpret_cast<int32_t*>(workspace + L.acc_off);
-        p.counters = reinterpret_cast<int32_t*>(workspace + L.counter_off);
         p.n = n; p.k = k; p.kp = kp;
-        p.slices_per_split = per;
-        p.splits = splits;
-        if (p.m <= 16)
-            hipLaunchKernelGGL(gemm_mfma_kernel<1>, dim3(tiles, splits), dim3(kBlock), 0, s, p);
-        else
-            hipLaunchKernelGGL(gemm_mfma_kernel<2>, dim3(tiles, splits), dim3(kBlock), 0, s, p);
+        const bool two_groups = p.m <= 16 && (n + 31) / 32 >= 512;
+        if (p.m > 16) {
+            if (waves == 4) launch_gemm<1, 4, 2>(p, s);
+            else if (waves == 8) launch_gemm<1, 8, 2>(p, s);
+            else launch_gemm<1, 16, 2>(p, s);
+        } else if (two_groups) {
+            if (waves == 4) launch_gemm<2, 4, 1>(p, s);
+            else if (waves == 8) launch_gemm<2, 8, 1>(p, s);
+            else launch_gemm<2, 16, 1>(p, s);
+        } else {
+            if (waves == 4) launch_gemm<1, 4, 1>(p, s);
+            else if (waves == 8) launch_gemm<1, 8, 1>(p, s);
+            else launch_gemm<1, 16, 1>(p, s);
+        }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -317,11 +293,16 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 
 int gemm_padded_k(int k) { return padded_k(k); }
 int gemm_padded_m(int m) { return padded_m(m); }
-size_t gemm_scratch_bytes(int m, int n, int k) { return gemm_layout(m, n, k).q_off; }
+size_t gemm_scratch_bytes(int m, int n, int k)
+{
+    (void)m; (void)n; (void)k;
+    return 0;   // the GEMM itself needs no workspace
+}
 hipError_t gemm_run(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* out, int m, int n,
                     int k, char* scratch, hipStream_t s)
 {
-    return run_gemm(x, act, w, ws, out, m, n, k, nullptr, scratch, s);
+    (void)scratch;
+    return run_gemm(x, act, w, ws, out, m, n, k, nullptr, s);
 }
 
 }  // namespace hq
@@ -348,7 +329,7 @@ extern "C" int hq_int4_i8_gemm(const int8_t* x, const float* act_scales, const u
     int8_t* q = reinterpret_cast<int8_t*>(ws + L.q_off);
     hipLaunchKernelGGL(batch_deinterleave_kernel, dim3(m), dim3(kBlock), 0, s, x, width, padded_k(width), q);
     if (hipGetLastError() != hipSuccess) return HQ_ERR_LAUNCH;
-    const hipError_t e = run_gemm(q, act_scales, weights, scales, output, m, rows, width, acc_out, ws, s);
+    const hipError_t e = run_gemm(q, act_scales, weights, scales, output, m, rows, width, acc_out, s);
     return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }
 
@@ -370,6 +351,6 @@ extern "C" int hq_quant_int4_gemm(const float* x, const uint8_t* weights, const 
     hipLaunchKernelGGL(batch_quant_kernel, dim3(m), dim3(kBlock), 0, s, x, width, padded_k(width), q, act,
                        q_out, act_scales_out);
     if (hipGetLastError() != hipSuccess) return HQ_ERR_LAUNCH;
-    const hipError_t e = run_gemm(q, act, weights, scales, output, m, rows, width, acc_out, ws, s);
+    const hipError_t e = run_gemm(q, act, weights, scales, output, m, rows, width, acc_out, s);
     return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }
