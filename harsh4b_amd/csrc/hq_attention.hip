@@ -450,8 +450,8 @@ int attention_splits(int context)
 template <int D, int GMAX, bool STEP>
 static hipError_t launch_attn(const AttnParams& a, hipStream_t s)
 {
-    const int splits = (a.max_chunks + kChunksPerBlock - 1) / kChunksPerBlock;
     const int batch = (!STEP && a.batch > 1) ? a.batch : 1;
+    const int splits = (a.max_chunks + kChunksPerBlock - 1) / kChunksPerBlock;
     hipLaunchKernelGGL((attention_kernel<D, GMAX, STEP, kChunksPerBlock>), dim3(a.kv_heads, splits, batch),
                        dim3(kBlock), 0, s, a);
     if (a.max_chunks > 1) {
