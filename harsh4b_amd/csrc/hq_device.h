@@ -169,36 +169,42 @@ __device__ __forceinline__ float wave_max64_all(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(unsigned, v), 0));
 }
 
+// Block barrier for LDS data only: the wave's LDS operations complete, then
+// s_barrier.  Unlike __syncthreads it does not wait for the wave's global
+// loads and stores, so weight loads issued before a block reduction keep
+// streaming through it.
+__device__ __forceinline__ void lds_sync()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Block-wide (256 threads) max of non-negative values; `red` is 4 floats of LDS.
 __device__ __forceinline__ float block_max_nonneg(float v, float* red)
 {
     v = wave_max64_all(v);
     const int wave = threadIdx.x / kWave;
     if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
-    __syncthreads();
+    lds_sync();
     const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
+    lds_sync();   // red may be written again after the return
     return r;
 }
 
 // Block-wide sum of 256 per-thread partials with the spec's halving tree
 // (partial i + partial i+o for o = 128, 64, ..., 1).  `red` is 256 floats of
-// LDS.  Levels 128 and 64 go through LDS, the last 64 lanes through the
-// wave tree.  Every thread returns the total.
+// LDS.  Every wave reads levels 128 and 64 of its lanes from LDS and runs
+// the wave tree over the remaining 64, so every thread returns the total
+// after one barrier.
 __device__ __forceinline__ float block_tree_sum256(float v, float* red)
 {
     const int t = threadIdx.x;
     red[t] = v;
-    __syncthreads();
-    if (t < 128) red[t] = red[t] + red[t + 128];
-    __syncthreads();
-    if (t < 64) {
-        const float r = wave_tree_sum64(red[t] + red[t + 64]);
-        if (t == 0) red[0] = r;
-    }
-    __syncthreads();
-    const float r = red[0];
-    __syncthreads();
+    lds_sync();
+    const int l = t & (kWave - 1);
+    const float r = wave_tree_sum64_all((red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]));
+    lds_sync();   // red may be written again after the return
     return r;
 }
 

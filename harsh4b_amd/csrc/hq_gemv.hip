@@ -173,9 +173,10 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     // of the activations: the HBM stream must start before any wait
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. activations -> LDS (overlaps the weight stream)
+    // 2. activations -> LDS (overlaps the weight stream: the barriers of the
+    // prologue wait for LDS only, not for the weight loads in flight)
     const float act = activation_prologue<XJ, PRO>(p, areg, xs, red);
-    __syncthreads();
+    lds_sync();
 
     float best_v = -__builtin_inff();   // EPI_ARGMAX: running best of this lane's rows
     int best_i = 0x7FFFFFFF;

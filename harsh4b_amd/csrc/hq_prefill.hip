@@ -76,15 +76,6 @@ struct RowParams {
     float* act;             // [batch]
 };
 
-// Block barrier for LDS data only: the wave's LDS operations complete, then
-// s_barrier (unlike __syncthreads it does not wait for global stores).
-__device__ __forceinline__ void lds_barrier()
-{
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 // One token (block) per row: the prologue of the step's GEMVs.  Thread t
 // holds elements t, t+THREADS, ... of the row in registers (NPT of them, all
 // loaded at once, the norm weights with them), so the row is read from
@@ -146,7 +137,7 @@ __global__ __launch_bounds__(THREADS) void prefill_rows_kernel(RowParams p)
             for (int j = 0; j < NPT; ++j)
                 if (tid + THREADS * j < k) ss = __builtin_fmaf(v[j], v[j], ss);
             red[tid] = ss;
-            lds_barrier();
+            lds_sync();
             const float r2 = (red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]);
             const float total = wave_tree_sum64_all(r2);
             const float r = __builtin_sqrtf(total / float(k) + p.eps);
@@ -166,7 +157,7 @@ __global__ __launch_bounds__(THREADS) void prefill_rows_kernel(RowParams p)
     for (int j = 0; j < NPT; ++j) amax = fmaxf(amax, fabsf(v[j]));   // 0 past k
     amax = wave_max64_all(amax);
     if (lane == 0) wmax[tid / kWave] = amax;
-    lds_barrier();
+    lds_sync();
     amax = wmax[0];
 #pragma unroll
     for (int w = 1; w < THREADS / kWave; ++w) amax = fmaxf(amax, wmax[w]);
