@@ -74,6 +74,12 @@ SEGMENTS = [
     (14, "end", "hand-off", "residual store -> next layer"),
 ]
 ATTENTION_POINTS = {25, 26, 27, 28, 29}
+# Past 256 positions the attention runs as GQA items and a combine spread
+# over every block, which record no points of their own: the segment from
+# the qkv rows to the attention output is then one "attention" segment.
+GQA_SEGMENTS = [s for s in SEGMENTS if s[0] not in (4, 25, 29)]
+GQA_SEGMENTS.insert(GQA_SEGMENTS.index((6, 7, "hand-off", "attention output: read + quant")),
+                    (4, 6, "attention", "attention phase: GQA items, hand-offs, combine"))
 CATEGORIES = ["body GEMV", "attention", "norm + quant", "hand-off", "sync"]
 
 
@@ -110,6 +116,7 @@ def part_trace(ctx, seed, reps=4):
     state.check_status()
     tr = traces[-1]
     has_att = (tr[:, 0, 25] != 0) & (tr[:, 0, 29] != 0)
+    segments = SEGMENTS if has_att.any() else GQA_SEGMENTS
     per_layer = []
     for L in range(TRACE_LAYERS - 1):
         rel = (tr[:, L, :] - tr[:, L, 0:1]) / 100.0            # 100 MHz clock -> us
@@ -120,7 +127,7 @@ def part_trace(ctx, seed, reps=4):
                 return float(np.median(end))
             col = rel[has_att, point] if point in ATTENTION_POINTS else rel[:, point]
             return float(np.median(col))
-        segs = [(a, b, cat, what, med(b) - med(a)) for a, b, cat, what in SEGMENTS]
+        segs = [(a, b, cat, what, med(b) - med(a)) for a, b, cat, what in segments]
         per_layer.append({"layer": TRACE_L0 + L, "us": float(np.median(end)), "segments": segs})
     return {"context": int(state.device_position.item()) + 1, "blocks": nb,
             "attention_blocks": int(has_att.sum()), "layers": per_layer}
