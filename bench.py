@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="CPU time of each decode baseline run (the GEMV runs take a quarter of it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--batch-sizes", default="8,16,32",
+                    help="batched: comma-separated M values; value is the largest M's rate")
     ap.add_argument("--no-configs", action="store_true",
                     help="decode: skip the configs[0]/[1]/[4] measurements folded into the line")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
@@ -418,7 +420,10 @@ def bench_batched(args):
     tok1 = steps / t1
     print(f"# batch 1 at context {ctx}: {tok1:.1f} tok/s", file=sys.stderr, flush=True)
     per_m = {}
-    for m in (8, 16, 32):
+    sizes = sorted({int(x) for x in args.batch_sizes.split(",") if x.strip()})
+    if not sizes or sizes[0] < 1:
+        raise SystemExit("--batch-sizes needs positive integers")
+    for m in sizes:
         states = []
         for i in range(m):
             st = model.new_state(cap)
@@ -440,16 +445,17 @@ def bench_batched(args):
               f"({ms / (1e3 / tok1):.2f}x the batch-1 step)", file=sys.stderr, flush=True)
         model._batch_graph = None
         del states
-    top = per_m[32]
-    result = {"metric": "batched greedy decode sequence-tokens/s (configs[3], M=32, context 256)",
+    top_m = sizes[-1]
+    top = per_m[top_m]
+    result = {"metric": f"batched greedy decode sequence-tokens/s (configs[3], M={top_m}, context {ctx})",
               "value": top["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
               "ms_per_step": top["ms_per_step"], "higher_is_better": True, "scaling": "weak",
               "vs_baseline": None, "dtype": "int8",
               "data": "synthetic: random-init int4 weights, random 256-token prompts (seeds 4+i)",
-              "config": {"workload": f"configs[3]: batched decode of M = 8/16/32 sequences at context {ctx}, "
-                                     "each with its own fp16 KV cache, greedy",
-                         "global_batch": 32, "seq_len": ctx, "parallelism": "none (1 GPU)"},
-              "roofline": {"kernel": "whole batched step (hq_decode_batch), M=32", "bound": "hbm",
+              "config": {"workload": f"configs[3]: batched decode of M = {'/'.join(map(str, sizes))} sequences "
+                                     f"at context {ctx}, each with its own fp16 KV cache, greedy",
+                         "global_batch": top_m, "seq_len": ctx, "parallelism": "none (1 GPU)"},
+              "roofline": {"kernel": f"whole batched step (hq_decode_batch), M={top_m}", "bound": "hbm",
                            "achieved": top["achieved_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": top["hbm_frac"], "traffic": None, "algorithmic_bytes": top["bytes_per_step"]},
               "batch1_tok_s": round(tok1, 1), "per_m": per_m}

@@ -154,6 +154,137 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
     }
 }
 
+// The same products with the weight rows staged through LDS, for rows of up
+// to HMAX packed bytes.  The block's R = 16 RG rows are one contiguous
+// R * K/2 byte range of the matrix; its threads read it in 16-byte chunks,
+// consecutive lanes taking consecutive chunks, so one wave instruction reads
+// 1 KB of contiguous memory (an MFMA-shaped load -- 16 rows x 64 bytes --
+// streams a 25 MB matrix in 7.2 us where contiguous 1 KB reads take 5.2 us).
+// The chunks go to LDS rows padded by 16 bytes: the 16 rows of an A operand
+// then start 4 banks apart, so the 16 lanes of a ds_read_b128 phase hit 64
+// distinct banks.  Each wave's activation (B) loads go out with the weight
+// loads; after one LDS barrier the wave runs the MFMAs of its double steps
+// with A from LDS, and the int32 partial tiles meet in the same LDS.
+// DS * W covers the double steps of any K up to 2 * HMAX (one round of B
+// loads per wave), CPT * W * 64 chunks cover the block's rows.
+template <int RG, int W, int BT, int DS, int CPT, int HMAX>
+__global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
+{
+    constexpr int R = 16 * RG;
+    constexpr int RS = HMAX + 16;                       // padded LDS row (bytes)
+    constexpr int NRED = RG * BT * 4;                   // partial registers per lane
+    static_assert(W * NRED * kWave * 4 <= R * RS, "the partial tiles alias the staged rows");
+    static_assert(CPT * kWave * W * 16 >= R * HMAX, "the chunks of a thread cover the block's rows");
+    static_assert(DS * W * 128 >= 2 * HMAX, "one round of B loads covers a wave's double steps");
+    __shared__ __align__(16) uint8_t a_s[R * RS];
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
+    const int q = lane >> 4;
+    const int r16 = lane & 15;
+    const int row0 = blockIdx.x * R;
+    const int half = p.k >> 1;                          // packed bytes per row (a multiple of 16)
+    const int cpr = half >> 4;                          // 16-byte chunks per row
+    const int total = min(R, p.n - row0) * cpr;         // chunks of the block's rows
+    const uint8_t* wb = p.w + size_t(row0) * size_t(half);
+    // Every load below is unconditional (clamped into range), so the
+    // compiler tracks them by count: the LDS stores wait for the weight
+    // chunks alone, and no branch splits the burst.  A chunk index past the
+    // block's rows re-reads (and re-stores, to the same place) the last one.
+    uint4 v[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = min(tid + kWave * W * j, total - 1);
+        v[j] = load16_nt(wb + size_t(c) * 16);
+    }
+    const int nds = (p.k + 127) >> 7;
+    const int ds0 = nds * wave / W, ds1 = nds * (wave + 1) / W;
+    uint4 xb[DS][BT][2];
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+        const int8_t* brow = p.x + size_t(min(16 * b + r16, p.m - 1)) * size_t(p.kp);
+#pragma unroll
+        for (int j = 0; j < DS; ++j) {
+            // columns 2pb .. 2pb + 32 of a double step inside the row (the
+            // MFMAs of the steps past the wave's range are skipped)
+            const int8_t* xp = brow + 2 * (min(ds0 + j, nds - 1) * 64 + 16 * q);
+            xb[j][b][0] = *reinterpret_cast<const uint4*>(xp);
+            xb[j][b][1] = *reinterpret_cast<const uint4*>(xp + 16);
+        }
+    }
+    // the epilogue's activation and row scales, fetched with the rest
+    constexpr int EPT = (R * 16 * BT + kWave * W - 1) / (kWave * W);
+    float act_e[EPT], ws_e[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + kWave * W * i;
+        act_e[i] = p.act[min(e / R, p.m - 1)];   // sequence e / R, row e % R
+        ws_e[i] = p.ws[min(row0 + e % R, p.n - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = min(tid + kWave * W * j, total - 1);
+        const int r = int(unsigned(c) / unsigned(cpr));
+        *reinterpret_cast<uint4*>(a_s + r * RS + (c - r * cpr) * 16) = v[j];
+    }
+    lds_sync();
+
+    i32x4 acc[RG][BT];
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int b = 0; b < BT; ++b) acc[rg][b] = i32x4{0, 0, 0, 0};
+    constexpr uint32_t m4 = 0xF0F0F0F0u;
+#pragma unroll
+    for (int j = 0; j < DS; ++j) {
+        const int pb = (ds0 + j) * 64 + 16 * q;        // this lane's 16 packed bytes of the row
+        if (ds0 + j < ds1) {
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                // past K the activations are zero, so the padding read there adds 0
+                const uint4 w = pb < half ? *reinterpret_cast<const uint4*>(a_s + (16 * rg + r16) * RS + pb)
+                                          : make_uint4(0, 0, 0, 0);
+                const i32x4 a0 = {int((w.x << 4) & m4), int(w.x & m4), int((w.y << 4) & m4), int(w.y & m4)};
+                const i32x4 a1 = {int((w.z << 4) & m4), int(w.z & m4), int((w.w << 4) & m4), int(w.w & m4)};
+#pragma unroll
+                for (int b = 0; b < BT; ++b) {
+                    const uint4 x0 = xb[j][b][0], x1 = xb[j][b][1];
+                    acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        a0, i32x4{int(x0.x), int(x0.y), int(x0.z), int(x0.w)}, acc[rg][b], 0, 0, 0);
+                    acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        a1, i32x4{int(x1.x), int(x1.y), int(x1.z), int(x1.w)}, acc[rg][b], 0, 0, 0);
+                }
+            }
+        }
+    }
+    lds_sync();   // every wave's A reads are done: the partials reuse the LDS
+    int32_t (*red)[NRED][kWave] = reinterpret_cast<int32_t (*)[NRED][kWave]>(a_s);
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+        for (int b = 0; b < BT; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][(rg * BT + b) * 4 + r][lane] = acc[rg][b][r];
+    lds_sync();
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + kWave * W * i;
+        if (e >= R * 16 * BT) break;
+        const int rl = e % R, ml = e / R;
+        const int rg = rl >> 4, rr = rl & 15, b = ml >> 4, col = ml & 15;
+        const int src = col + 16 * (rr >> 2), reg = (rg * BT + b) * 4 + (rr & 3);
+        int32_t sum = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < W; ++w2) sum += red[w2][reg][src];
+        const int mm = 16 * b + col, n = row0 + rl;
+        if (mm < p.m && n < p.n) {
+            const int a = sum >> 4;
+            p.out[size_t(mm) * p.n + n] = (float(a) * act_e[i]) * ws_e[i];
+            if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
+        }
+    }
+}
+
 // Per-sequence spec quantization: block m quantizes row m into q (row
 // stride kp, de-interleaved per 8 columns: the 4 even columns, then the 4
 // odd ones) and, when given, q_out (natural order).  Thread t handles the
@@ -251,9 +382,41 @@ static void launch_gemm(const GemmParams& p, hipStream_t s)
                        p);
 }
 
-// x: the de-interleaved padded activations.  Waves per block: the fewest of
-// 4, 8, 16 whose K ranges fit one round of loads; rows per block: 32 when
-// that still leaves 512 blocks or more (one sequence tile), else 16.
+template <int RG, int W, int BT, int HMAX>
+static void launch_gemm_lds(const GemmParams& p, hipStream_t s)
+{
+    constexpr int R = 16 * RG;
+    constexpr int DS = (2 * HMAX / 128 + W - 1) / W;
+    constexpr int CPT = (R * HMAX / 16 + kWave * W - 1) / (kWave * W);
+    hipLaunchKernelGGL((gemm_lds_kernel<RG, W, BT, DS, CPT, HMAX>), dim3((p.n + R - 1) / R), dim3(kWave * W), 0, s,
+                       p);
+}
+
+// Rows of up to 5120 packed bytes (K <= 10240) take the LDS-staged kernel:
+// 4 waves per block up to K = 2560, 8 up to 4096, 16 beyond; 32 rows per
+// block for one sequence tile over 2048 blocks or more (the LM head: 43.2
+// against 47.8 us at M = 8, where gate_up's 608 blocks of 32 rows took 11.2
+// against 10.4 us for 1216 of 16).
+template <int BT>
+static bool launch_staged(const GemmParams& p, bool two_groups, hipStream_t s)
+{
+    const int half = p.k >> 1;
+    if (half <= 1280) {
+        if (two_groups) launch_gemm_lds<2, 4, BT, 1280>(p, s);
+        else launch_gemm_lds<1, 4, BT, 1280>(p, s);
+    } else if (half <= 2048) {
+        launch_gemm_lds<1, 8, BT, 2048>(p, s);
+    } else if (half <= 5120) {
+        launch_gemm_lds<1, 16, BT, 5120>(p, s);
+    } else {
+        return false;
+    }
+    return true;
+}
+
+// x: the de-interleaved padded activations.  Wider rows: the kernel with
+// MFMA-shaped weight loads; waves per block: the fewest of 4, 8, 16 whose K
+// ranges fit one round of loads; 32 rows per block from 512 blocks up.
 static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, const float* ws,
                            float* out, int m, int n, int k, int32_t* acc_out, hipStream_t s)
 {
@@ -269,8 +432,10 @@ static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, 
         p.out = out + size_t(m0) * n;
         p.acc_out = acc_out ? acc_out + size_t(m0) * n : nullptr;
         p.n = n; p.k = k; p.kp = kp;
-        const bool two_groups = p.m <= 16 && (n + 31) / 32 >= 512;
-        if (p.m > 16) {
+        const bool two_groups = p.m <= 16 && (n + 31) / 32 >= ((k >> 1) <= 5120 ? 2048 : 512);
+        const bool staged = p.m > 16 ? launch_staged<2>(p, two_groups, s) : launch_staged<1>(p, two_groups, s);
+        if (staged) {
+        } else if (p.m > 16) {
             if (waves == 4) launch_gemm<1, 4, 2>(p, s);
             else if (waves == 8) launch_gemm<1, 8, 2>(p, s);
             else launch_gemm<1, 16, 2>(p, s);

@@ -329,8 +329,8 @@ def test_sample_logits_follows_the_generator():
 @pytest.mark.parametrize("m", [1, 8, 16, 32, 40])
 @pytest.mark.parametrize("rows,width", [(2560, 9728), (6144, 2560), (2560, 4096), (19456, 2560), (100, 96)])
 def test_batched_gemm_bit_exact(m, rows, width):
-    # Qwen3-4B's down, qkv, o (K split across blocks) and gate_up (unsplit,
-    # 304 row tiles) shapes, and a ragged one
+    # Qwen3-4B's down, qkv, o and gate_up shapes (rows staged through LDS)
+    # and a ragged one
     ls = lightspark()
     rng = np.random.default_rng(m * 31 + rows)
     w = random_int4(rng, rows, width)
@@ -356,3 +356,22 @@ def test_batched_gemm_bit_exact(m, rows, width):
     for i in (0, m - 1):
         one = ls.int4_i8_gemv(qo[i].contiguous(), p, float(to_host(ao)[i]))
         assert_bits_equal(to_host(one), ref_out[i], f"gemv row {i}")
+
+
+@pytest.mark.parametrize("m", [3, 17])
+def test_batched_gemm_wide_rows(m):
+    # rows wider than 10240 columns take the kernel with MFMA-shaped loads
+    ls = lightspark()
+    rng = np.random.default_rng(900 + m)
+    rows, width = 72, 10496
+    w = random_int4(rng, rows, width)
+    packed = oracle.pack_int4(w)
+    s = rng.uniform(0.005, 0.02, rows).astype(np.float32)
+    q = rng.integers(-127, 128, (m, width)).astype(np.int8)
+    a = rng.uniform(0.001, 0.01, m).astype(np.float32)
+    p = ls.LiteSparkProjection(to_dev(packed), to_dev(s))
+    acc = torch.empty((m, rows), dtype=torch.int32, device=dev())
+    out = ls.int4_i8_gemm(to_dev(q), to_dev(a), p, acc_out=acc)
+    assert_bits_equal(to_host(acc), oracle.int4_i8_gemm_acc(q, packed, rows, width), "wide acc")
+    ref = np.stack([oracle.int4_i8_gemv(q[i], packed, s, a[i], rows, width) for i in range(m)])
+    assert_bits_equal(to_host(out), ref, "wide out")
