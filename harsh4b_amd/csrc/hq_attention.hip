@@ -101,8 +101,11 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         pos = -1;
         n = a.context + int(blockIdx.z);     // query z of a batch sees z more positions
     }
-    const uint16_t* keys = a.keys;
-    const uint16_t* values = a.values;
+    uint16_t* keys = a.keys;
+    uint16_t* values = a.values;
+    const float* qkv = a.qkv;
+    bool rawq = STEP;     // q (and the current k/v) from the raw projection
+    bool kvnew = STEP;    // the current position's k/v written and used from LDS
     if (!STEP && a.table) {
         // batched decode: query z is sequence z at its own position, in its
         // own cache (its layer slab: capacity * kv_heads * D elements)
@@ -113,6 +116,15 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         const size_t slab = size_t(cap) * size_t(a.kv_heads) * size_t(D);
         keys = a.table->keys[z] + size_t(a.layer) * slab;
         values = a.table->values[z] + size_t(a.layer) * slab;
+        if (a.qkv) {
+            // a batched step: row z of the raw projection, RoPE at the
+            // (clamped) position; a position outside the cache (flagged by
+            // the embedding kernel) writes nothing and reads the cache as is
+            rawq = true;
+            kvnew = zpos >= 0 && zpos < cap;
+            pos = n - 1;
+            qkv = a.qkv + size_t(z) * size_t(a.kv_heads) * size_t(G + 2) * D;
+        }
     }
     // per-query regions of a batch (blockIdx.z = 0 outside PLAIN batches)
     const size_t zq = size_t(blockIdx.z) * size_t(a.kv_heads) * G * D;
@@ -124,7 +136,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     const int c_begin = split * CPB;
     const int c_end = min(nc, c_begin + CPB);
     const size_t kv_off = size_t(g) * D;
-    const int cur_chunk = STEP ? nc - 1 : -1;     // chunk holding the current position
+    const int cur_chunk = kvnew ? nc - 1 : -1;    // chunk holding the current position
 
     uint4 kreg[T::kPerThread], vreg[T::kPerThread];
     {
@@ -133,13 +145,15 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     }
     __builtin_amdgcn_sched_barrier(0);   // the chunk loads go out before the query prologue
 
-    // ---- query heads (and in STEP mode the current k/v) ---------------------
-    if constexpr (STEP) {
-        static_assert(D == 128, "STEP mode is written for head_dim 128");
+    // ---- query heads (and from the raw projection the current k/v) ---------
+    static_assert(!STEP || D == 128, "STEP mode is written for head_dim 128");
+    bool plain_q = true;
+    if constexpr (D == 128) if (rawq) {
+        plain_q = false;
         const float* cs = a.rope_cos + size_t(pos) * (D / 2);
         const float* sn = a.rope_sin + size_t(pos) * (D / 2);
         for (int h = wave; h < G; h += kBlock / kWave) {
-            const float* src = a.qkv + size_t(g * G + h) * D;
+            const float* src = qkv + size_t(g * G + h) * D;
             const float x0 = src[lane], x1 = src[lane + 64];
             float p = __builtin_fmaf(x0, x0, 0.0f);
             p = __builtin_fmaf(x1, x1, p);
@@ -151,12 +165,12 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
             q_s[h][lane] = y0 * c0 - y1 * s0;
             q_s[h][lane + 64] = y1 * c0 + y0 * s0;
         }
-        if (split == nsplit - 1) {
+        if (kvnew && split == nsplit - 1) {
             const int heads = a.kv_heads * G;
-            uint16_t* kdst = a.keys + size_t(pos) * a.time_stride + kv_off;
-            uint16_t* vdst = a.values + size_t(pos) * a.time_stride + kv_off;
+            uint16_t* kdst = keys + size_t(pos) * a.time_stride + kv_off;
+            uint16_t* vdst = values + size_t(pos) * a.time_stride + kv_off;
             if (wave == 0) {
-                const float* src = a.qkv + size_t(heads + g) * D;
+                const float* src = qkv + size_t(heads + g) * D;
                 const float x0 = src[lane], x1 = src[lane + 64];
                 float p = __builtin_fmaf(x0, x0, 0.0f);
                 p = __builtin_fmaf(x1, x1, p);
@@ -172,7 +186,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                 kc_s[lane] = h0;
                 kc_s[lane + 64] = h1;
             } else if (wave == 1) {
-                const float* src = a.qkv + size_t(heads + a.kv_heads + g) * D;
+                const float* src = qkv + size_t(heads + a.kv_heads + g) * D;
                 const uint16_t h0 = f32_to_f16(src[lane]);
                 const uint16_t h1 = f32_to_f16(src[lane + 64]);
                 vdst[lane] = h0;
@@ -181,9 +195,9 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                 vc_s[lane + 64] = h1;
             }
         }
-    } else {
-        for (int i = tid; i < G * D; i += kBlock) q_s[i / D][i % D] = a.q[zq + size_t(g * G) * D + i];
     }
+    if (plain_q)
+        for (int i = tid; i < G * D; i += kBlock) q_s[i / D][i % D] = a.q[zq + size_t(g * G) * D + i];
     __syncthreads();
 
     const int grp = tid >> 4;       // 16 lane groups for the scores
@@ -432,6 +446,164 @@ __global__ __launch_bounds__(kBlock) void attention_combine_kernel(AttnParams a)
     if (live) a.out[size_t(z) * size_t(heads) * D + size_t(hh) * D + d] = O * (1.0f / L);
 }
 
+// The batched step's attention epilogue: block z forms sequence z's output
+// row -- the chunk combine of attention_combine_kernel for every (head, dim),
+// same arithmetic, or the row attention_kernel combined in-block when the
+// context is one chunk -- and quantizes it as the row kernels do (the row's
+// maximum |value|, floored at 1e-5; quant_i8 with 127 / amax; columns
+// de-interleaved per 8), so the o projection reads it as its GEMM input.
+// Thread t holds (head t / D + HPP * i, dim t % D) for i < NO.
+constexpr int kCombineThreads = 1024;
+constexpr int kCombineMaxHeads = 64;
+constexpr int kCombineBatch = 64;      // chunks whose a_c, l_c are staged at once
+template <int D>
+__global__ __launch_bounds__(kCombineThreads) void batch_combine_quant_kernel(AttnParams a)
+{
+    constexpr int C = kAttnChunk;
+    constexpr int T = kCombineThreads;
+    constexpr int HPP = T / D;                         // heads per pass
+    constexpr int NO = kCombineMaxHeads / HPP;         // outputs per thread
+    constexpr int CB = kCombineBatch;
+    constexpr int pstride = D + 2;
+    __shared__ float mx_s[NO][T / kWave];
+    __shared__ float M_s[kCombineMaxHeads];
+    __shared__ float al_s[kCombineMaxHeads][CB];
+    __shared__ float l_s[kCombineMaxHeads][CB];
+    __shared__ float wred[T / kWave];
+    const int z = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
+    const int d = tid % D, h0 = tid / D;
+    const int H = a.kv_heads * a.groups;
+    const int cap = a.table->capacity[z];
+    const int n = min(max(*a.table->position[z], 0), cap - 1) + 1;
+    const int nc = (n + C - 1) / C;
+    float val[NO];
+    if (nc == 1) {
+        const float* row = a.out + size_t(z) * H * D;
+#pragma unroll
+        for (int i = 0; i < NO; ++i) {
+            const int hh = h0 + HPP * i;
+            val[i] = hh < H ? row[hh * D + d] : 0.0f;
+        }
+    } else {
+        const float* part = a.part + size_t(z) * H * size_t(a.max_chunks) * pstride;
+        static_assert(D % kWave == 0, "a head's threads are whole waves");
+        if (nc > CB) {
+            // M over every chunk first (several staged batches follow):
+            // thread d of a head takes chunks d, d + D, ...
+            float mm[NO];
+#pragma unroll
+            for (int i = 0; i < NO; ++i) mm[i] = -__builtin_inff();
+            for (int c = d; c < nc; c += D)
+#pragma unroll
+                for (int i = 0; i < NO; ++i)
+                    mm[i] = fmaxf(mm[i], part[(size_t(min(h0 + HPP * i, H - 1)) * a.max_chunks + c) * pstride]);
+#pragma unroll
+            for (int i = 0; i < NO; ++i) {
+                mm[i] = wave_max64_all(mm[i]);
+                if (lane == 0) mx_s[i][wave] = mm[i];
+            }
+            lds_sync();
+            if (d == 0) {
+#pragma unroll
+                for (int i = 0; i < NO; ++i) {
+                    const int hh = h0 + HPP * i;
+                    if (hh >= H) continue;
+                    float m2 = mx_s[i][h0 * (D / kWave)];
+                    for (int w = 1; w < D / kWave; ++w) m2 = fmaxf(m2, mx_s[i][h0 * (D / kWave) + w]);
+                    M_s[hh] = m2;
+                }
+            }
+        }
+        float L[NO], O[NO];
+#pragma unroll
+        for (int i = 0; i < NO; ++i) L[i] = O[i] = 0.0f;
+        for (int c0 = 0; c0 < nc; c0 += CB) {
+            const int nb = min(CB, nc - c0);
+            // the o values of the batch's first 8 chunks go out with its m, l
+            float ov[NO][8];
+#pragma unroll
+            for (int i = 0; i < NO; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    ov[i][j] = (h0 + HPP * i < H && j < nb)
+                                   ? part[(size_t(h0 + HPP * i) * a.max_chunks + c0 + j) * pstride + 2 + d]
+                                   : 0.0f;
+            lds_sync();   // M_s written / the previous batch's staged values read
+            for (int idx = tid; idx < H * nb; idx += T) {
+                const int hh = idx / nb, c = idx - hh * nb;
+                const float* pp = part + (size_t(hh) * a.max_chunks + c0 + c) * pstride;
+                al_s[hh][c] = pp[0];
+                l_s[hh][c] = pp[1];
+            }
+            lds_sync();
+            if (nc <= CB) {
+                for (int hh = tid; hh < H; hh += T) {
+                    float m2 = al_s[hh][0];
+                    for (int c = 1; c < nb; ++c) m2 = fmaxf(m2, al_s[hh][c]);
+                    M_s[hh] = m2;
+                }
+                lds_sync();
+            }
+            // a_c = exp(m_c - M) in place of m_c
+            for (int idx = tid; idx < H * nb; idx += T) {
+                const int hh = idx / nb, c = idx - hh * nb;
+                al_s[hh][c] = spec_expf(al_s[hh][c] - M_s[hh]);
+            }
+            lds_sync();
+            for (int c = 0; c < nb; c += 8) {
+                if (c > 0) {
+#pragma unroll
+                    for (int i = 0; i < NO; ++i)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            ov[i][j] = (h0 + HPP * i < H && c + j < nb)
+                                           ? part[(size_t(h0 + HPP * i) * a.max_chunks + c0 + c + j) * pstride + 2 + d]
+                                           : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < NO; ++i) {
+                    const int hh = h0 + HPP * i;
+                    if (hh >= H) continue;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        if (c + j < nb) {
+                            const float al = al_s[hh][c + j];
+                            L[i] = __builtin_fmaf(al, l_s[hh][c + j], L[i]);
+                            O[i] = __builtin_fmaf(al, ov[i][j], O[i]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NO; ++i) val[i] = h0 + HPP * i < H ? O[i] * (1.0f / L[i]) : 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NO; ++i) amax = fmaxf(amax, fabsf(val[i]));   // 0 past the heads
+    amax = wave_max64_all(amax);
+    if (lane == 0) wred[wave] = amax;
+    lds_sync();
+    amax = wred[0];
+#pragma unroll
+    for (int w = 1; w < T / kWave; ++w) amax = fmaxf(amax, wred[w]);
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+    int8_t* qr = a.q8 + size_t(z) * a.kp;
+#pragma unroll
+    for (int i = 0; i < NO; ++i) {
+        const int hh = h0 + HPP * i;
+        if (hh < H) {
+            const int e = hh * D + d;
+            qr[(e & ~7) + ((e & 1) ? 4 + ((e & 7) >> 1) : ((e & 7) >> 1))] = quant_i8(val[i], inv);
+        }
+    }
+    if (tid == 0) a.act[z] = amax / 127.0f;
+}
+
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim)
 {
     return size_t(heads) * size_t(max_chunks) * size_t(head_dim + 2);
@@ -460,6 +632,21 @@ static hipError_t launch_attn(const AttnParams& a, hipStream_t s)
         hipLaunchKernelGGL((attention_combine_kernel<D, STEP>), dim3((heads + hpb - 1) / hpb, batch), dim3(kBlock),
                            0, s, a);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
+{
+    if (a.head_dim != 128 || !a.table || !a.qkv || !a.q8 || !a.act || a.groups > 8 ||
+        a.kv_heads * a.groups > kCombineMaxHeads || a.batch < 1)
+        return hipErrorInvalidValue;
+    const int splits = (a.max_chunks + kChunksPerBlock - 1) / kChunksPerBlock;
+    const dim3 grid(a.kv_heads, splits, a.batch);
+    if (a.groups <= 4)
+        hipLaunchKernelGGL((attention_kernel<128, 4, false, kChunksPerBlock>), grid, dim3(kBlock), 0, s, a);
+    else
+        hipLaunchKernelGGL((attention_kernel<128, 8, false, kChunksPerBlock>), grid, dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(batch_combine_quant_kernel<128>, dim3(a.batch), dim3(kCombineThreads), 0, s, a);
     return hipGetLastError();
 }
 

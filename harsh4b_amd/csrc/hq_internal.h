@@ -86,12 +86,20 @@ struct AttnParams {
     float* out;                 // [heads, D]
     // PLAIN batches of a batched decode step (nullable): query z attends the
     // cache of sequence z (layer `layer`) up to its position, table->position[z]
-    // + 1 positions; keys, values and context above are then unused
+    // + 1 positions; keys, values and context above are then unused.  With
+    // qkv set as well, query z is computed from row z of the raw projection
+    // as in STEP mode (the current k/v go to sequence z's cache), and
+    // launch_batch_attention quantizes each output row into q8 (row stride
+    // kp, de-interleaved) with its scale in act[z].
     const BatchTable* table;
     int layer;
+    int8_t* q8;
+    float* act;
+    int kp;
 };
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);
+hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s);
 
 // ---- batched GEMM driver (hq_gemm.hip) ---------------------------------------
 // x: int8 activations de-interleaved per 8 columns (even columns, then odd),

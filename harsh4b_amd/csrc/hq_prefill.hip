@@ -280,6 +280,9 @@ static bool prefill_fits(const hq_model* m)
            m->hidden > 0 && m->intermediate > 0 && m->vocab > 0;
 }
 
+// The batched step's attention epilogue holds a row of up to 64 heads.
+static bool batch_fits(const hq_model* m) { return prefill_fits(m) && m->heads <= 64; }
+
 // The GEMM reads row m of its activations at m * gemm_padded_k(width): the
 // row stride follows each projection's own width.  Rows of up to 2560, 4096
 // and 10240 values take 10, 16 and 40 registers per thread.
@@ -351,57 +354,6 @@ __global__ __launch_bounds__(kBlock) void batch_embed_kernel(const uint8_t* emb,
         const int hi = int(int8_t(b)) >> 4;
         xr[2 * j] = float(lo) * s;
         xr[2 * j + 1] = float(hi) * s;
-    }
-}
-
-// prefill_qk_kernel for the batch: token m is sequence m at its own position,
-// its K/V rows go to its own cache (layer `layer`); a position outside the
-// cache (flagged by the embedding kernel) writes nothing.
-__global__ __launch_bounds__(kBlock) void batch_qk_kernel(QkParams p, const BatchTable* T, int layer)
-{
-    constexpr int D = 128;
-    const int m = blockIdx.x;
-    const int slot = blockIdx.y * (kBlock / kWave) + threadIdx.x / kWave;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int total = p.heads + 2 * p.kv_heads;
-    if (slot >= total) return;
-    const int cap = T->capacity[m];
-    const int raw = *T->position[m];
-    const bool inside = raw >= 0 && raw < cap;
-    const int pos = min(max(raw, 0), cap - 1);
-    const size_t slab = size_t(cap) * size_t(p.kv_heads) * D;
-    uint16_t* keys = T->keys[m] + size_t(layer) * slab;
-    uint16_t* values = T->values[m] + size_t(layer) * slab;
-    const float* src = p.qkv + size_t(m) * total * D + size_t(slot) * D;
-    const float x0 = src[lane], x1 = src[lane + 64];
-    if (slot >= p.heads + p.kv_heads) {
-        if (inside) {
-            uint16_t* vdst = values + size_t(pos) * p.time_stride + size_t(slot - p.heads - p.kv_heads) * D;
-            vdst[lane] = f32_to_f16(x0);
-            vdst[lane + 64] = f32_to_f16(x1);
-        }
-        return;
-    }
-    const bool is_q = slot < p.heads;
-    const float* w = is_q ? p.q_norm : p.k_norm;
-    float s = __builtin_fmaf(x0, x0, 0.0f);
-    s = __builtin_fmaf(x1, x1, s);
-    const float ss = wave_tree_sum64_all(s);
-    const float r = __builtin_sqrtf(ss / float(D) + p.eps);
-    const float y0 = (x0 / r) * w[lane];
-    const float y1 = (x1 / r) * w[lane + 64];
-    const float c0 = p.rope_cos[size_t(pos) * (D / 2) + lane];
-    const float s0 = p.rope_sin[size_t(pos) * (D / 2) + lane];
-    const float a = y0 * c0 - y1 * s0;
-    const float b = y1 * c0 + y0 * s0;
-    if (is_q) {
-        float* qd = p.q + size_t(m) * p.heads * D + size_t(slot) * D;
-        qd[lane] = a;
-        qd[lane + 64] = b;
-    } else if (inside) {
-        uint16_t* kdst = keys + size_t(pos) * p.time_stride + size_t(slot - p.heads) * D;
-        kdst[lane] = f32_to_f16(a);
-        kdst[lane + 64] = f32_to_f16(b);
     }
 }
 
@@ -483,7 +435,7 @@ __global__ __launch_bounds__(kBlock) void batch_store_x_kernel(const float* x, i
 }
 
 struct BatchLayout {
-    size_t x, q8, act, qkv, qh, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, table,
+    size_t x, q8, act, qkv, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, table,
         total;
     int kp, max_chunks, qkv_rows, qd, arg_blocks;
 };
@@ -506,7 +458,6 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.q8 = take(size_t(gemm_padded_m(B)) * L.kp);
     L.act = take(size_t(B) * 4);
     L.qkv = take(size_t(B) * L.qkv_rows * 4);
-    L.qh = take(size_t(B) * L.qd * 4);
     L.att = take(size_t(B) * L.qd * 4);
     L.proj = take(size_t(B) * H * 4);
     L.gu = take(size_t(B) * 2 * I * 4);
@@ -642,14 +593,14 @@ extern "C" int hq_prefill(const hq_model* m, const hq_state* st, const int32_t* 
 
 extern "C" size_t hq_decode_batch_workspace_bytes(const hq_model* model, int max_capacity)
 {
-    if (!prefill_fits(model) || max_capacity <= 0) return 0;
+    if (!batch_fits(model) || max_capacity <= 0) return 0;
     return batch_layout(model, max_capacity).total;
 }
 
 extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int count, int max_capacity,
                                void* workspace, void* stream)
 {
-    if (!prefill_fits(m) || !states || !workspace || count < 1 || count > kMaxDecodeBatch || max_capacity <= 0)
+    if (!batch_fits(m) || !states || !workspace || count < 1 || count > kMaxDecodeBatch || max_capacity <= 0)
         return HQ_ERR_ARG;
     if (reinterpret_cast<uintptr_t>(workspace) & 255u) return HQ_ERR_ALIGN;
     if (!m->embedding || !m->embedding_scales || !m->final_norm || !m->rope_cos || !m->rope_sin) return HQ_ERR_ARG;
@@ -678,7 +629,6 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
     int8_t* q8 = reinterpret_cast<int8_t*>(ws + L.q8);
     float* act = reinterpret_cast<float*>(ws + L.act);
     float* qkv = reinterpret_cast<float*>(ws + L.qkv);
-    float* qh = reinterpret_cast<float*>(ws + L.qh);
     float* att = reinterpret_cast<float*>(ws + L.att);
     float* proj = reinterpret_cast<float*>(ws + L.proj);
     float* gu = reinterpret_cast<float*>(ws + L.gu);
@@ -687,7 +637,6 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
     BatchTable* table = reinterpret_cast<BatchTable*>(ws + L.table);
     const int H = m->hidden, I = m->intermediate, D = m->head_dim, KV = m->kv_heads, M = count;
     const long long time_stride = (long long)KV * D;
-    const int slots = (m->heads + 2 * KV + kBlock / kWave - 1) / (kBlock / kWave);
     auto ok = [] { return hipGetLastError() == hipSuccess; };
     hipLaunchKernelGGL(batch_table_kernel, dim3(1), dim3(kBlock), 0, s, t, table);
     hipLaunchKernelGGL(batch_embed_kernel, dim3(M), dim3(kBlock), 0, s, m->embedding, m->embedding_scales, m->vocab,
@@ -708,23 +657,16 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         if ((e = run_rows(l == 0 ? ROW_NORM : ROW_RESID_NORM, rp, M, s))) return e;
         if (gemm_run(q8, act, Ly.qkv, Ly.qkv_scales, qkv, M, L.qkv_rows, H, gemm, s) != hipSuccess)
             return HQ_ERR_LAUNCH;
-        QkParams qp{};
-        qp.qkv = qkv;
-        qp.q_norm = Ly.q_norm;
-        qp.k_norm = Ly.k_norm;
-        qp.rope_cos = m->rope_cos;
-        qp.rope_sin = m->rope_sin;
-        qp.eps = m->eps;
-        qp.heads = m->heads;
-        qp.kv_heads = KV;
-        qp.time_stride = time_stride;
-        qp.q = qh;
-        hipLaunchKernelGGL(batch_qk_kernel, dim3(M, slots), dim3(kBlock), 0, s, qp, (const BatchTable*)table, l);
-        if (!ok()) return HQ_ERR_LAUNCH;
+        // q/k head norms, RoPE and the K/V write of each sequence inside the
+        // attention kernel; its output rows combined and quantized for o
         AttnParams a{};
-        a.q = qh;
+        a.qkv = qkv;
+        a.q_norm = Ly.q_norm;
+        a.k_norm = Ly.k_norm;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        a.eps = m->eps;
         a.time_stride = time_stride;
-        a.context = 1;
         a.batch = M;
         a.kv_heads = KV;
         a.groups = m->heads / KV;
@@ -734,13 +676,11 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         a.out = att;
         a.table = table;
         a.layer = l;
-        if (launch_attention(a, false, s) != hipSuccess) return HQ_ERR_LAUNCH;
-        rp.x = att;
-        rp.add = nullptr;
-        rp.gamma = nullptr;
-        rp.k = m->heads * D;
-        if ((e = run_rows(ROW_PLAIN, rp, M, s))) return e;
-        if (gemm_run(q8, act, Ly.o, Ly.o_scales, proj, M, H, rp.k, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        a.q8 = q8;
+        a.act = act;
+        a.kp = gemm_padded_k(L.qd);
+        if (launch_batch_attention(a, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        if (gemm_run(q8, act, Ly.o, Ly.o_scales, proj, M, H, L.qd, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
         rp.x = x;
         rp.add = proj;
         rp.gamma = Ly.post_norm;
