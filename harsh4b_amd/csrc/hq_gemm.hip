@@ -394,15 +394,17 @@ static void launch_gemm_lds(const GemmParams& p, hipStream_t s)
 
 // Rows of up to 5120 packed bytes (K <= 10240) take the LDS-staged kernel:
 // 4 waves per block up to K = 2560, 8 up to 4096, 16 beyond; 32 rows per
-// block for one sequence tile over 2048 blocks or more (the LM head: 43.2
-// against 47.8 us at M = 8, where gate_up's 608 blocks of 32 rows took 11.2
-// against 10.4 us for 1216 of 16).
+// block up to K = 2560 for two sequence tiles, and for one over 2048 blocks
+// or more (the LM head: 43.2 against 47.8 us at M = 8, where gate_up's 608
+// blocks of 32 rows took 11.2 against 10.4 us for 1216 of 16).
 template <int BT>
 static bool launch_staged(const GemmParams& p, bool two_groups, hipStream_t s)
 {
     const int half = p.k >> 1;
     if (half <= 1280) {
-        if (two_groups) launch_gemm_lds<2, 4, BT, 1280>(p, s);
+        // two sequence tiles share each weight row over 32 rows (M = 32:
+        // gate_up 18.8 -> 16.9 us, the LM head 106.8 -> 81.7 us)
+        if (two_groups || BT == 2) launch_gemm_lds<2, 4, BT, 1280>(p, s);
         else launch_gemm_lds<1, 4, BT, 1280>(p, s);
     } else if (half <= 2048) {
         launch_gemm_lds<1, 8, BT, 2048>(p, s);
