@@ -448,8 +448,8 @@ __global__ __launch_bounds__(kBlock) void attention_combine_kernel(AttnParams a)
 
 // The batched step's attention epilogue: block z forms sequence z's output
 // row -- the chunk combine of attention_combine_kernel for every (head, dim),
-// same arithmetic, or the row attention_kernel combined in-block when the
-// context is one chunk -- and quantizes it as the row kernels do (the row's
+// same arithmetic, or the row attention_kernel combined in-block when one
+// block held the whole context -- and quantizes it as the row kernels do (the row's
 // maximum |value|, floored at 1e-5; quant_i8 with 127 / amax; columns
 // de-interleaved per 8), so the o projection reads it as its GEMM input.
 // Thread t holds (head t / D + HPP * i, dim t % D) for i < NO.
@@ -480,7 +480,8 @@ __global__ __launch_bounds__(kCombineThreads) void batch_combine_quant_kernel(At
     const int n = min(max(*a.table->position[z], 0), cap - 1) + 1;
     const int nc = (n + C - 1) / C;
     float val[NO];
-    if (nc == 1) {
+    if (nc <= a.cpb) {
+        // one block held every chunk of each head and combined them itself
         const float* row = a.out + size_t(z) * H * D;
 #pragma unroll
         for (int i = 0; i < NO; ++i) {
@@ -640,13 +641,19 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
     if (a.head_dim != 128 || !a.table || !a.qkv || !a.q8 || !a.act || a.groups > 8 ||
         a.kv_heads * a.groups > kCombineMaxHeads || a.batch < 1)
         return hipErrorInvalidValue;
-    const int splits = (a.max_chunks + kChunksPerBlock - 1) / kChunksPerBlock;
-    const dim3 grid(a.kv_heads, splits, a.batch);
-    if (a.groups <= 4)
-        hipLaunchKernelGGL((attention_kernel<128, 4, false, kChunksPerBlock>), grid, dim3(kBlock), 0, s, a);
-    else
-        hipLaunchKernelGGL((attention_kernel<128, 8, false, kChunksPerBlock>), grid, dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(batch_combine_quant_kernel<128>, dim3(a.batch), dim3(kCombineThreads), 0, s, a);
+    // one chunk per block while the grid fits about one round of the chip
+    // (four 256-thread blocks per CU), else two
+    AttnParams b = a;
+    b.cpb = a.kv_heads * a.max_chunks * a.batch <= 1024 ? 1 : 2;
+    const dim3 grid(a.kv_heads, (a.max_chunks + b.cpb - 1) / b.cpb, a.batch);
+    if (b.cpb == 1) {
+        if (a.groups <= 4) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1>), grid, dim3(kBlock), 0, s, b);
+        else hipLaunchKernelGGL((attention_kernel<128, 8, false, 1>), grid, dim3(kBlock), 0, s, b);
+    } else {
+        if (a.groups <= 4) hipLaunchKernelGGL((attention_kernel<128, 4, false, 2>), grid, dim3(kBlock), 0, s, b);
+        else hipLaunchKernelGGL((attention_kernel<128, 8, false, 2>), grid, dim3(kBlock), 0, s, b);
+    }
+    hipLaunchKernelGGL(batch_combine_quant_kernel<128>, dim3(a.batch), dim3(kCombineThreads), 0, s, b);
     return hipGetLastError();
 }
 

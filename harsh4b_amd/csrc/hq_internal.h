@@ -96,6 +96,7 @@ struct AttnParams {
     int8_t* q8;
     float* act;
     int kp;
+    int cpb;                    // chunks per attention block (set by launch_batch_attention)
 };
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);
