@@ -48,6 +48,10 @@ struct GemmParams {
     float* out;               // [m, N]
     int32_t* acc_out;         // nullable [m, N]
     int m, n, k, kp;          // kp: padded row stride of x (a multiple of kSlice)
+    // SwiGLU launches (gemm_lds_kernel<2, ..., true>): w holds gate rows
+    // [0, n) then up rows [n, 2n); out [m, n] receives SwiGLU(gate, up) and
+    // pmax [blocks, m] each block's maximum |out| per sequence
+    float* pmax;
 };
 
 // De-interleave 8 int8 columns (a, b = the two little-endian dwords) into
@@ -167,9 +171,10 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
 // with A from LDS, and the int32 partial tiles meet in the same LDS.
 // DS * W covers the double steps of any K up to 2 * HMAX (one round of B
 // loads per wave), CPT * W * 64 chunks cover the block's rows.
-template <int RG, int W, int BT, int DS, int CPT, int HMAX>
+template <int RG, int W, int BT, int DS, int CPT, int HMAX, bool SWIGLU = false>
 __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
 {
+    static_assert(!SWIGLU || RG == 2, "a SwiGLU block pairs 16 gate rows with their 16 up rows");
     constexpr int R = 16 * RG;
     constexpr int RS = HMAX + 16;                       // padded LDS row (bytes)
     constexpr int NRED = RG * BT * 4;                   // partial registers per lane
@@ -185,18 +190,28 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
     const int row0 = blockIdx.x * R;
     const int half = p.k >> 1;                          // packed bytes per row (a multiple of 16)
     const int cpr = half >> 4;                          // 16-byte chunks per row
-    const int total = min(R, p.n - row0) * cpr;         // chunks of the block's rows
-    const uint8_t* wb = p.w + size_t(row0) * size_t(half);
     // Every load below is unconditional (clamped into range), so the
     // compiler tracks them by count: the LDS stores wait for the weight
     // chunks alone, and no branch splits the burst.  A chunk index past the
     // block's rows re-reads (and re-stores, to the same place) the last one.
+    // SwiGLU: LDS rows 0-15 are gate rows 16b.., 16-31 the up rows n + 16b..
+    // (two contiguous ranges); a row past n re-reads the last valid one.
+    const int g0 = blockIdx.x * 16;
+    const int ng = min(16, p.n - g0);                   // SwiGLU: valid rows per range
+    const int total = SWIGLU ? R * cpr : min(R, p.n - row0) * cpr;
+    const uint8_t* wb = p.w + size_t(row0) * size_t(half);
+    auto chunk_addr = [&](int c) {
+        if constexpr (SWIGLU) {
+            const int r = int(unsigned(c) / unsigned(cpr));
+            const int row = (r >= 16 ? p.n : 0) + g0 + min(r & 15, ng - 1);
+            return p.w + size_t(row) * size_t(half) + size_t(c - r * cpr) * 16;
+        } else {
+            return wb + size_t(c) * 16;
+        }
+    };
     uint4 v[CPT];
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int c = min(tid + kWave * W * j, total - 1);
-        v[j] = load16_nt(wb + size_t(c) * 16);
-    }
+    for (int j = 0; j < CPT; ++j) v[j] = load16_nt(chunk_addr(min(tid + kWave * W * j, total - 1)));
     const int nds = (p.k + 127) >> 7;
     const int ds0 = nds * wave / W, ds1 = nds * (wave + 1) / W;
     uint4 xb[DS][BT][2];
@@ -213,13 +228,22 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
         }
     }
     // the epilogue's activation and row scales, fetched with the rest
-    constexpr int EPT = (R * 16 * BT + kWave * W - 1) / (kWave * W);
-    float act_e[EPT], ws_e[EPT];
+    // (SwiGLU: element e = sequence e / 16, column e % 16 of the gate and up
+    // tiles; the up row's scale in wu_e)
+    constexpr int NE = SWIGLU ? 16 * 16 * BT : R * 16 * BT;
+    constexpr int ER = SWIGLU ? 16 : R;
+    constexpr int EPT = (NE + kWave * W - 1) / (kWave * W);
+    float act_e[EPT], ws_e[EPT], wu_e[SWIGLU ? EPT : 1];
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const int e = tid + kWave * W * i;
-        act_e[i] = p.act[min(e / R, p.m - 1)];   // sequence e / R, row e % R
-        ws_e[i] = p.ws[min(row0 + e % R, p.n - 1)];
+        act_e[i] = p.act[min(e / ER, p.m - 1)];   // sequence e / ER, row e % ER
+        if constexpr (SWIGLU) {
+            ws_e[i] = p.ws[g0 + min(e % 16, ng - 1)];
+            wu_e[i] = p.ws[p.n + g0 + min(e % 16, ng - 1)];
+        } else {
+            ws_e[i] = p.ws[min(row0 + e % R, p.n - 1)];
+        }
     }
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
@@ -266,23 +290,93 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][(rg * BT + b) * 4 + r][lane] = acc[rg][b][r];
     lds_sync();
+    if constexpr (SWIGLU) {
+        // element e: sequence e / 16, column e % 16 of the gate and up tiles;
+        // the 16 columns of a sequence sit in one 16-lane row of a wave
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const int e = tid + kWave * W * i;
-        if (e >= R * 16 * BT) break;
-        const int rl = e % R, ml = e / R;
-        const int rg = rl >> 4, rr = rl & 15, b = ml >> 4, col = ml & 15;
-        const int src = col + 16 * (rr >> 2), reg = (rg * BT + b) * 4 + (rr & 3);
-        int32_t sum = 0;
+        for (int i = 0; i < EPT; ++i) {
+            const int e = tid + kWave * W * i;
+            if (e >= NE) break;
+            const int rr = e & 15, ml = e >> 4;
+            const int b = ml >> 4, col = ml & 15;
+            const int src = col + 16 * (rr >> 2);
+            const int regg = b * 4 + (rr & 3), regu = (BT + b) * 4 + (rr & 3);
+            int32_t sg = 0, su = 0;
 #pragma unroll
-        for (int w2 = 0; w2 < W; ++w2) sum += red[w2][reg][src];
-        const int mm = 16 * b + col, n = row0 + rl;
-        if (mm < p.m && n < p.n) {
-            const int a = sum >> 4;
-            p.out[size_t(mm) * p.n + n] = (float(a) * act_e[i]) * ws_e[i];
-            if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
+            for (int w2 = 0; w2 < W; ++w2) {
+                sg += red[w2][regg][src];
+                su += red[w2][regu][src];
+            }
+            const float g = (float(sg >> 4) * act_e[i]) * ws_e[i];
+            const float u = (float(su >> 4) * act_e[i]) * wu_e[i];
+            const float t = 1.0f + spec_expf(-g);
+            const float v = (g / t) * u;
+            const bool ok = ml < p.m && rr < ng;
+            if (ok) p.out[size_t(ml) * p.n + g0 + rr] = v;
+            float mx = ok ? fabsf(v) : 0.0f;
+#pragma unroll
+            for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+            if (rr == 0 && ml < p.m) p.pmax[size_t(blockIdx.x) * p.m + ml] = mx;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const int e = tid + kWave * W * i;
+            if (e >= NE) break;
+            const int rl = e % R, ml = e / R;
+            const int rg = rl >> 4, rr = rl & 15, b = ml >> 4, col = ml & 15;
+            const int src = col + 16 * (rr >> 2), reg = (rg * BT + b) * 4 + (rr & 3);
+            int32_t sum = 0;
+#pragma unroll
+            for (int w2 = 0; w2 < W; ++w2) sum += red[w2][reg][src];
+            const int mm = 16 * b + col, n = row0 + rl;
+            if (mm < p.m && n < p.n) {
+                const int a = sum >> 4;
+                p.out[size_t(mm) * p.n + n] = (float(a) * act_e[i]) * ws_e[i];
+                if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
+            }
         }
     }
+}
+
+// The batched step's down input: block m (1024 threads) takes sequence m's
+// SwiGLU row (gemm_lds_kernel's SwiGLU output), its maximum |value| from the
+// GEMM blocks' partial maxima (order-free), and quantizes it as the SwiGLU
+// row kernel does (amax floored at 1e-5, quant_i8 with 127 / amax, columns
+// de-interleaved per 8, row stride kp), with amax / 127 in act[m].
+constexpr int kActQuantThreads = 1024;
+constexpr int kActQuantNPT = 10;     // rows of up to 10240 values
+__global__ __launch_bounds__(kActQuantThreads) void batch_act_quant_kernel(const float* a, const float* pmax,
+                                                                            int nblocks, int m_count, int n, int kp,
+                                                                            int8_t* q, float* act)
+{
+    __shared__ float wred[kActQuantThreads / kWave];
+    const int m = blockIdx.x;
+    const int t = threadIdx.x;
+    const float* row = a + size_t(m) * n;
+    float v[kActQuantNPT];
+#pragma unroll
+    for (int j = 0; j < kActQuantNPT; ++j) {
+        const int i = t + kActQuantThreads * j;
+        v[j] = i < n ? row[i] : 0.0f;
+    }
+    float mx = 0.0f;
+    for (int b = t; b < nblocks; b += kActQuantThreads) mx = fmaxf(mx, pmax[size_t(b) * m_count + m]);
+    mx = wave_max64_all(mx);
+    if ((t & (kWave - 1)) == 0) wred[t / kWave] = mx;
+    lds_sync();
+    float amax = wred[0];
+#pragma unroll
+    for (int w = 1; w < kActQuantThreads / kWave; ++w) amax = fmaxf(amax, wred[w]);
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+    int8_t* qr = q + size_t(m) * kp;
+#pragma unroll
+    for (int j = 0; j < kActQuantNPT; ++j) {
+        const int i = t + kActQuantThreads * j;
+        if (i < n) qr[(i & ~7) + ((i & 1) ? 4 + ((i & 7) >> 1) : ((i & 7) >> 1))] = quant_i8(v[j], inv);
+    }
+    if (t == 0) act[m] = amax / 127.0f;
 }
 
 // Per-sequence spec quantization: block m quantizes row m into q (row
@@ -457,6 +551,44 @@ static hipError_t run_gemm(const int8_t* x, const float* act, const uint8_t* w, 
 }
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int W, int BT, int HMAX>
+static void launch_swiglu(const GemmParams& p, hipStream_t s)
+{
+    constexpr int DS = (2 * HMAX / 128 + W - 1) / W;
+    constexpr int CPT = (32 * HMAX / 16 + kWave * W - 1) / (kWave * W);
+    hipLaunchKernelGGL((gemm_lds_kernel<2, W, BT, DS, CPT, HMAX, true>), dim3((p.n + 15) / 16), dim3(kWave * W), 0,
+                       s, p);
+}
+
+int gemm_swiglu_blocks(int n) { return (n + 15) / 16; }
+
+// gate_up with SwiGLU in the GEMM epilogue, then the down input's
+// quantization: act_out [m, n] fp32, q [m, kq] int8 + act [m].
+hipError_t gemm_run_swiglu(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* act_out,
+                           int m, int n, int k, float* pmax, int8_t* q, int kq, float* act_q, hipStream_t s)
+{
+    if (m < 1 || m > kMaxBatch || (k >> 1) > 2048 || n > kActQuantThreads * kActQuantNPT || !pmax)
+        return hipErrorInvalidValue;
+    GemmParams p{};
+    p.m = m;
+    p.x = x;
+    p.act = act;
+    p.w = w; p.ws = ws;
+    p.out = act_out;
+    p.n = n; p.k = k; p.kp = padded_k(k);
+    p.pmax = pmax;
+    if ((k >> 1) <= 1280) {
+        if (m > 16) launch_swiglu<4, 2, 1280>(p, s);
+        else launch_swiglu<4, 1, 1280>(p, s);
+    } else {
+        if (m > 16) launch_swiglu<8, 2, 2048>(p, s);
+        else launch_swiglu<8, 1, 2048>(p, s);
+    }
+    hipLaunchKernelGGL(batch_act_quant_kernel, dim3(m), dim3(kActQuantThreads), 0, s, act_out, pmax,
+                       gemm_swiglu_blocks(n), m, n, kq, q, act_q);
+    return hipGetLastError();
+}
 
 int gemm_padded_k(int k) { return padded_k(k); }
 int gemm_padded_m(int m) { return padded_m(m); }

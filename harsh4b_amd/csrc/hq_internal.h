@@ -110,6 +110,13 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s);
 int gemm_padded_k(int k);
 int gemm_padded_m(int m);
 size_t gemm_scratch_bytes(int m, int n, int k);
+// gate_up (w: gate rows [0, n), up rows [n, 2n)) with SwiGLU in the GEMM
+// epilogue into act_out [m, n], then its quantization for the down GEMM into
+// q [m, kq] (de-interleaved) and act_q [m], as the SwiGLU row kernel makes
+// them.  pmax: gemm_swiglu_blocks(n) * m floats.
+hipError_t gemm_run_swiglu(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* act_out,
+                           int m, int n, int k, float* pmax, int8_t* q, int kq, float* act_q, hipStream_t s);
+int gemm_swiglu_blocks(int n);
 hipError_t gemm_run(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* out, int m, int n,
                     int k, char* scratch, hipStream_t s);
 hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s);

@@ -280,8 +280,9 @@ static bool prefill_fits(const hq_model* m)
            m->hidden > 0 && m->intermediate > 0 && m->vocab > 0;
 }
 
-// The batched step's attention epilogue holds a row of up to 64 heads.
-static bool batch_fits(const hq_model* m) { return prefill_fits(m) && m->heads <= 64; }
+// The batched step's attention epilogue holds a row of up to 64 heads; its
+// gate_up GEMM with the SwiGLU epilogue takes rows of up to 4096 columns.
+static bool batch_fits(const hq_model* m) { return prefill_fits(m) && m->heads <= 64 && m->hidden <= 4096; }
 
 // The GEMM reads row m of its activations at m * gemm_padded_k(width): the
 // row stride follows each projection's own width.  Rows of up to 2560, 4096
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(kBlock) void batch_store_x_kernel(const float* x, i
 }
 
 struct BatchLayout {
-    size_t x, q8, act, qkv, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, table,
+    size_t x, q8, act, qkv, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, pmax, table,
         total;
     int kp, max_chunks, qkv_rows, qd, arg_blocks;
 };
@@ -472,6 +473,7 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.pval = take(size_t(B) * L.arg_blocks * 4);
     L.pidx = take(size_t(B) * L.arg_blocks * 4);
     L.tickets = take(size_t(B) * ticket_words(L.arg_blocks) * 4);
+    L.pmax = take(size_t(gemm_swiglu_blocks(I)) * B * 4);
     L.table = take(sizeof(BatchTable));
     L.total = off;
     return L;
@@ -686,14 +688,10 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         rp.gamma = Ly.post_norm;
         rp.k = H;
         if ((e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
-        if (gemm_run(q8, act, Ly.gate_up, Ly.gate_up_scales, gu, M, 2 * I, H, gemm, s) != hipSuccess)
+        // gate_up with SwiGLU in its epilogue, then the down input's quant
+        if (gemm_run_swiglu(q8, act, Ly.gate_up, Ly.gate_up_scales, gu, M, I, H, reinterpret_cast<float*>(ws + L.pmax),
+                            q8, gemm_padded_k(I), act, s) != hipSuccess)
             return HQ_ERR_LAUNCH;
-        rp.x = nullptr;
-        rp.add = nullptr;
-        rp.gate_up = gu;
-        rp.gamma = nullptr;
-        rp.k = I;
-        if ((e = run_rows(ROW_SWIGLU, rp, M, s))) return e;
         if (gemm_run(q8, act, Ly.down, Ly.down_scales, proj, M, H, I, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
     }
     // the last layer's down output into the residual, final RMSNorm, tied LM

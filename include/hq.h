@@ -266,8 +266,9 @@ int hq_prefill(const hq_model* model, const hq_state* state, const int32_t* toke
  * model, max_capacity) bytes, 256-byte aligned, zero-filled before first use
  * (its counters are left at zero by every call).  A full cache sets
  * HQ_STEP_FULL and a bad token HQ_STEP_BAD_TOKEN in that state's status.
- * Shapes: those hq_prefill takes, with at most 64 query heads (the workspace
- * size is 0 and the call HQ_ERR_ARG otherwise). */
+ * Shapes: those hq_prefill takes, with at most 64 query heads and a hidden
+ * size of at most 4096 (the workspace size is 0 and the call HQ_ERR_ARG
+ * otherwise). */
 size_t hq_decode_batch_workspace_bytes(const hq_model* model, int max_capacity);
 int hq_decode_batch(const hq_model* model, const hq_state* states, int count, int max_capacity,
                     void* workspace, void* stream);
