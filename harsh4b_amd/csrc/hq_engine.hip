@@ -72,7 +72,7 @@ constexpr int kCopyWave0 = kIWaves, kCopyWaves = 8;  // the waves that copy atte
 // kTraceL0+3: input wave 0 at points 0-15, weight wave 0 at points 16-23,
 // attention (input wave 0) at points 24-31.
 constexpr int kTraceL0 = 16;
-constexpr int kTracePoints = 96;   // 48-63: per-wave act polled, 64-79: per-wave xq written, 80-95: per-wave act phase entry
+constexpr int kTracePoints = 96;   // 48-53: GQA item (item blocks), 54-56: GQA combine; 57-95 free
 constexpr int kTraceWords = 4 * kTracePoints;
 #endif
 
@@ -1132,6 +1132,7 @@ __device__ void gqa_item(const EngineParams& p, const hq_layer& Ly, int l, int k
     const int ncg = min(cg, nc - c0);
     const bool cur = g == ngq - 1;           // the group holding the current position
     constexpr int pstride = kD + 2;
+    if (w == 0) TRACE(l, 48);
 
     if (w < G) {
         // wave w: query head kvh*G + w (dims lane, lane+64); wave 0 of the
@@ -1208,10 +1209,12 @@ __device__ void gqa_item(const EngineParams& p, const hq_layer& Ly, int l, int k
             vl[lane + 64] = v1;
         }
     }
+    if (w == 0) TRACE(l, 49);
     // the copy waves' K/V copies have landed (they issued them), the query
     // heads and the current row are in place
     if (is_copy_wave(w)) wait_all_memory();
     __syncthreads();
+    if (w == 0) TRACE(l, 50);
 
     // scores: wave w takes positions 4w .. 4w+3 of every chunk (16 lanes per
     // position, 8 dims each) for every query head; the K rows are read once
@@ -1250,6 +1253,7 @@ __device__ void gqa_item(const EngineParams& p, const hq_layer& Ly, int l, int k
         }
     }
     __syncthreads();
+    if (w == 0) TRACE(l, 51);
 
     // chunk partials: task (head hh, chunk c, half of the dims); wave w takes
     // tasks w, w + 16, ...; each publishes its o values (and m, l) directly
@@ -1271,9 +1275,11 @@ __device__ void gqa_item(const EngineParams& p, const hq_layer& Ly, int l, int k
             ll_store(cp + 2 + d, o, epoch_att);
         }
     }
+    if (w == 0) TRACE(l, 52);
     // the item's LDS (K/V chunks, queries, scores) may be reused once every
     // wave is done
     __syncthreads();
+    if (w == 0) TRACE(l, 53);
 }
 
 // Entries i < count (64-bit {value, epoch}, at src_of(i)) into dst[i] as
@@ -1325,7 +1331,7 @@ __device__ __forceinline__ void gather_entries(int count, F&& src_of, float* dst
 // four input waves meet at their barrier.
 constexpr int kCombineChunks = 512;   // chunks per staged batch (at most)
 __device__ void gqa_combine(const EngineParams& p, int nc, const Slot& z, uint32_t epoch_att, int& bseq,
-                            unsigned& budget)
+                            unsigned& budget, int tl = -1)
 {
     constexpr int pstride = kD + 2;
     constexpr int kStage = int(sizeof(S.kv) / (sizeof(float)));
@@ -1358,9 +1364,11 @@ __device__ void gqa_combine(const EngineParams& p, int nc, const Slot& z, uint32
         }, stage, epoch_att, budget, p.status);
     };
     // M of each head (S.wmax[k]): wave k < nh reduces the m values of head k
+    if (w == 0) TRACE(tl, 54);
     for (int cb = 0; cb < nc; cb += cb2) {
         const int nb = min(cb2, nc - cb);
         gather_batch(cb, nb, single);
+        if (w == 0) TRACE(tl, 55);
         ibar(bseq, budget, p.status);
         if (w < nh) {
             float mm = -__builtin_inff();
@@ -1402,6 +1410,7 @@ __device__ void gqa_combine(const EngineParams& p, int nc, const Slot& z, uint32
         }
         ibar(bseq, budget, p.status);
     }
+    if (w == 0) TRACE(tl, 56);
     if (t < ne) hs_store(z.att() + e0 + t, O * (1.0f / L));
 }
 
@@ -1504,7 +1513,7 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         attention_phase(p, Ly, l, pos, z, E + 2, budget);
         {
             const int nc = (pos + 1 + kAttnChunk - 1) / kAttnChunk;
-            if (nc > kGroup) gqa_combine(p, nc, z, E + 2, bseq, budget);
+            if (nc > kGroup) gqa_combine(p, nc, z, E + 2, bseq, budget, l);
         }
 
         // ---- P3: quant -> (o) -> residual ---------------------------------------------

@@ -73,13 +73,21 @@ SEGMENTS = [
     (22, 14, "body GEMV", "down (dot, rows to the input waves)"),
     (14, "end", "hand-off", "residual store -> next layer"),
 ]
-ATTENTION_POINTS = {25, 26, 27, 28, 29}
-# Past 256 positions the attention runs as GQA items and a combine spread
-# over every block, which record no points of their own: the segment from
-# the qkv rows to the attention output is then one "attention" segment.
+ATTENTION_POINTS = {25, 26, 27, 28, 29, 48, 49, 50, 51, 52, 53}
+# Past 256 positions the attention runs as GQA items (kv head, group of
+# chunks: points 48-53, taken in the blocks that ran one) and a combine
+# spread over every block (points 54-56).
 GQA_SEGMENTS = [s for s in SEGMENTS if s[0] not in (4, 25, 29)]
-GQA_SEGMENTS.insert(GQA_SEGMENTS.index((6, 7, "hand-off", "attention output: read + quant")),
-                    (4, 6, "attention", "attention phase: GQA items, hand-offs, combine"))
+GQA_SEGMENTS[GQA_SEGMENTS.index((6, 7, "hand-off", "attention output: read + quant")):
+             GQA_SEGMENTS.index((6, 7, "hand-off", "attention output: read + quant"))] = [
+    (4, 49, "hand-off", "qkv rows -> GQA items (q/k rows in)"),
+    (49, 50, "attention", "GQA item: q/k prologue, K/V copies landed"),
+    (50, 51, "attention", "GQA item: scores (4 query heads)"),
+    (51, 53, "attention", "GQA item: softmax, V, partials published"),
+    (53, 55, "hand-off", "chunk partials -> every block (gather)"),
+    (55, 56, "attention", "combine (M, a_c, L/O chains)"),
+    (56, 6, "hand-off", "attention output: watch"),
+]
 CATEGORIES = ["body GEMV", "attention", "norm + quant", "hand-off", "sync"]
 
 
@@ -117,6 +125,8 @@ def part_trace(ctx, seed, reps=4):
     tr = traces[-1]
     has_att = (tr[:, 0, 25] != 0) & (tr[:, 0, 29] != 0)
     segments = SEGMENTS if has_att.any() else GQA_SEGMENTS
+    if not has_att.any():
+        has_att = (tr[:, 0, 48] != 0) & (tr[:, 0, 53] != 0)     # the blocks that ran a GQA item
     per_layer = []
     for L in range(TRACE_LAYERS - 1):
         rel = (tr[:, L, :] - tr[:, L, 0:1]) / 100.0            # 100 MHz clock -> us
