@@ -16,8 +16,9 @@ its launch stream; the body-weight bandwidth of that launch; and, under
 with its own roofline and CPU baseline: configs[0] (one fused quant + int4
 GEMV 2560 -> 9728 over rotating weight copies), configs[1] (one decoder
 layer's body GEMVs: the standalone GEMV kernels and the layer kernel's
-per-layer share) and configs[4] (the same decode at context 4096, with the
-attention's KV bandwidth).  cpu_baseline is the CPU oracle (this repository's
+per-layer share), configs[4] (the same decode at context 4096, with the
+attention's KV bandwidth) and configs[3] (the batched decode step of M = 8
+and 32 sequences at context 256).  cpu_baseline is the CPU oracle (this repository's
 C restatement of the reference path; AVX-512 VNNI GEMVs where the host has
 them) decoding the same model on this host, on all available cores and on
 the reference's default 6 threads, with the CPU model and core counts.
@@ -67,7 +68,7 @@ def parse():
     ap.add_argument("--batch-sizes", default="8,16,32",
                     help="batched: comma-separated M values; value is the largest M's rate")
     ap.add_argument("--no-configs", action="store_true",
-                    help="decode: skip the configs[0]/[1]/[4] measurements folded into the line")
+                    help="decode: skip the configs[0]/[1]/[3]/[4] measurements folded into the line")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="print the traffic summary of rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE output "
                          "directories of --workload layers and --workload copy runs")
@@ -377,23 +378,17 @@ def batched_step_bytes(config, m, context):
     return weights + lm_head + m * per_seq
 
 
-def bench_batched(args):
-    """batched greedy decode of M = 8, 16 and 32 independent
-    sequences at context 256 (each prefilled with its own random 256-token
+def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None):
+    """batched greedy decode of M independent sequences (M in
+    `sizes`) at context `ctx` (each prefilled with its own random ctx-token
     prompt), one hq_decode_batch step per token of every sequence, replayed
-    from a HIP graph.  value = sequence-tokens/s at M = 32; per M the step
-    time, tok/s, the step's HBM bytes over its time (weights once per step +
-    M K/V caches), and the speedup over M batch-1 decode steps of the same
-    model at the same context."""
+    from a HIP graph.  Per M: the step time, sequence-tokens/s, the step's
+    HBM bytes over its time (weights once per step + M K/V caches), and the
+    ratio to M batch-1 decode steps of the same model at the same context.
+    The largest M gives the case's value and roofline."""
     import numpy as np
     import torch
-    from harsh4b_amd.config import QWEN3_4B
-    from harsh4b_amd.synthetic import random_model
-    cfg = QWEN3_4B
-    ctx = args.ctx if args.ctx is not None else 256
-    steps, warmup = max(1, min(args.steps, 64)), max(1, min(args.warmup, 8))
-    print(f"# building random Qwen3-4B int4 model (seed {args.seed})", file=sys.stderr, flush=True)
-    model = random_model(cfg, seed=args.seed)
+    cfg = model.config
     vocab = int(cfg["vocab_size"])
     cap = ctx + warmup + steps + 4
 
@@ -418,11 +413,8 @@ def bench_batched(args):
     one.check_status()
     del one
     tok1 = steps / t1
-    print(f"# batch 1 at context {ctx}: {tok1:.1f} tok/s", file=sys.stderr, flush=True)
+    print(f"# configs[3] batch 1 at context {ctx}: {tok1:.1f} tok/s", file=sys.stderr, flush=True)
     per_m = {}
-    sizes = sorted({int(x) for x in args.batch_sizes.split(",") if x.strip()})
-    if not sizes or sizes[0] < 1:
-        raise SystemExit("--batch-sizes needs positive integers")
     for m in sizes:
         states = []
         for i in range(m):
@@ -447,31 +439,57 @@ def bench_batched(args):
         del states
     top_m = sizes[-1]
     top = per_m[top_m]
+    res = {"workload": f"configs[3]: batched decode of M = {'/'.join(map(str, sizes))} sequences at context "
+                       f"{ctx}, each with its own fp16 KV cache, greedy; value at M = {top_m}",
+           "value": top["tok_s"], "unit": "sequence-tok/s", "steps": steps, "warmup": warmup,
+           "ms_per_step": top["ms_per_step"],
+           "roofline": {"kernel": f"whole batched step (hq_decode_batch), M={top_m}", "bound": "hbm",
+                        "achieved": top["achieved_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": top["hbm_frac"], "traffic": None, "algorithmic_bytes": top["bytes_per_step"]},
+           "batch1_tok_s": round(tok1, 1), "per_m": per_m}
+    if cpu_seconds > 0:
+        res["cpu_baseline"] = cpu_baseline_batched(model, ctx, cpu_seconds, ref)
+    return res
+
+
+def bench_batched(args):
+    """configs[3] as its own line (see batched_case): M = --batch-sizes
+    (default 8, 16, 32) at context 256; value = sequence-tokens/s at the
+    largest M."""
+    from harsh4b_amd.config import QWEN3_4B
+    from harsh4b_amd.synthetic import random_model
+    ctx = args.ctx if args.ctx is not None else 256
+    steps, warmup = max(1, min(args.steps, 64)), max(1, min(args.warmup, 8))
+    sizes = sorted({int(x) for x in args.batch_sizes.split(",") if x.strip()})
+    if not sizes or sizes[0] < 1:
+        raise SystemExit("--batch-sizes needs positive integers")
+    print(f"# building random Qwen3-4B int4 model (seed {args.seed})", file=sys.stderr, flush=True)
+    model = random_model(QWEN3_4B, seed=args.seed)
+    case = batched_case(model, ctx, sizes, steps, warmup, 0 if args.no_cpu_baseline else args.cpu_seconds)
+    top_m = sizes[-1]
     result = {"metric": f"batched greedy decode sequence-tokens/s (configs[3], M={top_m}, context {ctx})",
-              "value": top["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
-              "ms_per_step": top["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+              "value": case["value"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+              "ms_per_step": case["ms_per_step"], "higher_is_better": True, "scaling": "weak",
               "vs_baseline": None, "dtype": "int8",
-              "data": "synthetic: random-init int4 weights, random 256-token prompts (seeds 4+i)",
-              "config": {"workload": f"configs[3]: batched decode of M = {'/'.join(map(str, sizes))} sequences "
-                                     f"at context {ctx}, each with its own fp16 KV cache, greedy",
-                         "global_batch": top_m, "seq_len": ctx, "parallelism": "none (1 GPU)"},
-              "roofline": {"kernel": f"whole batched step (hq_decode_batch), M={top_m}", "bound": "hbm",
-                           "achieved": top["achieved_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": top["hbm_frac"], "traffic": None, "algorithmic_bytes": top["bytes_per_step"]},
-              "batch1_tok_s": round(tok1, 1), "per_m": per_m}
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_batched(model, ctx, args.cpu_seconds)
+              "data": f"synthetic: random-init int4 weights, random {ctx}-token prompts (seeds 4+i)",
+              "config": {"workload": case["workload"], "global_batch": top_m, "seq_len": ctx,
+                         "parallelism": "none (1 GPU)"},
+              "roofline": case["roofline"], "batch1_tok_s": case["batch1_tok_s"], "per_m": case["per_m"]}
+    if "cpu_baseline" in case:
+        result["cpu_baseline"] = case["cpu_baseline"]
     print(json.dumps(result), flush=True)
 
 
-def cpu_baseline_batched(model, ctx, seconds):
+def cpu_baseline_batched(model, ctx, seconds, ref=None):
     """The oracle decoding sequences one step at a time (the reference has no
-    batching: M sequences cost M steps), from a cache of `ctx` positions."""
+    batching: M sequences cost M steps), from a cache of `ctx` positions.
+    `ref`: an oracle model of the same weights, if one is at hand."""
     import numpy as np
     import oracle
     from harsh4b_amd.synthetic import host_arrays
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    ref = oracle.OracleModel(model.config, host_arrays(model))
+    if ref is None:
+        ref = oracle.OracleModel(model.config, host_arrays(model))
     rs = ref.new_state(ctx + 64)
     rng = np.random.default_rng(4)
     for name in ("keys", "values"):
@@ -978,10 +996,12 @@ def main():
         ref = oracle.OracleModel(model.config, arrays)
     cpu_s = 0 if args.no_cpu_baseline else args.cpu_seconds
     if args.workload == "decode" and not args.no_configs:
-        print("# configs[0], [1] and [4]", file=sys.stderr, flush=True)
+        print("# configs[0], [1], [4] and [3]", file=sys.stderr, flush=True)
         configs = {"configs[0]": gemv_case(args, cpu_s / 4),
                    "configs[1]": layer_case(cfg, per_kind_ms, layers_ms, arrays, cpu_s / 4),
                    "configs[4]": long_case(args, model, lib, cfg, ref, cpu_s, (context, layers_ms))}
+        print("# configs[3]", file=sys.stderr, flush=True)
+        configs["configs[3]"] = batched_case(model, 256, [8, 32], 16, 2, cpu_s / 4, ref)
         result["configs"] = configs
         att = attention_case(args, torch)
         print(f"# hq_gqa_decode at context 4096: {att['us_per_call']:.2f} us, {att['achieved']:.0f} GB/s",

@@ -476,8 +476,9 @@ static void gqa_split_impl(const float* query, const void* keys, const void* val
     const float scale = 1.0f / sqrtf((float)head_dim);
     const int nchunks = (context + chunk - 1) / chunk;
     const int dpl = head_dim / 16;
-    /* query heads are independent: one OpenMP thread per head at a time */
-#pragma omp parallel for schedule(dynamic, 1) if (context >= 256)
+    /* query heads are independent: one OpenMP thread per head at a time
+     * (from 32 positions up: below that a head is too little work) */
+#pragma omp parallel for schedule(dynamic, 1) if (context >= 32)
     for (int qh = 0; qh < kv_heads * groups; ++qh) {
         {
             const int g = qh / groups;
