@@ -184,7 +184,7 @@ class QwenDecodeState:
         s.activated, s.logits = self.activated.data_ptr(), self.logits.data_ptr()
         s.workspace = self.workspace.data_ptr()
         self.struct = s
-        self._graph = None
+        self._graphs = {}          # steps -> captured graph of that many greedy steps
         self._prefill_ws = None
 
     def synchronize(self) -> None:
@@ -201,9 +201,9 @@ class QwenDecodeState:
             raise RuntimeError("a phase wait of the persistent layer kernel gave up")
 
     def close(self) -> None:
-        if self._graph is not None:
-            _native.lib().hq_graph_destroy(self._graph)
-            self._graph = None
+        for handle in self._graphs.values():
+            _native.lib().hq_graph_destroy(handle)
+        self._graphs = {}
 
     def __del__(self):
         try:
@@ -358,6 +358,8 @@ class LiteSparkQwen:
         state.synchronize()
         return int(state.token.item())
 
+    GRAPH_STEPS = (64, 8, 1)   # greedy steps per captured graph, largest first
+
     def decode_greedy(self, state: QwenDecodeState, steps: int, use_graph: bool = True,
                       check_status: bool = True) -> None:
         """Run `steps` greedy steps feeding each argmax token back on the device
@@ -371,14 +373,21 @@ class LiteSparkQwen:
             raise ValueError("decode state capacity exhausted")
         lib = _native.lib()
         if use_graph:
-            if state._graph is None:
-                handle = ctypes.c_void_p()
-                check(lib.hq_graph_capture(ctypes.byref(self.struct), ctypes.byref(state.struct), 1,
-                                           state.stream.cuda_stream, ctypes.byref(handle)),
-                      "hq_graph_capture")
-                state._graph = handle.value
-            for _ in range(steps):
-                check(lib.hq_graph_launch(state._graph, state.stream.cuda_stream), "hq_graph_launch")
+            def graph(n):
+                if n not in state._graphs:
+                    handle = ctypes.c_void_p()
+                    check(lib.hq_graph_capture(ctypes.byref(self.struct), ctypes.byref(state.struct), n,
+                                               state.stream.cuda_stream, ctypes.byref(handle)),
+                          "hq_graph_capture")
+                    state._graphs[n] = handle.value
+                return state._graphs[n]
+            # up to GRAPH_STEPS[0] steps per graph launch: the GPU idles
+            # between consecutive graph launches (about 140 us at batch 1)
+            left = steps
+            for n in self.GRAPH_STEPS:
+                while left >= n:
+                    check(lib.hq_graph_launch(graph(n), state.stream.cuda_stream), "hq_graph_launch")
+                    left -= n
         else:
             for _ in range(steps):
                 check(lib.hq_decode_step(ctypes.byref(self.struct), ctypes.byref(state.struct),
