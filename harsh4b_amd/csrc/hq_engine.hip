@@ -1026,29 +1026,38 @@ __device__ void attention_item(const EngineParams& p, const hq_layer& Ly, int l,
         const float4 qb = *reinterpret_cast<const float4*>(&S.aq[l16 * 8 + 4]);
         qv[0] = qa.x; qv[1] = qa.y; qv[2] = qa.z; qv[3] = qa.w;
         qv[4] = qb.x; qv[5] = qb.y; qv[6] = qb.z; qv[7] = qb.w;
-        uint4 kw[kGroup];
-        static_for<kGroup>([&](auto c) {
-            kw[c] = c < ncg ? *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]) : make_uint4(0, 0, 0, 0);
-        });
-        float pp[kGroup];
-        static_for<kGroup>([&](auto c) {
-            const uint32_t kk[4] = {kw[c].x, kw[c].y, kw[c].z, kw[c].w};
-            float a = 0.0f;
+        // the code is specialized on the chunk count, so only the item's
+        // chunks are computed (36 layers at context 64: 742 -> 737 us; the
+        // GQA items' scores likewise: 905 -> 872 us at context 272)
+        auto scores = [&](auto nc_const) {
+            constexpr int NC = decltype(nc_const)::value;
+            uint4 kw[NC];
+            static_for<NC>([&](auto c) { kw[c] = *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]); });
+            float pp[NC];
+            static_for<NC>([&](auto c) {
+                const uint32_t kk[4] = {kw[c].x, kw[c].y, kw[c].z, kw[c].w};
+                float a = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
-                a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
-            }
-            pp[c] = a;
-        });
-        static_for<kGroup>([&](auto c) { pp[c] = row_tree_sum16(pp[c]); });
-        if (l16 == 0)
-            static_for<kGroup>([&](auto c) {
-                if (c < ncg) {
+                for (int i = 0; i < 4; ++i) {
+                    a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
+                    a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
+                }
+                pp[c] = a;
+            });
+            static_for<NC>([&](auto c) { pp[c] = row_tree_sum16(pp[c]); });
+            if (l16 == 0)
+                static_for<NC>([&](auto c) {
                     const int tn = min(kAttnChunk, n - (c0 + c) * kAttnChunk);
                     S.as[c * kAttnChunk + t] = t < tn ? pp[c] * scale : -__builtin_inff();
-                }
-            });
+                });
+        };
+        static_assert(kGroup == 4, "one specialization per chunk count");
+        switch (ncg) {
+        case 1: scores(std::integral_constant<int, 1>{}); break;
+        case 2: scores(std::integral_constant<int, 2>{}); break;
+        case 3: scores(std::integral_constant<int, 3>{}); break;
+        default: scores(std::integral_constant<int, 4>{}); break;
+        }
     }
     __syncthreads();
     if (w == 0) TRACE(l, 27);
@@ -1222,34 +1231,40 @@ __device__ void gqa_item(const EngineParams& p, const hq_layer& Ly, int l, int k
         const float scale = 1.0f / __builtin_sqrtf(float(kD));
         const int l16 = lane & 15;
         const int t = w * 4 + (lane >> 4);
-        uint4 kw[kGroup];
-        static_for<kGroup>([&](auto c) {
-            kw[c] = c < ncg ? *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]) : make_uint4(0, 0, 0, 0);
-        });
-        for (int hh = 0; hh < G; ++hh) {
-            float qv[8];
-            const float4 qa = *reinterpret_cast<const float4*>(&S.gq[hh][l16 * 8]);
-            const float4 qb = *reinterpret_cast<const float4*>(&S.gq[hh][l16 * 8 + 4]);
-            qv[0] = qa.x; qv[1] = qa.y; qv[2] = qa.z; qv[3] = qa.w;
-            qv[4] = qb.x; qv[5] = qb.y; qv[6] = qb.z; qv[7] = qb.w;
-            float pp[kGroup];
-            static_for<kGroup>([&](auto c) {
-                const uint32_t kk[4] = {kw[c].x, kw[c].y, kw[c].z, kw[c].w};
-                float a = 0.0f;
+        // specialized on the chunk count: only the item's chunks are computed
+        auto scores = [&](auto nc_const) {
+            constexpr int NC = decltype(nc_const)::value;
+            uint4 kw[NC];
+            static_for<NC>([&](auto c) { kw[c] = *reinterpret_cast<const uint4*>(&S.kv[c].k[t * kD + l16 * 8]); });
+            for (int hh = 0; hh < G; ++hh) {
+                float qv[8];
+                const float4 qa = *reinterpret_cast<const float4*>(&S.gq[hh][l16 * 8]);
+                const float4 qb = *reinterpret_cast<const float4*>(&S.gq[hh][l16 * 8 + 4]);
+                qv[0] = qa.x; qv[1] = qa.y; qv[2] = qa.z; qv[3] = qa.w;
+                qv[4] = qb.x; qv[5] = qb.y; qv[6] = qb.z; qv[7] = qb.w;
+                float pp[NC];
+                static_for<NC>([&](auto c) {
+                    const uint32_t kk[4] = {kw[c].x, kw[c].y, kw[c].z, kw[c].w};
+                    float a = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
-                    a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
-                }
-                pp[c] = row_tree_sum16(a);
-            });
-            if (l16 == 0)
-                static_for<kGroup>([&](auto c) {
-                    if (c < ncg) {
+                    for (int i = 0; i < 4; ++i) {
+                        a = __builtin_fmaf(qv[2 * i], f16_to_f32(uint16_t(kk[i])), a);
+                        a = __builtin_fmaf(qv[2 * i + 1], f16_to_f32(uint16_t(kk[i] >> 16)), a);
+                    }
+                    pp[c] = row_tree_sum16(a);
+                });
+                if (l16 == 0)
+                    static_for<NC>([&](auto c) {
                         const int tn = min(kAttnChunk, n - (c0 + c) * kAttnChunk);
                         S.gs[hh][c * kAttnChunk + t] = t < tn ? pp[c] * scale : -__builtin_inff();
-                    }
-                });
+                    });
+            }
+        };
+        switch (ncg) {
+        case 1: scores(std::integral_constant<int, 1>{}); break;
+        case 2: scores(std::integral_constant<int, 2>{}); break;
+        case 3: scores(std::integral_constant<int, 3>{}); break;
+        default: scores(std::integral_constant<int, 4>{}); break;
         }
     }
     __syncthreads();
