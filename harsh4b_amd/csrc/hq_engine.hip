@@ -403,6 +403,7 @@ __device__ __forceinline__ float rmsnorm_quant(float (&x)[NPT], int n, const flo
                                                int tl = -1, int tp = 0)
 {
     const int t = opaque_tid();
+    n = __builtin_amdgcn_readfirstlane(n);   // (uniform; an SGPR operand for the asm below)
     asm volatile("" : "+s"(n));   // keep float(n) from being hoisted out of the layer loop
     float ss = 0.0f;
 #pragma unroll
