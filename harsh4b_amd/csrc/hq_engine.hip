@@ -867,6 +867,22 @@ __device__ __forceinline__ bool block_has_item(const EngineParams& p, int pos)
     return item_slot(blockIdx.x, gridDim.x, p.G) < p.heads;
 }
 
+// n when the blocks that run attention items at position pos are exactly
+// blocks [0, n) (as block_has_item assigns them), else -1.
+__device__ __forceinline__ int item_block_prefix(const EngineParams& p, int pos)
+{
+    const int n = pos + 1;
+    const int nc = (n + kAttnChunk - 1) / kAttnChunk;
+    const int NB = int(gridDim.x);
+    if ((nc + kGroup - 1) / kGroup > 1) {
+        const int cg = gqa_group(nc, p.kv_heads, NB);
+        return min(NB, p.kv_heads * ((nc + cg - 1) / cg));
+    }
+    // item_slot maps blocks [0, 32k) onto slots [0, 32k), else it is the identity
+    if (p.G != 4 || (NB & 31) != 0 || (p.heads & 31) == 0) return min(NB, p.heads);
+    return -1;
+}
+
 // V accumulation of one or two chains per lane: o[d] = fmaf chain of
 // e_t * v_t[d] over ascending t of a chunk (positions past the context have
 // e_t = 0 and zero V rows: their fmaf returns the accumulator unchanged, bit
@@ -1666,8 +1682,21 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     // the hand-off set of this launch (launches alternate between two)
     const int set = int((base / (5u * uint32_t(p.L))) & 1u);
     Rows R;
-    R.h0 = split_begin(p.H, b, NB);
-    R.h1 = split_begin(p.H, b + 1, NB);
+    // The hidden rows (o, down and the residual entries) go to the blocks
+    // without attention items when those can hold them (one row per weight
+    // wave): an item block finishes its o dot last (36 layers at context 64:
+    // its o rows' residual entries arrived about 1.5 us after the others'
+    // in every layer).  A block without rows gets the empty range at H - 1:
+    // its loads clamp to valid rows and it stores nothing.
+    const int nit = item_block_prefix(p, pos);
+    const int nfree = NB - nit;
+    if (nit > 0 && nfree > 0 && (p.H + nfree - 1) / nfree <= min(kWWaves, kMaxOwn)) {
+        R.h0 = b < nit ? p.H - 1 : split_begin(p.H, b - nit, nfree);
+        R.h1 = b < nit ? p.H - 1 : split_begin(p.H, b - nit + 1, nfree);
+    } else {
+        R.h0 = split_begin(p.H, b, NB);
+        R.h1 = split_begin(p.H, b + 1, NB);
+    }
     R.q0 = split_begin(p.qkv_rows, b, NB);
     R.q1 = split_begin(p.qkv_rows, b + 1, NB);
     // SwiGLU rows in whole groups of 8, so a block's quantized outputs fill
