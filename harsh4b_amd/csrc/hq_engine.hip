@@ -1613,15 +1613,24 @@ __device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32
         // ---- P3: quant -> (o) -> residual ---------------------------------------------
         float gpost[kHidNPT];
         {
-            float att[kAttNPT];
             TRACE(l, 5);
-            watch_last(z.att(), qd, budget, p.status);
-            TRACE(l, 6);
-            poll_into<kAttNPT>(z.att(), qd, att, budget, p.status);
-            post_hs();
-            load_gamma(Ly.post_norm, H, gpost);
-            const float act = quantize(att, qd, kOLPR * kOC * 32, bseq, budget, p.status);
-            post_xq(act);
+            if (nown > 0) {
+                float att[kAttNPT];
+                watch_last(z.att(), qd, budget, p.status);
+                TRACE(l, 6);
+                poll_into<kAttNPT>(z.att(), qd, att, budget, p.status);
+                post_hs();
+                load_gamma(Ly.post_norm, H, gpost);
+                const float act = quantize(att, qd, kOLPR * kOC * 32, bseq, budget, p.status);
+                post_xq(act);
+            } else {
+                // (block-uniform) no o rows here: the weight waves' o dot
+                // runs on the previous input and stores nothing, so only
+                // the counters move on
+                post_hs();
+                load_gamma(Ly.post_norm, H, gpost);
+                post_xq(0.0f);
+            }
             TRACE(l, 7);
         }
         block_sync();   // the weight waves' results in S.res
