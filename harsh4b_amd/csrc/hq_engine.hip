@@ -1691,27 +1691,34 @@ __global__ __launch_bounds__(eng::kThreads) void engine_kernel(EngineParams p)
     // the hand-off set of this launch (launches alternate between two)
     const int set = int((base / (5u * uint32_t(p.L))) & 1u);
     Rows R;
-    // The hidden rows (o, down and the residual entries) go to the blocks
-    // without attention items when those can hold them (one row per weight
-    // wave): an item block finishes its o dot last (36 layers at context 64:
-    // its o rows' residual entries arrived about 1.5 us after the others'
-    // in every layer).  A block without rows gets the empty range at H - 1:
-    // its loads clamp to valid rows and it stores nothing.
+    R.q0 = split_begin(p.qkv_rows, b, NB);
+    R.q1 = split_begin(p.qkv_rows, b + 1, NB);
+    // The hidden rows (o, down and the residual entries) and the SwiGLU rows
+    // go to the blocks without attention items when those can hold them
+    // (one hidden row and four SwiGLU pairs per weight wave): an item block
+    // is the last to post its o and gate_up inputs (36 layers at context
+    // 64: its residual entries arrived about 1.5 us after the others' in
+    // every layer).  A block without rows gets empty ranges at H - 1 and I:
+    // its loads clamp to valid rows and it stores nothing.  SwiGLU rows go
+    // in whole groups of 8, so a block's quantized outputs fill whole 8-byte
+    // groups of the de-interleaved activation layout.
     const int nit = item_block_prefix(p, pos);
     const int nfree = NB - nit;
-    if (nit > 0 && nfree > 0 && (p.H + nfree - 1) / nfree <= min(kWWaves, kMaxOwn)) {
-        R.h0 = b < nit ? p.H - 1 : split_begin(p.H, b - nit, nfree);
-        R.h1 = b < nit ? p.H - 1 : split_begin(p.H, b - nit + 1, nfree);
+    const int ng8 = p.I / 8;
+    if (nit > 0 && nfree > 0 && (p.H + nfree - 1) / nfree <= min(kWWaves, kMaxOwn) &&
+        8 * ((ng8 + nfree - 1) / nfree) <= min(kWWaves * 4, kMaxRes)) {
+        const bool item = b < nit;
+        const int j = b - nit;
+        R.h0 = item ? p.H - 1 : split_begin(p.H, j, nfree);
+        R.h1 = item ? p.H - 1 : split_begin(p.H, j + 1, nfree);
+        R.g0 = item ? p.I : 8 * split_begin(ng8, j, nfree);
+        R.g1 = item ? p.I : 8 * split_begin(ng8, j + 1, nfree);
     } else {
         R.h0 = split_begin(p.H, b, NB);
         R.h1 = split_begin(p.H, b + 1, NB);
+        R.g0 = 8 * split_begin(ng8, b, NB);
+        R.g1 = 8 * split_begin(ng8, b + 1, NB);
     }
-    R.q0 = split_begin(p.qkv_rows, b, NB);
-    R.q1 = split_begin(p.qkv_rows, b + 1, NB);
-    // SwiGLU rows in whole groups of 8, so a block's quantized outputs fill
-    // whole 8-byte groups of the de-interleaved activation layout
-    R.g0 = 8 * split_begin(p.I / 8, b, NB);
-    R.g1 = 8 * split_begin(p.I / 8, b + 1, NB);
     {
         constexpr int kWords = sizeof(hq_layer) / sizeof(uint64_t);
         const uint64_t* src = reinterpret_cast<const uint64_t*>(p.layers);
