@@ -664,6 +664,7 @@ __device__ __forceinline__ void load_window(int e, unsigned& budget, int32_t* st
 __device__ void attention_phase(const EngineParams& p, const hq_layer& Ly, int l, int pos, const Slot& z,
                                 uint32_t epoch_att, unsigned& budget);
 __device__ __forceinline__ bool is_copy_wave(int w);
+template <bool GQA>
 __device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l, int pos);
 
 __device__ __forceinline__ bool block_has_item(const EngineParams& p, int pos);
@@ -703,9 +704,9 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         const bool more = l + 1 < p.L;
         const hq_layer& Ly = S.lay[l];
         const hq_layer& Ln = S.lay[more ? l + 1 : l];
-        // this layer's first attention item: its K/V copies land while the
-        // qkv GEMV and its hand-off run
-        if (is_copy_wave(opaque_tid() / kWave)) prefetch_first_item(p, l, pos);
+        // this layer's first GQA item: its K/V copies land while the qkv
+        // GEMV and its hand-off run
+        if (is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<true>(p, l, pos);
         // ---- P1: qkv
         wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 1), budget, p.status);
         if (ww == 0) TRACE(l, 16);
@@ -719,6 +720,9 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 17);
         if (ww == kWWaves - 1) TRACE(l, 47);
+        // this layer's first per-head attention item: its K/V copies land
+        // while the qkv rows are handed on
+        if (is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<false>(p, l, pos);
         // ---- P2: the block's attention items (all waves)
         attention_phase(p, Ly, l, pos, slot_of(p, set, l), base + 5u * uint32_t(l) + 2u, budget);
         if (att_blk) load_window(4 * l + 1, budget, p.status);
@@ -836,19 +840,25 @@ __device__ __forceinline__ int gqa_group(int nc, int kv_heads, int nb);
 __device__ __forceinline__ int item_slot(int b, int NB, int G);
 
 // The copies of this block's first attention item of layer l (copy waves):
-// issued at the start of the layer, so they land while the qkv GEMV and its
-// hand-off run.  Items as in attention_phase.
+// GQA items (GQA true: more than kGroup chunks, up to three per item) at the
+// start of the layer, so they land while the qkv GEMV and its hand-off run;
+// per-head items (GQA false) after the qkv dot, so they land while its
+// hand-off runs (issued before it, the copy waves' next LDS read waited for
+// them, LDS DMA being counted with the loads: 36 layers at context 64,
+// 719 -> 707 us per launch; GQA items issued late: 1143 -> 1167 us at 4096).
+// Items as in attention_phase.
+template <bool GQA>
 __device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l, int pos)
 {
     const int n = pos + 1;
     const int nc = (n + kAttnChunk - 1) / kAttnChunk;
     const int ng = (nc + kGroup - 1) / kGroup;
     const int b = blockIdx.x;
-    if (ng > 1) {
+    if (GQA && ng > 1) {
         const int cg = gqa_group(nc, p.kv_heads, gridDim.x);
         const int ngq = (nc + cg - 1) / cg;
         if (b < p.kv_heads * ngq) prefetch_group(p, l, b / ngq, (b % ngq) * cg, min(cg, nc - (b % ngq) * cg), n, pos);
-    } else {
+    } else if (!GQA && ng == 1) {
         const int k = item_slot(b, gridDim.x, p.G);   // per-head item: query head k
         if (k < p.heads) prefetch_group(p, l, k / p.G, 0, nc, n, pos);
     }
