@@ -843,9 +843,10 @@ __device__ __forceinline__ int item_slot(int b, int NB, int G);
 // GQA items (GQA true: more than kGroup chunks, up to three per item) at the
 // start of the layer, so they land while the qkv GEMV and its hand-off run;
 // per-head items (GQA false) after the qkv dot, so they land while its
-// hand-off runs (issued before it, the copy waves' next LDS read waited for
-// them, LDS DMA being counted with the loads: 36 layers at context 64,
-// 719 -> 707 us per launch; GQA items issued late: 1143 -> 1167 us at 4096).
+// hand-off runs (issued before it, an item block's weight waves took the
+// qkv input about 0.5 us later than the other blocks': 36 layers at context
+// 64, 719 -> 707 us per launch; GQA items issued late: 1143 -> 1167 us at
+// 4096).
 // Items as in attention_phase.
 template <bool GQA>
 __device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l, int pos)
