@@ -22,6 +22,8 @@
 // (each a contiguous range of double steps, all of its loads in flight at
 // once) and their int32 partial tiles meet in LDS, so no split of K crosses
 // blocks: no atomics, no arrival tickets, no zeroed workspace.
+#include <utility>
+
 #include "hq_device.h"
 #include "hq_internal.h"
 
@@ -52,6 +54,12 @@ struct GemmParams {
     // [0, n) then up rows [n, 2n); out [m, n] receives SwiGLU(gate, up) and
     // pmax [blocks, m] each block's maximum |out| per sequence
     float* pmax;
+    // Tail launches (gemm_lds_kernel<..., TAIL = true>, the batched step's o
+    // and down GEMMs): the outputs go to ll [m, n] as {value, epoch} entries
+    // (epoch = *epoch_ctr << 7 | epoch_id, unique per launch of a step), and
+    // block gridDim.x - m + s then finishes row s: the residual add into tx,
+    // RMSNorm with tgamma, quantization into tq (row stride tkq) and tact.
+    GemmTail tail;
 };
 
 // De-interleave 8 int8 columns (a, b = the two little-endian dwords) into
@@ -158,6 +166,123 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
     }
 }
 
+// ---- batched-step tails ------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t tail_epoch(const GemmTail& t)
+{
+    return (*t.epoch_ctr << 7) | uint32_t(t.epoch_id);
+}
+__device__ __forceinline__ bool tail_ready(uint64_t v, uint32_t ep)
+{
+    return int32_t(uint32_t(v >> 32) - ep) >= 0;
+}
+__device__ __forceinline__ uint64_t tail_load(const uint64_t* p)
+{
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr unsigned kTailSpinLimit = 1u << 22;   // rounds a tail waits before it gives up (HQ_STEP_SYNC)
+
+// f(0) .. f(N-1) with compile-time indices (register arrays stay in registers)
+template <class F, int... J>
+__device__ __forceinline__ void unrolled_impl(F&& f, std::integer_sequence<int, J...>)
+{
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void unrolled(F&& f)
+{
+    unrolled_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Row s of a tail launch, by threads 0-255 of one block (the others only
+// take the barriers): once every block's entry of the row is current (each
+// block stores its outputs before its tail begins; blocks start in index
+// order, so the blocks a tail waits for are running or done), the same
+// operations as the row kernel's RESID_NORM mode: x + GEMM output into the
+// residual, RMSNorm (256 strided fmaf partials, halving tree), the
+// normalized row's maximum over the four waves in order, quantization into
+// the de-interleaved row and act = amax / 127.
+template <int NPT>
+__device__ void gemm_tail_row(const GemmParams& p, int s, uint32_t ep, float* red, float* wmax)
+{
+    const GemmTail& T = p.tail;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int k = p.n;
+    const bool on = tid < kBlock;
+    float* xr = T.x + size_t(s) * k;
+    float v[NPT], gam[NPT];
+    if (on) {
+        const uint64_t* src = T.ll + size_t(s) * k;
+        uint64_t e[NPT];
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const int i = tid + kBlock * j;
+            v[j] = i < k ? xr[i] : 0.0f;
+            gam[j] = i < k ? T.gamma[i] : 0.0f;
+            e[j] = i < k ? tail_load(src + i) : uint64_t(ep) << 32;
+        }
+        unsigned spins = 0;
+        while (true) {
+            bool pending = false;
+            unrolled<NPT>([&](auto j) { pending |= !tail_ready(e[j], ep); });
+            if (!pending) break;
+            if (++spins == kTailSpinLimit) {
+                atomicOr(T.table->status[s], HQ_STEP_SYNC);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            unrolled<NPT>([&](auto j) {
+                if (!tail_ready(e[j], ep)) e[j] = tail_load(src + tid + kBlock * j);
+            });
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const int i = tid + kBlock * j;
+            v[j] = i < k ? v[j] + bits_f32(uint32_t(e[j])) : 0.0f;
+            if (i < k) {
+                xr[i] = v[j];   // the new residual (this block alone reads and writes row s)
+                ss = __builtin_fmaf(v[j], v[j], ss);
+            }
+        }
+        red[tid] = ss;
+    }
+    __syncthreads();
+    if (on) {
+        const float r2 = (red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]);
+        const float total = wave_tree_sum64_all(r2);
+        const float r = __builtin_sqrtf(total / float(k) + T.eps);
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const int i = tid + kBlock * j;
+            v[j] = i < k ? (v[j] / r) * gam[j] : 0.0f;
+            amax = fmaxf(amax, fabsf(v[j]));
+        }
+        amax = wave_max64_all(amax);
+        if (lane == 0) wmax[tid / kWave] = amax;
+    }
+    __syncthreads();
+    if (on) {
+        float amax = wmax[0];
+#pragma unroll
+        for (int w = 1; w < kBlock / kWave; ++w) amax = fmaxf(amax, wmax[w]);
+        amax = fmaxf(amax, 1e-5f);
+        const float inv = 127.0f / amax;
+        int8_t* qr = T.q + size_t(s) * T.kq;
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const int i = tid + kBlock * j;
+            if (i < k) qr[xq_offset(i)] = quant_i8(v[j], inv);
+        }
+        if (tid == 0) T.act[s] = amax / 127.0f;
+    }
+}
+// tail rows of up to 2560 values (wider rows hold more registers than a
+// 1024-thread down launch has: they take the row kernel instead)
+constexpr int kTailNPT = 10;
+
 // The same products with the weight rows staged through LDS, for rows of up
 // to HMAX packed bytes.  The block's R = 16 RG rows are one contiguous
 // R * K/2 byte range of the matrix; its threads read it in 16-byte chunks,
@@ -171,10 +296,12 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
 // with A from LDS, and the int32 partial tiles meet in the same LDS.
 // DS * W covers the double steps of any K up to 2 * HMAX (one round of B
 // loads per wave), CPT * W * 64 chunks cover the block's rows.
-template <int RG, int W, int BT, int DS, int CPT, int HMAX, bool SWIGLU = false>
+template <int RG, int W, int BT, int DS, int CPT, int HMAX, bool SWIGLU = false, int TAIL = 0>
 __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
 {
     static_assert(!SWIGLU || RG == 2, "a SwiGLU block pairs 16 gate rows with their 16 up rows");
+    // TAIL: 0, or the values per thread of a tail row (rows of up to 256 * TAIL)
+    static_assert(!TAIL || (!SWIGLU && W >= 4), "a tail takes 256 threads of a plain launch");
     constexpr int R = 16 * RG;
     constexpr int RS = HMAX + 16;                       // padded LDS row (bytes)
     constexpr int NRED = RG * BT * 4;                   // partial registers per lane
@@ -319,6 +446,7 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
             if (rr == 0 && ml < p.m) p.pmax[size_t(blockIdx.x) * p.m + ml] = mx;
         }
     } else {
+        const uint32_t ep = TAIL ? tail_epoch(p.tail) : 0u;
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
             const int e = tid + kWave * W * i;
@@ -332,9 +460,24 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
             const int mm = 16 * b + col, n = row0 + rl;
             if (mm < p.m && n < p.n) {
                 const int a = sum >> 4;
-                p.out[size_t(mm) * p.n + n] = (float(a) * act_e[i]) * ws_e[i];
-                if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
+                const float v = (float(a) * act_e[i]) * ws_e[i];
+                if constexpr (TAIL) {
+                    __hip_atomic_store(p.tail.ll + size_t(mm) * p.n + n, (uint64_t(ep) << 32) | uint64_t(f32_bits(v)),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    p.out[size_t(mm) * p.n + n] = v;
+                    if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
+                }
             }
+        }
+    }
+    if constexpr (TAIL) {
+        const uint32_t ep = tail_epoch(p.tail);
+        const int s = int(blockIdx.x) - (int(gridDim.x) - p.m);
+        if (s >= 0) {   // (block-uniform)
+            __shared__ float t_red[kBlock];
+            __shared__ float t_wmax[kBlock / kWave];
+            gemm_tail_row<TAIL>(p, s, ep, t_red, t_wmax);
         }
     }
 }
@@ -562,6 +705,46 @@ static void launch_swiglu(const GemmParams& p, hipStream_t s)
 }
 
 int gemm_swiglu_blocks(int n) { return (n + 15) / 16; }
+
+template <int W, int BT, int HMAX>
+static void launch_tail(const GemmParams& p, hipStream_t s)
+{
+    constexpr int DS = (2 * HMAX / 128 + W - 1) / W;
+    constexpr int CPT = (16 * HMAX / 16 + kWave * W - 1) / (kWave * W);
+    hipLaunchKernelGGL((gemm_lds_kernel<1, W, BT, DS, CPT, HMAX, false, kTailNPT>), dim3((p.n + 15) / 16),
+                       dim3(kWave * W), 0, s, p);
+}
+
+bool gemm_tail_fits(int m, int n, int k)
+{
+    const int half = k >> 1;
+    return m >= 1 && m <= kMaxBatch && n <= kBlock * kTailNPT && (n + 15) / 16 >= m && half > 1280 &&
+           half <= 5120;
+}
+
+// The batched step's o and down GEMMs with the residual + RMSNorm + quant
+// rows of the next GEMM's input in their tail (see GemmParams::tail).
+hipError_t gemm_run_tail(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int m, int n, int k,
+                         const GemmTail& tail, hipStream_t s)
+{
+    if (!gemm_tail_fits(m, n, k) || tail.epoch_id < 0 || tail.epoch_id >= 128) return hipErrorInvalidValue;
+    GemmParams p{};
+    p.m = m;
+    p.x = x;
+    p.act = act;
+    p.w = w; p.ws = ws;
+    p.n = n; p.k = k; p.kp = padded_k(k);
+    p.tail = tail;
+    const int half = k >> 1;
+    if (half <= 2048) {
+        if (m > 16) launch_tail<8, 2, 2048>(p, s);
+        else launch_tail<8, 1, 2048>(p, s);
+    } else {
+        if (m > 16) launch_tail<16, 2, 5120>(p, s);
+        else launch_tail<16, 1, 5120>(p, s);
+    }
+    return hipGetLastError();
+}
 
 // gate_up with SwiGLU in the GEMM epilogue, then the down input's
 // quantization: act_out [m, n] fp32, q [m, kq] int8 + act [m].

@@ -117,6 +117,26 @@ size_t gemm_scratch_bytes(int m, int n, int k);
 hipError_t gemm_run_swiglu(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* act_out,
                            int m, int n, int k, float* pmax, int8_t* q, int kq, float* act_q, hipStream_t s);
 int gemm_swiglu_blocks(int n);
+
+// The batched step's o and down GEMMs with the next GEMM's input rows in
+// their tail: the outputs go to ll as {value, epoch} entries and the last m
+// blocks each finish one sequence's row (residual add into x, RMSNorm with
+// gamma, quantization into q / act), as the RESID_NORM row kernel does.
+struct GemmTail {
+    uint64_t* ll;               // [m, n]
+    const uint32_t* epoch_ctr;  // the step counter (bumped by the step's first kernel)
+    int epoch_id;               // 0 .. 127, unique per launch within a step
+    float* x;                   // [m, n] residual rows, updated
+    const float* gamma;         // [n]
+    float eps;
+    int8_t* q;                  // [m, kq] de-interleaved, zero past n
+    int kq;
+    float* act;                 // [m]
+    const BatchTable* table;    // status words of the sequences
+};
+bool gemm_tail_fits(int m, int n, int k);
+hipError_t gemm_run_tail(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int m, int n, int k,
+                         const GemmTail& tail, hipStream_t s);
 hipError_t gemm_run(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* out, int m, int n,
                     int k, char* scratch, hipStream_t s);
 hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s);

@@ -324,11 +324,14 @@ static int run_rows(int mode, RowParams p, int rows, hipStream_t s)
 
 // ---- batched decode step ----------------------------------------------------------
 
-__global__ void batch_table_kernel(BatchTable t, BatchTable* dst)
+// The step's table into the workspace, and the step counter one up (the
+// GEMM tails' entries of this step carry it).
+__global__ void batch_table_kernel(BatchTable t, BatchTable* dst, uint32_t* step_ctr)
 {
     const uint32_t* src = reinterpret_cast<const uint32_t*>(&t);
     uint32_t* d = reinterpret_cast<uint32_t*>(dst);
     for (int i = threadIdx.x; i < int(sizeof(BatchTable) / 4); i += blockDim.x) d[i] = src[i];
+    if (threadIdx.x == 0) *step_ctr += 1u;
 }
 
 // Block m: the embedding row of sequence m's current token (a token outside
@@ -436,8 +439,8 @@ __global__ __launch_bounds__(kBlock) void batch_store_x_kernel(const float* x, i
 }
 
 struct BatchLayout {
-    size_t x, q8, act, qkv, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, pmax, table,
-        total;
+    size_t x, q8, act, qkv, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, pmax, table, ll,
+        step_ctr, total;
     int kp, max_chunks, qkv_rows, qd, arg_blocks;
 };
 
@@ -475,6 +478,8 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.tickets = take(size_t(B) * ticket_words(L.arg_blocks) * 4);
     L.pmax = take(size_t(gemm_swiglu_blocks(I)) * B * 4);
     L.table = take(sizeof(BatchTable));
+    L.ll = take(size_t(B) * H * 8);
+    L.step_ctr = take(4);
     L.total = off;
     return L;
 }
@@ -640,7 +645,8 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
     const int H = m->hidden, I = m->intermediate, D = m->head_dim, KV = m->kv_heads, M = count;
     const long long time_stride = (long long)KV * D;
     auto ok = [] { return hipGetLastError() == hipSuccess; };
-    hipLaunchKernelGGL(batch_table_kernel, dim3(1), dim3(kBlock), 0, s, t, table);
+    uint32_t* step_ctr = reinterpret_cast<uint32_t*>(ws + L.step_ctr);
+    hipLaunchKernelGGL(batch_table_kernel, dim3(1), dim3(kBlock), 0, s, t, table, step_ctr);
     hipLaunchKernelGGL(batch_embed_kernel, dim3(M), dim3(kBlock), 0, s, m->embedding, m->embedding_scales, m->vocab,
                        H, table, x);
     if (!ok()) return HQ_ERR_LAUNCH;
@@ -649,6 +655,19 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
     rp.q = q8;
     rp.act = act;
     int e;
+    // The o and down GEMMs finish the next GEMM's input rows in their tails
+    // (residual add, RMSNorm, quantization) where the shapes allow, instead
+    // of a row kernel after them.
+    const bool tails = m->layers <= 64 && gemm_tail_fits(M, H, L.qd) && gemm_tail_fits(M, H, I);
+    GemmTail tl{};
+    tl.ll = reinterpret_cast<uint64_t*>(ws + L.ll);
+    tl.epoch_ctr = step_ctr;
+    tl.x = x;
+    tl.eps = m->eps;
+    tl.q = q8;
+    tl.kq = gemm_padded_k(H);
+    tl.act = act;
+    tl.table = table;
     for (int l = 0; l < m->layers; ++l) {
         const hq_layer& Ly = m->layer[l];
         rp.x = x;
@@ -656,7 +675,7 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         rp.gate_up = nullptr;
         rp.gamma = Ly.input_norm;
         rp.k = H;
-        if ((e = run_rows(l == 0 ? ROW_NORM : ROW_RESID_NORM, rp, M, s))) return e;
+        if ((l == 0 || !tails) && (e = run_rows(l == 0 ? ROW_NORM : ROW_RESID_NORM, rp, M, s))) return e;
         if (gemm_run(q8, act, Ly.qkv, Ly.qkv_scales, qkv, M, L.qkv_rows, H, gemm, s) != hipSuccess)
             return HQ_ERR_LAUNCH;
         // q/k head norms, RoPE and the K/V write of each sequence inside the
@@ -682,26 +701,40 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         a.act = act;
         a.kp = gemm_padded_k(L.qd);
         if (launch_batch_attention(a, s) != hipSuccess) return HQ_ERR_LAUNCH;
-        if (gemm_run(q8, act, Ly.o, Ly.o_scales, proj, M, H, L.qd, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
-        rp.x = x;
-        rp.add = proj;
-        rp.gamma = Ly.post_norm;
-        rp.k = H;
-        if ((e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
+        if (tails) {
+            tl.epoch_id = 2 * l;
+            tl.gamma = Ly.post_norm;
+            if (gemm_run_tail(q8, act, Ly.o, Ly.o_scales, M, H, L.qd, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        } else {
+            if (gemm_run(q8, act, Ly.o, Ly.o_scales, proj, M, H, L.qd, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
+            rp.x = x;
+            rp.add = proj;
+            rp.gamma = Ly.post_norm;
+            rp.k = H;
+            if ((e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
+        }
         // gate_up with SwiGLU in its epilogue, then the down input's quant
         if (gemm_run_swiglu(q8, act, Ly.gate_up, Ly.gate_up_scales, gu, M, I, H, reinterpret_cast<float*>(ws + L.pmax),
                             q8, gemm_padded_k(I), act, s) != hipSuccess)
             return HQ_ERR_LAUNCH;
-        if (gemm_run(q8, act, Ly.down, Ly.down_scales, proj, M, H, I, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        if (tails) {
+            // the next layer's input rows (the final norm's after the last layer)
+            tl.epoch_id = 2 * l + 1;
+            tl.gamma = l + 1 < m->layers ? m->layer[l + 1].input_norm : m->final_norm;
+            if (gemm_run_tail(q8, act, Ly.down, Ly.down_scales, M, H, I, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        } else if (gemm_run(q8, act, Ly.down, Ly.down_scales, proj, M, H, I, gemm, s) != hipSuccess) {
+            return HQ_ERR_LAUNCH;
+        }
     }
-    // the last layer's down output into the residual, final RMSNorm, tied LM
-    // head over the batch, per-sequence argmax and position advance
+    // the last layer's down output into the residual, final RMSNorm (in the
+    // last down GEMM's tail where it has one), tied LM head over the batch,
+    // per-sequence argmax and position advance
     rp.x = x;
     rp.add = proj;
     rp.gate_up = nullptr;
     rp.gamma = m->final_norm;
     rp.k = H;
-    if ((e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
+    if (!tails && (e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
     if (gemm_run(q8, act, m->embedding, m->embedding_scales, logits, M, m->vocab, H, gemm, s) != hipSuccess)
         return HQ_ERR_LAUNCH;
     hipLaunchKernelGGL(batch_argmax_kernel, dim3(L.arg_blocks, M), dim3(kBlock), 0, s, logits, m->vocab,
