@@ -56,9 +56,11 @@ struct GemmParams {
     float* pmax;
     // Tail launches (gemm_lds_kernel<..., TAIL = true>, the batched step's o
     // and down GEMMs): the outputs go to ll [m, n] as {value, epoch} entries
-    // (epoch = *epoch_ctr << 7 | epoch_id, unique per launch of a step), and
-    // block gridDim.x - m + s then finishes row s: the residual add into tx,
-    // RMSNorm with tgamma, quantization into tq (row stride tkq) and tact.
+    // (epoch = *epoch_ctr << 8 | epoch_id, unique per launch of a step), and
+    // the last blocks finish the rows: the residual add into x, RMSNorm with
+    // gamma and quantization into q / act (o, down: one block per row), or the
+    // quantization of the SwiGLU row with its maximum from the blocks' entries
+    // in pmax (gate_up: four blocks per row).
     GemmTail tail;
 };
 
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
 
 __device__ __forceinline__ uint32_t tail_epoch(const GemmTail& t)
 {
-    return (*t.epoch_ctr << 7) | uint32_t(t.epoch_id);
+    return (*t.epoch_ctr << 8) | uint32_t(t.epoch_id);
 }
 __device__ __forceinline__ bool tail_ready(uint64_t v, uint32_t ep)
 {
@@ -179,6 +181,10 @@ __device__ __forceinline__ bool tail_ready(uint64_t v, uint32_t ep)
 __device__ __forceinline__ uint64_t tail_load(const uint64_t* p)
 {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tail_store(uint64_t* p, float v, uint32_t ep)
+{
+    __hip_atomic_store(p, (uint64_t(ep) << 32) | uint64_t(f32_bits(v)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 constexpr unsigned kTailSpinLimit = 1u << 22;   // rounds a tail waits before it gives up (HQ_STEP_SYNC)
 
@@ -283,6 +289,76 @@ __device__ void gemm_tail_row(const GemmParams& p, int s, uint32_t ep, float* re
 // 1024-thread down launch has: they take the row kernel instead)
 constexpr int kTailNPT = 10;
 
+// Quarter qt of SwiGLU row s (values [qt*Q, qt*Q + Q), Q = 2560), by threads
+// 0-255 of one block: the row's maximum |value| over the launch's block
+// entries (order-free), then the same quantization as batch_act_quant_kernel
+// (amax floored at 1e-5, quant_i8 with 127 / amax, de-interleaved per 8,
+// act = amax / 127, written by quarter 0).
+constexpr int kSwigluTailQ = kBlock * 10;   // values per tail block: rows of up to 4 * 2560
+constexpr int kSwigluTailB = 3;             // block maxima per thread: up to 768 blocks
+__device__ void gemm_swiglu_tail_row(const GemmParams& p, int s, int qt, uint32_t ep, float* wmax)
+{
+    const GemmTail& T = p.tail;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int nb = int(gridDim.x);
+    const int n = p.n;
+    const bool on = tid < kBlock;
+    // this block's values, requested with the block maxima
+    const int i0 = qt * kSwigluTailQ + tid;
+    const uint64_t* vsrc = T.ll + size_t(s) * n;
+    const uint64_t ready = uint64_t(ep) << 32;
+    uint64_t e[10], mb[kSwigluTailB];
+    float mx = 0.0f;
+    if (on) {
+        unrolled<10>([&](auto j) {
+            const int i = i0 + kBlock * j;
+            e[j] = i < n ? tail_load(vsrc + i) : ready;
+        });
+        unrolled<kSwigluTailB>([&](auto j) {
+            const int b = tid + kBlock * j;
+            mb[j] = b < nb ? tail_load(T.pmax + size_t(b) * p.m + s) : ready;
+        });
+        unsigned spins = 0;
+        while (true) {
+            bool pending = false;
+            unrolled<kSwigluTailB>([&](auto j) { pending |= !tail_ready(mb[j], ep); });
+            unrolled<10>([&](auto j) { pending |= !tail_ready(e[j], ep); });
+            if (!pending) break;
+            if (++spins == kTailSpinLimit) {
+                atomicOr(T.table->status[s], HQ_STEP_SYNC);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            unrolled<kSwigluTailB>([&](auto j) {
+                if (!tail_ready(mb[j], ep)) mb[j] = tail_load(T.pmax + size_t(tid + kBlock * j) * p.m + s);
+            });
+            unrolled<10>([&](auto j) {
+                if (!tail_ready(e[j], ep)) e[j] = tail_load(vsrc + i0 + kBlock * j);
+            });
+        }
+        unrolled<kSwigluTailB>([&](auto j) {
+            if (tid + kBlock * j < nb) mx = fmaxf(mx, bits_f32(uint32_t(mb[j])));
+        });
+        mx = wave_max64_all(mx);
+        if (lane == 0) wmax[tid / kWave] = mx;
+    }
+    __syncthreads();
+    if (on) {
+        float amax = wmax[0];
+#pragma unroll
+        for (int w = 1; w < kBlock / kWave; ++w) amax = fmaxf(amax, wmax[w]);
+        amax = fmaxf(amax, 1e-5f);
+        const float inv = 127.0f / amax;
+        int8_t* qr = T.q + size_t(s) * T.kq;
+        unrolled<10>([&](auto j) {
+            const int i = i0 + kBlock * j;
+            if (i < n) qr[xq_offset(i)] = quant_i8(bits_f32(uint32_t(e[j])), inv);
+        });
+        if (qt == 0 && tid == 0) T.act[s] = amax / 127.0f;
+    }
+}
+
 // The same products with the weight rows staged through LDS, for rows of up
 // to HMAX packed bytes.  The block's R = 16 RG rows are one contiguous
 // R * K/2 byte range of the matrix; its threads read it in 16-byte chunks,
@@ -301,7 +377,7 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
 {
     static_assert(!SWIGLU || RG == 2, "a SwiGLU block pairs 16 gate rows with their 16 up rows");
     // TAIL: 0, or the values per thread of a tail row (rows of up to 256 * TAIL)
-    static_assert(!TAIL || (!SWIGLU && W >= 4), "a tail takes 256 threads of a plain launch");
+    static_assert(!TAIL || W >= 4, "a tail takes 256 threads of the block");
     constexpr int R = 16 * RG;
     constexpr int RS = HMAX + 16;                       // padded LDS row (bytes)
     constexpr int NRED = RG * BT * 4;                   // partial registers per lane
@@ -417,6 +493,7 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][(rg * BT + b) * 4 + r][lane] = acc[rg][b][r];
     lds_sync();
+    const uint32_t ep = TAIL ? tail_epoch(p.tail) : 0u;
     if constexpr (SWIGLU) {
         // element e: sequence e / 16, column e % 16 of the gate and up tiles;
         // the 16 columns of a sequence sit in one 16-lane row of a wave
@@ -439,14 +516,19 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
             const float t = 1.0f + spec_expf(-g);
             const float v = (g / t) * u;
             const bool ok = ml < p.m && rr < ng;
-            if (ok) p.out[size_t(ml) * p.n + g0 + rr] = v;
+            if (ok) {
+                if constexpr (TAIL) tail_store(p.tail.ll + size_t(ml) * p.n + g0 + rr, v, ep);
+                else p.out[size_t(ml) * p.n + g0 + rr] = v;
+            }
             float mx = ok ? fabsf(v) : 0.0f;
 #pragma unroll
             for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
-            if (rr == 0 && ml < p.m) p.pmax[size_t(blockIdx.x) * p.m + ml] = mx;
+            if (rr == 0 && ml < p.m) {
+                if constexpr (TAIL) tail_store(p.tail.pmax + size_t(blockIdx.x) * p.m + ml, mx, ep);
+                else p.pmax[size_t(blockIdx.x) * p.m + ml] = mx;
+            }
         }
     } else {
-        const uint32_t ep = TAIL ? tail_epoch(p.tail) : 0u;
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
             const int e = tid + kWave * W * i;
@@ -472,12 +554,14 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
         }
     }
     if constexpr (TAIL) {
-        const uint32_t ep = tail_epoch(p.tail);
-        const int s = int(blockIdx.x) - (int(gridDim.x) - p.m);
-        if (s >= 0) {   // (block-uniform)
-            __shared__ float t_red[kBlock];
-            __shared__ float t_wmax[kBlock / kWave];
-            gemm_tail_row<TAIL>(p, s, ep, t_red, t_wmax);
+        __shared__ float t_red[kBlock];
+        __shared__ float t_wmax[kBlock / kWave];
+        if constexpr (SWIGLU) {
+            const int u = int(blockIdx.x) - (int(gridDim.x) - 4 * p.m);
+            if (u >= 0) gemm_swiglu_tail_row(p, u % p.m, u / p.m, ep, t_wmax);   // (block-uniform)
+        } else {
+            const int s = int(blockIdx.x) - (int(gridDim.x) - p.m);
+            if (s >= 0) gemm_tail_row<TAIL>(p, s, ep, t_red, t_wmax);   // (block-uniform)
         }
     }
 }
@@ -707,6 +791,15 @@ static void launch_swiglu(const GemmParams& p, hipStream_t s)
 int gemm_swiglu_blocks(int n) { return (n + 15) / 16; }
 
 template <int W, int BT, int HMAX>
+static void launch_swiglu_tail(const GemmParams& p, hipStream_t s)
+{
+    constexpr int DS = (2 * HMAX / 128 + W - 1) / W;
+    constexpr int CPT = (32 * HMAX / 16 + kWave * W - 1) / (kWave * W);
+    hipLaunchKernelGGL((gemm_lds_kernel<2, W, BT, DS, CPT, HMAX, true, 1>), dim3((p.n + 15) / 16), dim3(kWave * W), 0,
+                       s, p);
+}
+
+template <int W, int BT, int HMAX>
 static void launch_tail(const GemmParams& p, hipStream_t s)
 {
     constexpr int DS = (2 * HMAX / 128 + W - 1) / W;
@@ -727,7 +820,7 @@ bool gemm_tail_fits(int m, int n, int k)
 hipError_t gemm_run_tail(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int m, int n, int k,
                          const GemmTail& tail, hipStream_t s)
 {
-    if (!gemm_tail_fits(m, n, k) || tail.epoch_id < 0 || tail.epoch_id >= 128) return hipErrorInvalidValue;
+    if (!gemm_tail_fits(m, n, k) || tail.epoch_id < 0 || tail.epoch_id >= 256) return hipErrorInvalidValue;
     GemmParams p{};
     p.m = m;
     p.x = x;
@@ -770,6 +863,36 @@ hipError_t gemm_run_swiglu(const int8_t* x, const float* act, const uint8_t* w, 
     }
     hipLaunchKernelGGL(batch_act_quant_kernel, dim3(m), dim3(kActQuantThreads), 0, s, act_out, pmax,
                        gemm_swiglu_blocks(n), m, n, kq, q, act_q);
+    return hipGetLastError();
+}
+
+bool gemm_swiglu_tail_fits(int m, int n, int k)
+{
+    return m >= 1 && m <= kMaxBatch && (k >> 1) <= 2048 && n <= 4 * kSwigluTailQ &&
+           gemm_swiglu_blocks(n) <= kBlock * kSwigluTailB && gemm_swiglu_blocks(n) >= 4 * m;
+}
+
+// gate_up with SwiGLU in the epilogue and the down input's quantization in
+// the tail (see GemmParams::tail; tail.ll holds [m, n] entries, tail.pmax
+// gemm_swiglu_blocks(n) * m).
+hipError_t gemm_run_swiglu_tail(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int m, int n,
+                                int k, const GemmTail& tail, hipStream_t s)
+{
+    if (!gemm_swiglu_tail_fits(m, n, k) || tail.epoch_id < 0 || tail.epoch_id >= 256) return hipErrorInvalidValue;
+    GemmParams p{};
+    p.m = m;
+    p.x = x;
+    p.act = act;
+    p.w = w; p.ws = ws;
+    p.n = n; p.k = k; p.kp = padded_k(k);
+    p.tail = tail;
+    if ((k >> 1) <= 1280) {
+        if (m > 16) launch_swiglu_tail<4, 2, 1280>(p, s);
+        else launch_swiglu_tail<4, 1, 1280>(p, s);
+    } else {
+        if (m > 16) launch_swiglu_tail<8, 2, 2048>(p, s);
+        else launch_swiglu_tail<8, 1, 2048>(p, s);
+    }
     return hipGetLastError();
 }
 

@@ -125,7 +125,7 @@ int gemm_swiglu_blocks(int n);
 struct GemmTail {
     uint64_t* ll;               // [m, n]
     const uint32_t* epoch_ctr;  // the step counter (bumped by the step's first kernel)
-    int epoch_id;               // 0 .. 127, unique per launch within a step
+    int epoch_id;               // 0 .. 255, unique per launch within a step
     float* x;                   // [m, n] residual rows, updated
     const float* gamma;         // [n]
     float eps;
@@ -133,8 +133,12 @@ struct GemmTail {
     int kq;
     float* act;                 // [m]
     const BatchTable* table;    // status words of the sequences
+    uint64_t* pmax;             // gate_up: [blocks, m] entries, each block's maximum |SwiGLU| per row
 };
 bool gemm_tail_fits(int m, int n, int k);
+bool gemm_swiglu_tail_fits(int m, int n, int k);
+hipError_t gemm_run_swiglu_tail(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int m, int n,
+                                int k, const GemmTail& tail, hipStream_t s);
 hipError_t gemm_run_tail(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int m, int n, int k,
                          const GemmTail& tail, hipStream_t s);
 hipError_t gemm_run(const int8_t* x, const float* act, const uint8_t* w, const float* ws, float* out, int m, int n,

@@ -440,7 +440,7 @@ __global__ __launch_bounds__(kBlock) void batch_store_x_kernel(const float* x, i
 
 struct BatchLayout {
     size_t x, q8, act, qkv, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, pmax, table, ll,
-        step_ctr, total;
+        pmax_ll, step_ctr, total;
     int kp, max_chunks, qkv_rows, qd, arg_blocks;
 };
 
@@ -478,7 +478,8 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.tickets = take(size_t(B) * ticket_words(L.arg_blocks) * 4);
     L.pmax = take(size_t(gemm_swiglu_blocks(I)) * B * 4);
     L.table = take(sizeof(BatchTable));
-    L.ll = take(size_t(B) * H * 8);
+    L.ll = take(size_t(B) * (H > I ? H : I) * 8);
+    L.pmax_ll = take(size_t(gemm_swiglu_blocks(I)) * B * 8);
     L.step_ctr = take(4);
     L.total = off;
     return L;
@@ -659,13 +660,14 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
     // (residual add, RMSNorm, quantization) where the shapes allow, instead
     // of a row kernel after them.
     const bool tails = m->layers <= 64 && gemm_tail_fits(M, H, L.qd) && gemm_tail_fits(M, H, I);
+    const bool swiglu_tail = tails && gemm_swiglu_tail_fits(M, I, H);
     GemmTail tl{};
+    tl.pmax = reinterpret_cast<uint64_t*>(ws + L.pmax_ll);
     tl.ll = reinterpret_cast<uint64_t*>(ws + L.ll);
     tl.epoch_ctr = step_ctr;
     tl.x = x;
     tl.eps = m->eps;
     tl.q = q8;
-    tl.kq = gemm_padded_k(H);
     tl.act = act;
     tl.table = table;
     for (int l = 0; l < m->layers; ++l) {
@@ -702,8 +704,9 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         a.kp = gemm_padded_k(L.qd);
         if (launch_batch_attention(a, s) != hipSuccess) return HQ_ERR_LAUNCH;
         if (tails) {
-            tl.epoch_id = 2 * l;
+            tl.epoch_id = 3 * l;
             tl.gamma = Ly.post_norm;
+            tl.kq = gemm_padded_k(H);
             if (gemm_run_tail(q8, act, Ly.o, Ly.o_scales, M, H, L.qd, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
         } else {
             if (gemm_run(q8, act, Ly.o, Ly.o_scales, proj, M, H, L.qd, gemm, s) != hipSuccess) return HQ_ERR_LAUNCH;
@@ -714,13 +717,21 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
             if ((e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
         }
         // gate_up with SwiGLU in its epilogue, then the down input's quant
-        if (gemm_run_swiglu(q8, act, Ly.gate_up, Ly.gate_up_scales, gu, M, I, H, reinterpret_cast<float*>(ws + L.pmax),
-                            q8, gemm_padded_k(I), act, s) != hipSuccess)
+        // (in its tail where it has one)
+        if (swiglu_tail) {
+            tl.epoch_id = 3 * l + 1;
+            tl.kq = gemm_padded_k(I);
+            if (gemm_run_swiglu_tail(q8, act, Ly.gate_up, Ly.gate_up_scales, M, I, H, tl, s) != hipSuccess)
+                return HQ_ERR_LAUNCH;
+        } else if (gemm_run_swiglu(q8, act, Ly.gate_up, Ly.gate_up_scales, gu, M, I, H,
+                                   reinterpret_cast<float*>(ws + L.pmax), q8, gemm_padded_k(I), act, s) != hipSuccess) {
             return HQ_ERR_LAUNCH;
+        }
         if (tails) {
             // the next layer's input rows (the final norm's after the last layer)
-            tl.epoch_id = 2 * l + 1;
+            tl.epoch_id = 3 * l + 2;
             tl.gamma = l + 1 < m->layers ? m->layer[l + 1].input_norm : m->final_norm;
+            tl.kq = gemm_padded_k(H);
             if (gemm_run_tail(q8, act, Ly.down, Ly.down_scales, M, H, I, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
         } else if (gemm_run(q8, act, Ly.down, Ly.down_scales, proj, M, H, I, gemm, s) != hipSuccess) {
             return HQ_ERR_LAUNCH;
