@@ -64,8 +64,8 @@ __device__ __forceinline__ void load_chunk(const AttnParams& a, const uint16_t* 
 // attention_combine_kernel combines them.  Either way the combine runs over
 // ascending chunks, so the result is the same bits.
 
-template <int D, int GMAX, bool STEP, int CPB>
-__global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
+template <int D, int GMAX, bool STEP, int CPB, bool TAILS>
+__device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep)
 {
     constexpr int C = kAttnChunk;
     constexpr int DPL = D / 16;
@@ -129,7 +129,6 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
     // per-query regions of a batch (blockIdx.z = 0 outside PLAIN batches)
     const size_t zq = size_t(blockIdx.z) * size_t(a.kv_heads) * G * D;
     float* const out = a.out + zq;
-    float* const part = a.part + size_t(blockIdx.z) * size_t(a.kv_heads) * G * a.max_chunks * (D + 2);
     const int nc = (n + C - 1) / C;
     const int nsplit = (nc + CPB - 1) / CPB;
     if (split >= nsplit) return;
@@ -338,7 +337,8 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
                 L = __builtin_fmaf(al, l_s[h][ci], L);
                 O = __builtin_fmaf(al, o_s[ci][h][d], O);
             }
-            out[size_t(g * G + h) * D + d] = O * (1.0f / L);
+            if constexpr (TAILS) tail_store(a.ll_out + zq + size_t(g * G + h) * D + d, O * (1.0f / L), ep);
+            else out[size_t(g * G + h) * D + d] = O * (1.0f / L);
         }
         return;
     }
@@ -350,12 +350,157 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
         for (int r = 0; r < PAIRS; ++r) {
             const int h = h0 + HSTEP * r;
             if (h >= G) continue;
-            float* pp = part + (size_t(g * G + h) * a.max_chunks + c) * pstride;
-            publish_f(pp + 2 + d, o_s[ci][h][d]);
-            if (d == 0) { publish_f(pp, m_s[h][ci]); publish_f(pp + 1, l_s[h][ci]); }
+            const size_t off = size_t(blockIdx.z) * size_t(a.kv_heads) * G * a.max_chunks * pstride +
+                               (size_t(g * G + h) * a.max_chunks + c) * pstride;
+            if constexpr (TAILS) {
+                uint64_t* pp = a.ll_part + off;
+                tail_store(pp + 2 + d, o_s[ci][h][d], ep);
+                if (d == 0) { tail_store(pp, m_s[h][ci], ep); tail_store(pp + 1, l_s[h][ci], ep); }
+            } else {
+                float* pp = a.part + off;
+                publish_f(pp + 2 + d, o_s[ci][h][d]);
+                if (d == 0) { publish_f(pp, m_s[h][ci]); publish_f(pp + 1, l_s[h][ci]); }
+            }
         }
     }
-    // (attention_combine_kernel, launched next on the stream, combines them)
+    // (attention_combine_kernel or batch_combine_quant_kernel, launched next
+    // on the stream, or this launch's tail combines them)
+}
+
+// Tail of a batched-step attention launch (TAILS): block (sequence s, part
+// qt) finishes heads [qt*HQ, qt*HQ + HQ) of sequence s (HQ = H/8, two heads
+// per pass of 256 threads, NO outputs per thread): each output is
+// the single split's entry, or the combine of the chunk partials exactly as
+// batch_combine_quant_kernel computes it (M = max of m_c; a_c = exp(m_c -
+// M); L and O fmaf chains over ascending c; out = O * (1 / L)).  The row's
+// maximum |out| is each part's maximum (order-free) handed between the
+// eight blocks as entries; then the same quantization (amax floored at 1e-5,
+// quant_i8 with 127 / amax, de-interleaved, act = amax / 127).
+constexpr int kAttnTailChunks = 8;   // contexts of up to 8 chunks (max_chunks <= 8)
+constexpr int kAttnTailParts = 8;    // tail blocks per sequence
+constexpr int kAttnTailNO = 2;       // outputs per thread: up to 2 * 2 * 8 = 32 query heads
+template <int D>
+__device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
+{
+    static_assert(D == kBlock / 2, "two heads per pass of the block");
+    constexpr int NO = kAttnTailNO;
+    constexpr int NC = kAttnTailChunks;
+    constexpr int pstride = D + 2;
+    __shared__ float ml_s[2 * NO][NC][2];
+    __shared__ float wmax_s[kBlock / kWave];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int d = tid % D, h0 = tid / D;
+    const int H = a.kv_heads * a.groups;
+    const int HQ = H / kAttnTailParts;
+    const int hb = qt * HQ;
+    const int cap = a.table->capacity[s];
+    const int n = min(max(*a.table->position[s], 0), cap - 1) + 1;
+    const int nc = (n + kAttnChunk - 1) / kAttnChunk;
+    const uint64_t ready = uint64_t(ep) << 32;
+    const size_t HD = size_t(H) * D;
+    int32_t* status = a.table->status[s];
+    float val[NO];
+    auto wait = [&](auto& e, auto&& reload) {
+        unsigned spins = 0;
+        while (true) {
+            bool pending = false;
+            unrolled<sizeof(e) / sizeof(e[0])>([&](auto j) { pending |= !tail_ready(e[j], ep); });
+            if (!pending) return;
+            if (++spins == kTailSpinLimit) {
+                atomicOr(status, HQ_STEP_SYNC);
+                return;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            unrolled<sizeof(e) / sizeof(e[0])>([&](auto j) {
+                if (!tail_ready(e[j], ep)) e[j] = reload(j);
+            });
+        }
+    };
+    if (nc <= a.cpb) {
+        // one split held every chunk of each head and combined them itself
+        uint64_t e[NO];
+        auto src = [&](auto i) { return a.ll_out + size_t(s) * HD + size_t(hb + h0 + 2 * i) * D + d; };
+        unrolled<NO>([&](auto i) { e[i] = h0 + 2 * i < HQ ? tail_load(src(i)) : ready; });
+        wait(e, [&](auto i) { return tail_load(src(i)); });
+        unrolled<NO>([&](auto i) { val[i] = h0 + 2 * i < HQ ? bits_f32(uint32_t(e[i])) : 0.0f; });
+    } else {
+        const uint64_t* base = a.ll_part + size_t(s) * size_t(H) * a.max_chunks * pstride;
+        // m_c and l_c of the part's heads: entry tid = (head, chunk, m|l)
+        {
+            uint64_t e[1];
+            const int hq = tid / (2 * NC), c = (tid / 2) % NC, kind = tid & 1;
+            const bool mine = hq < HQ && c < nc;
+            auto src = [&](auto) { return base + (size_t(hb + hq) * a.max_chunks + c) * pstride + kind; };
+            e[0] = mine ? tail_load(src(0)) : ready;
+            wait(e, [&](auto j) { return tail_load(src(j)); });
+            if (mine) ml_s[hq][c][kind] = bits_f32(uint32_t(e[0]));
+        }
+        // o_c[d] of this thread's heads
+        uint64_t o[NO * NC];
+        auto osrc = [&](auto j) {
+            const int i = int(j) / NC, c = int(j) % NC;
+            return base + (size_t(hb + h0 + 2 * i) * a.max_chunks + c) * pstride + 2 + d;
+        };
+        unrolled<NO * NC>([&](auto j) {
+            o[j] = (h0 + 2 * (int(j) / NC) < HQ && int(j) % NC < nc) ? tail_load(osrc(j)) : ready;
+        });
+        wait(o, [&](auto j) { return tail_load(osrc(j)); });
+        __syncthreads();   // ml_s
+        unrolled<NO>([&](auto i) {
+            const int hq = h0 + 2 * i;
+            if (hq < HQ) {
+                float M = ml_s[hq][0][0];
+                for (int c = 1; c < nc; ++c) M = fmaxf(M, ml_s[hq][c][0]);
+                float L = 0.0f, O = 0.0f;
+                unrolled<NC>([&](auto c) {
+                    if (c < nc) {
+                        const float al = spec_expf(ml_s[hq][c][0] - M);
+                        L = __builtin_fmaf(al, ml_s[hq][c][1], L);
+                        O = __builtin_fmaf(al, bits_f32(uint32_t(o[i * NC + c])), O);
+                    }
+                });
+                val[i] = O * (1.0f / L);
+            } else {
+                val[i] = 0.0f;
+            }
+        });
+    }
+    // the row's maximum: this part's, then the eight parts'
+    float mx = 0.0f;
+    unrolled<NO>([&](auto i) { mx = fmaxf(mx, fabsf(val[i])); });
+    mx = wave_max64_all(mx);
+    if (lane == 0) wmax_s[tid / kWave] = mx;
+    __syncthreads();
+    if (tid == 0) {
+        float qm = wmax_s[0];
+        for (int w = 1; w < kBlock / kWave; ++w) qm = fmaxf(qm, wmax_s[w]);
+        tail_store(a.ll_max + size_t(s) * kAttnTailParts + qt, qm, ep);
+    }
+    uint64_t qe[kAttnTailParts];
+    unrolled<kAttnTailParts>([&](auto q) { qe[q] = tail_load(a.ll_max + size_t(s) * kAttnTailParts + q); });
+    wait(qe, [&](auto q) { return tail_load(a.ll_max + size_t(s) * kAttnTailParts + q); });
+    float amax = bits_f32(uint32_t(qe[0]));
+    unrolled<kAttnTailParts - 1>([&](auto q) { amax = fmaxf(amax, bits_f32(uint32_t(qe[q + 1]))); });
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+    int8_t* qr = a.q8 + size_t(s) * a.kp;
+    unrolled<NO>([&](auto i) {
+        if (h0 + 2 * i < HQ) qr[xq_offset((hb + h0 + 2 * i) * D + d)] = quant_i8(val[i], inv);
+    });
+    if (qt == 0 && tid == 0) a.act[s] = amax / 127.0f;
+}
+
+template <int D, int GMAX, bool STEP, int CPB, bool TAILS = false>
+__global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
+{
+    const uint32_t ep = TAILS ? (*a.epoch_ctr << 8) | uint32_t(a.epoch_id) : 0u;
+    attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep);
+    if constexpr (TAILS) {
+        const int lin = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+        const int u = lin - int(gridDim.x * gridDim.y * gridDim.z) + kAttnTailParts * a.batch;
+        if (u >= 0) attention_tail<D>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
+    }
 }
 
 // Combine of the chunk partials when a context spans several chunks: thread
@@ -646,6 +791,15 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
     AttnParams b = a;
     b.cpb = a.kv_heads * a.max_chunks * a.batch <= 1024 ? 1 : 2;
     const dim3 grid(a.kv_heads, (a.max_chunks + b.cpb - 1) / b.cpb, a.batch);
+    const int H = a.kv_heads * a.groups;
+    if (a.ll_part && a.ll_out && a.ll_max && a.epoch_ctr && a.epoch_id >= 0 && a.epoch_id < 256 &&
+        a.max_chunks <= kAttnTailChunks && a.groups <= 4 && H % (2 * kAttnTailParts) == 0 &&
+        H <= 2 * kAttnTailNO * kAttnTailParts && int(grid.x * grid.y * grid.z) >= kAttnTailParts * a.batch) {
+        // the combine and quantization in the launch's last blocks
+        if (b.cpb == 1) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1, true>), grid, dim3(kBlock), 0, s, b);
+        else hipLaunchKernelGGL((attention_kernel<128, 4, false, 2, true>), grid, dim3(kBlock), 0, s, b);
+        return hipGetLastError();
+    }
     if (b.cpb == 1) {
         if (a.groups <= 4) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1>), grid, dim3(kBlock), 0, s, b);
         else hipLaunchKernelGGL((attention_kernel<128, 8, false, 1>), grid, dim3(kBlock), 0, s, b);

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace hq {
 
 constexpr int kBlock = 256;   // threads per block for every hq kernel
@@ -318,6 +320,39 @@ __device__ __forceinline__ int8_t quant_i8(float v, float inv)
     float q = __builtin_rintf(v * inv);
     q = fminf(fmaxf(q, -127.0f), 127.0f);
     return static_cast<int8_t>(static_cast<int>(q));
+}
+
+// ---- {value, epoch} entries of the batched step's launch tails -------------------
+//
+// A launch's blocks hand values to its last blocks as 64-bit entries, the
+// value's bits in the low word and the launch's epoch in the high word,
+// with agent-scope stores and loads (no fences): an entry is current when
+// its epoch is not older than the launch's.
+
+__device__ __forceinline__ bool tail_ready(uint64_t v, uint32_t ep)
+{
+    return int32_t(uint32_t(v >> 32) - ep) >= 0;
+}
+__device__ __forceinline__ uint64_t tail_load(const uint64_t* p)
+{
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tail_store(uint64_t* p, float v, uint32_t ep)
+{
+    __hip_atomic_store(p, (uint64_t(ep) << 32) | uint64_t(f32_bits(v)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr unsigned kTailSpinLimit = 1u << 22;   // rounds a tail waits before it gives up (HQ_STEP_SYNC)
+
+// f(0) .. f(N-1) with compile-time indices (register arrays stay in registers)
+template <class F, int... J>
+__device__ __forceinline__ void unrolled_impl(F&& f, std::integer_sequence<int, J...>)
+{
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void unrolled(F&& f)
+{
+    unrolled_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 }  // namespace hq

@@ -22,8 +22,6 @@
 // (each a contiguous range of double steps, all of its loads in flight at
 // once) and their int32 partial tiles meet in LDS, so no split of K crosses
 // blocks: no atomics, no arrival tickets, no zeroed workspace.
-#include <utility>
-
 #include "hq_device.h"
 #include "hq_internal.h"
 
@@ -174,31 +172,7 @@ __device__ __forceinline__ uint32_t tail_epoch(const GemmTail& t)
 {
     return (*t.epoch_ctr << 8) | uint32_t(t.epoch_id);
 }
-__device__ __forceinline__ bool tail_ready(uint64_t v, uint32_t ep)
-{
-    return int32_t(uint32_t(v >> 32) - ep) >= 0;
-}
-__device__ __forceinline__ uint64_t tail_load(const uint64_t* p)
-{
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void tail_store(uint64_t* p, float v, uint32_t ep)
-{
-    __hip_atomic_store(p, (uint64_t(ep) << 32) | uint64_t(f32_bits(v)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-constexpr unsigned kTailSpinLimit = 1u << 22;   // rounds a tail waits before it gives up (HQ_STEP_SYNC)
 
-// f(0) .. f(N-1) with compile-time indices (register arrays stay in registers)
-template <class F, int... J>
-__device__ __forceinline__ void unrolled_impl(F&& f, std::integer_sequence<int, J...>)
-{
-    (f(std::integral_constant<int, J>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void unrolled(F&& f)
-{
-    unrolled_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 // Row s of a tail launch, by threads 0-255 of one block (the others only
 // take the barriers): once every block's entry of the row is current (each

@@ -97,6 +97,15 @@ struct AttnParams {
     float* act;
     int kp;
     int cpb;                    // chunks per attention block (set by launch_batch_attention)
+    // Batched-step tails (nullable): the chunk partials and single-split
+    // outputs go out as {value, epoch} entries (epoch = *epoch_ctr << 8 |
+    // epoch_id) and the launch's last 8 * batch blocks combine and quantize
+    // the rows, an eighth of the heads each, in place of the combine kernel.
+    uint64_t* ll_part;          // [batch, heads, max_chunks, D + 2]
+    uint64_t* ll_out;           // [batch, heads * D]
+    uint64_t* ll_max;           // [batch, 8] the parts' maxima
+    const uint32_t* epoch_ctr;
+    int epoch_id;
 };
 
 size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);

@@ -440,7 +440,7 @@ __global__ __launch_bounds__(kBlock) void batch_store_x_kernel(const float* x, i
 
 struct BatchLayout {
     size_t x, q8, act, qkv, att, proj, gu, gemm, attn_part, logits, pval, pidx, tickets, pmax, table, ll,
-        pmax_ll, step_ctr, total;
+        pmax_ll, ll_part, ll_out, ll_max, step_ctr, total;
     int kp, max_chunks, qkv_rows, qd, arg_blocks;
 };
 
@@ -479,6 +479,9 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.pmax = take(size_t(gemm_swiglu_blocks(I)) * B * 4);
     L.table = take(sizeof(BatchTable));
     L.ll = take(size_t(B) * (H > I ? H : I) * 8);
+    L.ll_part = take(size_t(B) * attention_workspace_floats(m->heads, L.max_chunks, D) * 8);
+    L.ll_out = take(size_t(B) * L.qd * 8);
+    L.ll_max = take(size_t(B) * 8 * 8);
     L.pmax_ll = take(size_t(gemm_swiglu_blocks(I)) * B * 8);
     L.step_ctr = take(4);
     L.total = off;
@@ -702,9 +705,16 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         a.q8 = q8;
         a.act = act;
         a.kp = gemm_padded_k(L.qd);
+        if (tails) {
+            a.ll_part = reinterpret_cast<uint64_t*>(ws + L.ll_part);
+            a.ll_out = reinterpret_cast<uint64_t*>(ws + L.ll_out);
+            a.ll_max = reinterpret_cast<uint64_t*>(ws + L.ll_max);
+            a.epoch_ctr = step_ctr;
+            a.epoch_id = 4 * l + 3;
+        }
         if (launch_batch_attention(a, s) != hipSuccess) return HQ_ERR_LAUNCH;
         if (tails) {
-            tl.epoch_id = 3 * l;
+            tl.epoch_id = 4 * l;
             tl.gamma = Ly.post_norm;
             tl.kq = gemm_padded_k(H);
             if (gemm_run_tail(q8, act, Ly.o, Ly.o_scales, M, H, L.qd, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
@@ -719,7 +729,7 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         // gate_up with SwiGLU in its epilogue, then the down input's quant
         // (in its tail where it has one)
         if (swiglu_tail) {
-            tl.epoch_id = 3 * l + 1;
+            tl.epoch_id = 4 * l + 1;
             tl.kq = gemm_padded_k(I);
             if (gemm_run_swiglu_tail(q8, act, Ly.gate_up, Ly.gate_up_scales, M, I, H, tl, s) != hipSuccess)
                 return HQ_ERR_LAUNCH;
@@ -729,7 +739,7 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         }
         if (tails) {
             // the next layer's input rows (the final norm's after the last layer)
-            tl.epoch_id = 3 * l + 2;
+            tl.epoch_id = 4 * l + 2;
             tl.gamma = l + 1 < m->layers ? m->layer[l + 1].input_norm : m->final_norm;
             tl.kq = gemm_padded_k(H);
             if (gemm_run_tail(q8, act, Ly.down, Ly.down_scales, M, H, I, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
