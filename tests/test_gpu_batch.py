@@ -106,19 +106,21 @@ def qwen():
     return model
 
 
-@pytest.mark.parametrize("m", [8, 32])
-def test_qwen3_4b_batch_matches_single_steps(qwen, m):
+@pytest.mark.parametrize("m,big", [(8, False), (32, False), (8, True)])
+def test_qwen3_4b_batch_matches_single_steps(qwen, m, big):
     # M sequences with histories of 1 .. 300 positions (one to five chunks
-    # of attention, one to two chunk groups), stepped together and alone
+    # of attention, one to two chunk groups), stepped together and alone;
+    # with `big` one state holds 600 positions (more than eight chunks: the
+    # attention's chunk partials go through the separate combine kernel)
     model = qwen
     rng = np.random.default_rng(100 + m)
     lengths = [int(v) for v in rng.integers(1, 300, m)]
     lengths[0], lengths[-1] = 1, 300
     prompts = [[int(t) for t in rng.integers(0, 151936, n)] for n in lengths]
     A, B = [], []
-    for pr in prompts:
+    for i, pr in enumerate(prompts):
         for group in (A, B):
-            st = model.new_state(len(pr) + 4)
+            st = model.new_state(600 if big and i == 1 else len(pr) + 4)
             model.prefill(pr, st)
             group.append(st)
     nxt = [int(t) for t in rng.integers(0, 151936, m)]
