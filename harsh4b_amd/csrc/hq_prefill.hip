@@ -24,7 +24,13 @@
 // workspace), then the final RMSNorm, the tied LM head as one GEMM over the
 // batch and a per-sequence argmax that feeds each greedy token back on the
 // device: M forward_token steps (cpu_lightspark.py:424-468) sharing every
-// weight read, bit-identical to them.
+// weight read, bit-identical to them.  Where the shapes allow, each layer is
+// five launches: the qkv GEMM; the attention, whose last blocks combine and
+// quantize each sequence's row; the o GEMM, whose last blocks add the
+// residual and run the post-attention norm and quantization; the gate_up
+// GEMM with SwiGLU, whose last blocks quantize the down input; the down
+// GEMM, whose last blocks add the residual and run the next layer's input
+// norm (the row, combine and quantization kernels otherwise).
 #include <algorithm>
 
 #include "hq_device.h"
