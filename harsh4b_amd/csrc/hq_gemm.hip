@@ -263,6 +263,13 @@ __device__ void gemm_tail_row(const GemmParams& p, int s, uint32_t ep, float* re
 // 1024-thread down launch has: they take the row kernel instead)
 constexpr int kTailNPT = 10;
 
+// Blocks of a tail launch that compute tiles (the rest finish rows).
+template <bool SWIGLU>
+__device__ __forceinline__ int tail_tiles(const GemmParams& p)
+{
+    return int(gridDim.x) - (SWIGLU ? 4 : 1) * p.m;
+}
+
 // Quarter qt of SwiGLU row s (values [qt*Q, qt*Q + Q), Q = 2560), by threads
 // 0-255 of one block: the row's maximum |value| over the launch's block
 // entries (order-free), then the same quantization as batch_act_quant_kernel
@@ -275,7 +282,7 @@ __device__ void gemm_swiglu_tail_row(const GemmParams& p, int s, int qt, uint32_
     const GemmTail& T = p.tail;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int nb = int(gridDim.x);
+    const int nb = tail_tiles<true>(p);   // the tile blocks' maxima
     const int n = p.n;
     const bool on = tid < kBlock;
     // this block's values, requested with the block maxima
@@ -359,6 +366,19 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
     static_assert(CPT * kWave * W * 16 >= R * HMAX, "the chunks of a thread cover the block's rows");
     static_assert(DS * W * 128 >= 2 * HMAX, "one round of B loads covers a wave's double steps");
     __shared__ __align__(16) uint8_t a_s[R * RS];
+    if constexpr (TAIL) {
+        // the launch's last blocks (after every tile's block, so each block
+        // they wait for has started) only finish rows: one per row (o,
+        // down) or four per row (gate_up)
+        const int u = int(blockIdx.x) - tail_tiles<SWIGLU>(p);
+        if (u >= 0) {   // (block-uniform)
+            __shared__ float t_red[kBlock];
+            __shared__ float t_wmax[kBlock / kWave];
+            if constexpr (SWIGLU) gemm_swiglu_tail_row(p, u % p.m, u / p.m, tail_epoch(p.tail), t_wmax);
+            else gemm_tail_row<TAIL>(p, u, tail_epoch(p.tail), t_red, t_wmax);
+            return;
+        }
+    }
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid & (kWave - 1);
@@ -525,17 +545,6 @@ __global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
                     if (p.acc_out) p.acc_out[size_t(mm) * p.n + n] = a;
                 }
             }
-        }
-    }
-    if constexpr (TAIL) {
-        __shared__ float t_red[kBlock];
-        __shared__ float t_wmax[kBlock / kWave];
-        if constexpr (SWIGLU) {
-            const int u = int(blockIdx.x) - (int(gridDim.x) - 4 * p.m);
-            if (u >= 0) gemm_swiglu_tail_row(p, u % p.m, u / p.m, ep, t_wmax);   // (block-uniform)
-        } else {
-            const int s = int(blockIdx.x) - (int(gridDim.x) - p.m);
-            if (s >= 0) gemm_tail_row<TAIL>(p, s, ep, t_red, t_wmax);   // (block-uniform)
         }
     }
 }
@@ -769,8 +778,8 @@ static void launch_swiglu_tail(const GemmParams& p, hipStream_t s)
 {
     constexpr int DS = (2 * HMAX / 128 + W - 1) / W;
     constexpr int CPT = (32 * HMAX / 16 + kWave * W - 1) / (kWave * W);
-    hipLaunchKernelGGL((gemm_lds_kernel<2, W, BT, DS, CPT, HMAX, true, 1>), dim3((p.n + 15) / 16), dim3(kWave * W), 0,
-                       s, p);
+    hipLaunchKernelGGL((gemm_lds_kernel<2, W, BT, DS, CPT, HMAX, true, 1>), dim3((p.n + 15) / 16 + 4 * p.m),
+                       dim3(kWave * W), 0, s, p);
 }
 
 template <int W, int BT, int HMAX>
@@ -778,7 +787,7 @@ static void launch_tail(const GemmParams& p, hipStream_t s)
 {
     constexpr int DS = (2 * HMAX / 128 + W - 1) / W;
     constexpr int CPT = (16 * HMAX / 16 + kWave * W - 1) / (kWave * W);
-    hipLaunchKernelGGL((gemm_lds_kernel<1, W, BT, DS, CPT, HMAX, false, kTailNPT>), dim3((p.n + 15) / 16),
+    hipLaunchKernelGGL((gemm_lds_kernel<1, W, BT, DS, CPT, HMAX, false, kTailNPT>), dim3((p.n + 15) / 16 + p.m),
                        dim3(kWave * W), 0, s, p);
 }
 
