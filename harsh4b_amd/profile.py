@@ -129,14 +129,21 @@ def part_trace(ctx, seed, reps=4):
         has_att = (tr[:, 0, 48] != 0) & (tr[:, 0, 53] != 0)     # the blocks that ran a GQA item
     per_layer = []
     for L in range(TRACE_LAYERS - 1):
-        rel = (tr[:, L, :] - tr[:, L, 0:1]) / 100.0            # 100 MHz clock -> us
+        # every block's points from one origin, the median layer start (the
+        # blocks that run attention items start a layer earlier than the
+        # others: they hold no hidden rows); a point's median is taken over
+        # the blocks that recorded it (a block that skips a phase leaves 0)
+        origin = np.median(tr[:, L, 0])
+        rel = (tr[:, L, :] - origin) / 100.0                   # 100 MHz clock -> us
         end = (tr[:, L + 1, 0] - tr[:, L, 0]) / 100.0
 
         def med(point):
             if point == "end":
-                return float(np.median(end))
-            col = rel[has_att, point] if point in ATTENTION_POINTS else rel[:, point]
-            return float(np.median(col))
+                return float((np.median(tr[:, L + 1, 0]) - origin) / 100.0)
+            sel = tr[:, L, point] != 0
+            if point in ATTENTION_POINTS:
+                sel &= has_att
+            return float(np.median(rel[sel, point]))
         segs = [(a, b, cat, what, med(b) - med(a)) for a, b, cat, what in segments]
         per_layer.append({"layer": TRACE_L0 + L, "us": float(np.median(end)), "segments": segs})
     return {"context": int(state.device_position.item()) + 1, "blocks": nb,
