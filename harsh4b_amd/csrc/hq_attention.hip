@@ -25,8 +25,7 @@
 //           ascending c; out = O * (1 / L).
 #include <mutex>
 
-#include "hq_device.h"
-#include "hq_internal.h"
+#include "hq_gemm_block.h"
 
 namespace hq {
 
@@ -64,26 +63,63 @@ __device__ __forceinline__ void load_chunk(const AttnParams& a, const uint16_t* 
 // attention_combine_kernel combines them.  Either way the combine runs over
 // ascending chunks, so the result is the same bits.
 
-template <int D, int GMAX, bool STEP, int CPB, bool TAILS>
-__device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep)
+// The LDS of one attention block.
+template <int D, int GMAX, int CPB>
+struct AttnLds {
+    float q_s[GMAX][D];
+    alignas(16) uint16_t k_s[kAttnChunk * ChunkTile<D>::kRowHalves];
+    alignas(16) uint16_t v_s[kAttnChunk * ChunkTile<D>::kRowHalves];
+    uint16_t kc_s[D];
+    uint16_t vc_s[D];
+    float e_s[GMAX][kAttnChunk];
+    float m_s[GMAX][CPB];
+    float l_s[GMAX][CPB];
+    float o_s[CPB][GMAX][D];   // per-chunk V partials
+};
+
+// Block (bx, by, bz) = (kv head, split, query) of an attention launch.
+// Two raw-projection values (dims lane and lane + 64 at p) from {value,
+// epoch} entries, once both are current (bounded wait).
+__device__ __forceinline__ void poll_pair(const uint64_t* p, uint32_t ep, int32_t* status, float& x0, float& x1)
+{
+    uint64_t e0 = tail_load(p), e1 = tail_load(p + 64);
+    unsigned spins = 0;
+    while (!(tail_ready(e0, ep) && tail_ready(e1, ep))) {
+        if (++spins == kTailSpinLimit) {
+            atomicOr(status, HQ_STEP_SYNC);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        if (!tail_ready(e0, ep)) e0 = tail_load(p);
+        if (!tail_ready(e1, ep)) e1 = tail_load(p + 64);
+    }
+    x0 = bits_f32(uint32_t(e0));
+    x1 = bits_f32(uint32_t(e1));
+}
+
+// QLL: the raw projection comes as {value, epoch} entries from the qkv GEMM
+// blocks of the same launch (a.qkv_ll) instead of the qkv buffer.
+template <int D, int GMAX, bool STEP, int CPB, bool TAILS, bool QLL = false>
+__device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep, AttnLds<D, GMAX, CPB>& lds,
+                                                int bx, int by, int bz)
 {
     constexpr int C = kAttnChunk;
     constexpr int DPL = D / 16;
     constexpr int PAIRS = (GMAX * D + kBlock - 1) / kBlock;   // (head, dim) pairs per thread
     constexpr int HSTEP = kBlock / D;                          // heads between a thread's pairs
     using T = ChunkTile<D>;
-    __shared__ float q_s[GMAX][D];
-    __shared__ __align__(16) uint16_t k_s[C * T::kRowHalves];
-    __shared__ __align__(16) uint16_t v_s[C * T::kRowHalves];
-    __shared__ uint16_t kc_s[D];
-    __shared__ uint16_t vc_s[D];
-    __shared__ float e_s[GMAX][C];
-    __shared__ float m_s[GMAX][CPB];
-    __shared__ float l_s[GMAX][CPB];
-    __shared__ float o_s[CPB][GMAX][D];   // per-chunk V partials
+    auto& q_s = lds.q_s;
+    auto& k_s = lds.k_s;
+    auto& v_s = lds.v_s;
+    auto& kc_s = lds.kc_s;
+    auto& vc_s = lds.vc_s;
+    auto& e_s = lds.e_s;
+    auto& m_s = lds.m_s;
+    auto& l_s = lds.l_s;
+    auto& o_s = lds.o_s;
 
-    const int g = blockIdx.x;
-    const int split = blockIdx.y;
+    const int g = bx;
+    const int split = by;
     const int G = a.groups;
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
@@ -99,7 +135,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
         n = pos + 1;
     } else {
         pos = -1;
-        n = a.context + int(blockIdx.z);     // query z of a batch sees z more positions
+        n = a.context + bz;     // query z of a batch sees z more positions
     }
     uint16_t* keys = a.keys;
     uint16_t* values = a.values;
@@ -109,7 +145,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
     if (!STEP && a.table) {
         // batched decode: query z is sequence z at its own position, in its
         // own cache (its layer slab: capacity * kv_heads * D elements)
-        const int z = blockIdx.z;
+        const int z = bz;
         const int zpos = *a.table->position[z];
         const int cap = a.table->capacity[z];
         n = min(max(zpos, 0), cap - 1) + 1;
@@ -126,8 +162,23 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
             qkv = a.qkv + size_t(z) * size_t(a.kv_heads) * size_t(G + 2) * D;
         }
     }
-    // per-query regions of a batch (blockIdx.z = 0 outside PLAIN batches)
-    const size_t zq = size_t(blockIdx.z) * size_t(a.kv_heads) * G * D;
+    const uint64_t* qll = nullptr;
+    int32_t* zstatus = nullptr;
+    if constexpr (QLL) {
+        qll = a.qkv_ll + size_t(bz) * size_t(a.kv_heads) * size_t(G + 2) * D;
+        zstatus = a.table->status[bz];
+    }
+    // dims lane and lane + 64 of raw-projection row `row`
+    auto raw2 = [&](size_t row, float& x0, float& x1) {
+        if constexpr (QLL) {
+            poll_pair(qll + row * D + lane, ep, zstatus, x0, x1);
+        } else {
+            x0 = qkv[row * D + lane];
+            x1 = qkv[row * D + lane + 64];
+        }
+    };
+    // per-query regions of a batch (bz = 0 outside PLAIN batches)
+    const size_t zq = size_t(bz) * size_t(a.kv_heads) * G * D;
     float* const out = a.out + zq;
     const int nc = (n + C - 1) / C;
     const int nsplit = (nc + CPB - 1) / CPB;
@@ -152,8 +203,8 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
         const float* cs = a.rope_cos + size_t(pos) * (D / 2);
         const float* sn = a.rope_sin + size_t(pos) * (D / 2);
         for (int h = wave; h < G; h += kBlock / kWave) {
-            const float* src = qkv + size_t(g * G + h) * D;
-            const float x0 = src[lane], x1 = src[lane + 64];
+            float x0, x1;
+            raw2(size_t(g * G + h), x0, x1);
             float p = __builtin_fmaf(x0, x0, 0.0f);
             p = __builtin_fmaf(x1, x1, p);
             const float ss = wave_tree_sum64_all(p);
@@ -169,8 +220,8 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
             uint16_t* kdst = keys + size_t(pos) * a.time_stride + kv_off;
             uint16_t* vdst = values + size_t(pos) * a.time_stride + kv_off;
             if (wave == 0) {
-                const float* src = qkv + size_t(heads + g) * D;
-                const float x0 = src[lane], x1 = src[lane + 64];
+                float x0, x1;
+                raw2(size_t(heads + g), x0, x1);
                 float p = __builtin_fmaf(x0, x0, 0.0f);
                 p = __builtin_fmaf(x1, x1, p);
                 const float ss = wave_tree_sum64_all(p);
@@ -185,9 +236,10 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
                 kc_s[lane] = h0;
                 kc_s[lane + 64] = h1;
             } else if (wave == 1) {
-                const float* src = qkv + size_t(heads + a.kv_heads + g) * D;
-                const uint16_t h0 = f32_to_f16(src[lane]);
-                const uint16_t h1 = f32_to_f16(src[lane + 64]);
+                float x0, x1;
+                raw2(size_t(heads + a.kv_heads + g), x0, x1);
+                const uint16_t h0 = f32_to_f16(x0);
+                const uint16_t h1 = f32_to_f16(x1);
                 vdst[lane] = h0;
                 vdst[lane + 64] = h1;
                 vc_s[lane] = h0;
@@ -350,7 +402,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
         for (int r = 0; r < PAIRS; ++r) {
             const int h = h0 + HSTEP * r;
             if (h >= G) continue;
-            const size_t off = size_t(blockIdx.z) * size_t(a.kv_heads) * G * a.max_chunks * pstride +
+            const size_t off = size_t(bz) * size_t(a.kv_heads) * G * a.max_chunks * pstride +
                                (size_t(g * G + h) * a.max_chunks + c) * pstride;
             if constexpr (TAILS) {
                 uint64_t* pp = a.ll_part + off;
@@ -494,13 +546,44 @@ __device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
 template <int D, int GMAX, bool STEP, int CPB, bool TAILS = false>
 __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
 {
+    __shared__ AttnLds<D, GMAX, CPB> lds;
     const uint32_t ep = TAILS ? (*a.epoch_ctr << 8) | uint32_t(a.epoch_id) : 0u;
-    attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep);
+    attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep, lds, int(blockIdx.x), int(blockIdx.y), int(blockIdx.z));
     if constexpr (TAILS) {
         const int lin = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
         const int u = lin - int(gridDim.x * gridDim.y * gridDim.z) + kAttnTailParts * a.batch;
         if (u >= 0) attention_tail<D>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
     }
+}
+
+// The batched step's qkv GEMM and attention in one launch: blocks [0, tiles)
+// compute the qkv rows (gemm_lds_block, K up to 2560) into {value, epoch}
+// entries; the blocks after them are the attention launch's blocks (kv head,
+// split, sequence; gy splits) with their tails, and take the raw projection
+// from those entries.  Every block an attention block waits for has started
+// before it (blocks start in index order).  One LDS buffer serves either role.
+template <int RG, int BT, int CPB>
+__global__ __launch_bounds__(kBlock) void qkv_attention_kernel(GemmParams gp, AttnParams a, int tiles, int gy)
+{
+    constexpr int HMAX = 1280;
+    constexpr int R = 16 * RG;
+    constexpr int DS = (2 * HMAX / 128 + 3) / 4;
+    constexpr int CPT = (R * HMAX / 16 + kBlock - 1) / kBlock;
+    union Lds {
+        alignas(16) uint8_t gemm[R * (HMAX + 16)];
+        AttnLds<128, 4, CPB> at;
+    };
+    __shared__ Lds lds;
+    if (int(blockIdx.x) < tiles) {   // (block-uniform)
+        gemm_lds_block<RG, 4, BT, DS, CPT, HMAX, false, -1>(gp, lds.gemm);
+        return;
+    }
+    const uint32_t ep = (*a.epoch_ctr << 8) | uint32_t(a.epoch_id);
+    const int k = int(blockIdx.x) - tiles;
+    const int gx = a.kv_heads;
+    attention_block<128, 4, false, CPB, true, true>(a, ep, lds.at, k % gx, (k / gx) % gy, k / (gx * gy));
+    const int u = k - gx * gy * a.batch + kAttnTailParts * a.batch;
+    if (u >= 0) attention_tail<128>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
 }
 
 // Combine of the chunk partials when a context spans several chunks: thread
@@ -808,6 +891,39 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
         else hipLaunchKernelGGL((attention_kernel<128, 8, false, 2>), grid, dim3(kBlock), 0, s, b);
     }
     hipLaunchKernelGGL(batch_combine_quant_kernel<128>, dim3(a.batch), dim3(kCombineThreads), 0, s, b);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_qkv_attention(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int k,
+                                      const AttnParams& a, hipStream_t s)
+{
+    const int H = a.kv_heads * a.groups;
+    const int rows = (H + 2 * a.kv_heads) * a.head_dim;
+    if (!a.qkv_ll || !a.ll_part || !a.ll_out || !a.ll_max || !a.epoch_ctr || a.epoch_id < 0 || a.epoch_id >= 256 ||
+        a.head_dim != 128 || !a.table || !a.qkv || !a.q8 || !a.act || a.batch < 1 || a.batch > 16 ||
+        a.max_chunks > kAttnTailChunks || a.groups > 4 || H % (2 * kAttnTailParts) != 0 ||
+        H > 2 * kAttnTailNO * kAttnTailParts || (k >> 1) > 1280 || (k & 31))
+        return hipErrorNotSupported;
+    AttnParams b = a;
+    b.cpb = a.kv_heads * a.max_chunks * a.batch <= 1024 ? 1 : 2;
+    const int gy = (a.max_chunks + b.cpb - 1) / b.cpb;
+    if (a.kv_heads * gy * a.batch < kAttnTailParts * a.batch) return hipErrorNotSupported;
+    GemmParams p{};
+    p.m = a.batch;
+    p.x = x;
+    p.act = act;
+    p.w = w; p.ws = ws;
+    p.n = rows; p.k = k; p.kp = gemm_padded_k(k);
+    p.tail.ll = a.qkv_ll;
+    p.tail.epoch_ctr = a.epoch_ctr;
+    p.tail.epoch_id = a.epoch_id;
+    // one 16-wide sequence tile, 16 rows per block (at M = 32 the launch's
+    // 960 blocks did not all fit on the chip at once: 3.08 -> 3.24 ms per
+    // step, where M = 8 gained 2.04 -> 1.93 ms)
+    const int tiles = (rows + 15) / 16;
+    const dim3 grid(tiles + a.kv_heads * gy * a.batch);
+    if (b.cpb == 1) hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 1>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
+    else hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 2>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
     return hipGetLastError();
 }
 

@@ -484,7 +484,7 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.tickets = take(size_t(B) * ticket_words(L.arg_blocks) * 4);
     L.pmax = take(size_t(gemm_swiglu_blocks(I)) * B * 4);
     L.table = take(sizeof(BatchTable));
-    L.ll = take(size_t(B) * (H > I ? H : I) * 8);
+    L.ll = take(size_t(B) * std::max(std::max(H, I), L.qkv_rows) * 8);
     L.ll_part = take(size_t(B) * attention_workspace_floats(m->heads, L.max_chunks, D) * 8);
     L.ll_out = take(size_t(B) * L.qd * 8);
     L.ll_max = take(size_t(B) * 8 * 8);
@@ -687,10 +687,10 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         rp.gamma = Ly.input_norm;
         rp.k = H;
         if ((l == 0 || !tails) && (e = run_rows(l == 0 ? ROW_NORM : ROW_RESID_NORM, rp, M, s))) return e;
-        if (gemm_run(q8, act, Ly.qkv, Ly.qkv_scales, qkv, M, L.qkv_rows, H, gemm, s) != hipSuccess)
-            return HQ_ERR_LAUNCH;
-        // q/k head norms, RoPE and the K/V write of each sequence inside the
-        // attention kernel; its output rows combined and quantized for o
+        // the qkv GEMM; q/k head norms, RoPE and the K/V write of each
+        // sequence inside the attention kernel; its output rows combined and
+        // quantized for o (the GEMM and the attention in one launch where the
+        // tails apply)
         AttnParams a{};
         a.qkv = qkv;
         a.q_norm = Ly.q_norm;
@@ -716,11 +716,21 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
             a.ll_out = reinterpret_cast<uint64_t*>(ws + L.ll_out);
             a.ll_max = reinterpret_cast<uint64_t*>(ws + L.ll_max);
             a.epoch_ctr = step_ctr;
-            a.epoch_id = 4 * l + 3;
+            a.epoch_id = 4 * l;   // (epoch ids rise in launch order: the entries share L.ll)
+            a.qkv_ll = reinterpret_cast<uint64_t*>(ws + L.ll);
         }
-        if (launch_batch_attention(a, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        hipError_t fe = hipErrorNotSupported;
+        if (tails) fe = launch_batch_qkv_attention(q8, act, Ly.qkv, Ly.qkv_scales, H, a, s);
+        if (fe == hipErrorNotSupported) {
+            a.qkv_ll = nullptr;
+            if (gemm_run(q8, act, Ly.qkv, Ly.qkv_scales, qkv, M, L.qkv_rows, H, gemm, s) != hipSuccess)
+                return HQ_ERR_LAUNCH;
+            if (launch_batch_attention(a, s) != hipSuccess) return HQ_ERR_LAUNCH;
+        } else if (fe != hipSuccess) {
+            return HQ_ERR_LAUNCH;
+        }
         if (tails) {
-            tl.epoch_id = 4 * l;
+            tl.epoch_id = 4 * l + 1;
             tl.gamma = Ly.post_norm;
             tl.kq = gemm_padded_k(H);
             if (gemm_run_tail(q8, act, Ly.o, Ly.o_scales, M, H, L.qd, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
@@ -735,7 +745,7 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         // gate_up with SwiGLU in its epilogue, then the down input's quant
         // (in its tail where it has one)
         if (swiglu_tail) {
-            tl.epoch_id = 4 * l + 1;
+            tl.epoch_id = 4 * l + 2;
             tl.kq = gemm_padded_k(I);
             if (gemm_run_swiglu_tail(q8, act, Ly.gate_up, Ly.gate_up_scales, M, I, H, tl, s) != hipSuccess)
                 return HQ_ERR_LAUNCH;
@@ -745,7 +755,7 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         }
         if (tails) {
             // the next layer's input rows (the final norm's after the last layer)
-            tl.epoch_id = 4 * l + 2;
+            tl.epoch_id = 4 * l + 3;
             tl.gamma = l + 1 < m->layers ? m->layer[l + 1].input_norm : m->final_norm;
             tl.kq = gemm_padded_k(H);
             if (gemm_run_tail(q8, act, Ly.down, Ly.down_scales, M, H, I, tl, s) != hipSuccess) return HQ_ERR_LAUNCH;
