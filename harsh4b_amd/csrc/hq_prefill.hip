@@ -25,8 +25,9 @@
 // batch and a per-sequence argmax that feeds each greedy token back on the
 // device: M forward_token steps (cpu_lightspark.py:424-468) sharing every
 // weight read, bit-identical to them.  Where the shapes allow, each layer is
-// five launches: the qkv GEMM; the attention, whose last blocks combine and
-// quantize each sequence's row; the o GEMM, whose last blocks add the
+// four launches (up to 16 sequences; five beyond): the qkv GEMM and the
+// attention in one (separate beyond 16), the attention's last blocks
+// combining and quantizing each sequence's row; the o GEMM, whose last blocks add the
 // residual and run the post-attention norm and quantization; the gate_up
 // GEMM with SwiGLU, whose last blocks quantize the down input; the down
 // GEMM, whose last blocks add the residual and run the next layer's input
