@@ -27,11 +27,12 @@
 // weight read, bit-identical to them.  Where the shapes allow, each layer is
 // four launches (up to 16 sequences; five beyond): the qkv GEMM and the
 // attention in one (separate beyond 16), the attention's last blocks
-// combining and quantizing each sequence's row; the o GEMM, whose last blocks add the
-// residual and run the post-attention norm and quantization; the gate_up
-// GEMM with SwiGLU, whose last blocks quantize the down input; the down
-// GEMM, whose last blocks add the residual and run the next layer's input
-// norm (the row, combine and quantization kernels otherwise).
+// combining and quantizing each sequence's row; the o GEMM, whose last
+// blocks add the residual and run the post-attention norm and
+// quantization; the gate_up GEMM with SwiGLU, whose last blocks quantize
+// the down input; the down GEMM, whose last blocks add the residual and run
+// the next layer's input norm (the row, combine and quantization kernels
+// otherwise).
 #include <algorithm>
 
 #include "hq_device.h"
