@@ -426,7 +426,9 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
 // batch_combine_quant_kernel computes it (M = max of m_c; a_c = exp(m_c -
 // M); L and O fmaf chains over ascending c; out = O * (1 / L)).  The row's
 // maximum |out| is each part's maximum (order-free) handed between the
-// eight blocks as entries; then the same quantization (amax floored at 1e-5,
+// eight blocks as entries (they wait for each other: the launch's other
+// blocks wait for nobody, so they finish and the at most 8 * 32 tail blocks
+// all get a place on the chip); then the same quantization (amax floored at 1e-5,
 // quant_i8 with 127 / amax, de-interleaved, act = amax / 127).
 constexpr int kAttnTailChunks = 8;   // contexts of up to 8 chunks (max_chunks <= 8)
 constexpr int kAttnTailParts = 8;    // tail blocks per sequence
