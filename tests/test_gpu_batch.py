@@ -106,10 +106,11 @@ def qwen():
     return model
 
 
-@pytest.mark.parametrize("m,big", [(8, False), (32, False), (8, True)])
+@pytest.mark.parametrize("m,big", [(8, False), (32, False), (8, True), (16, False), (1, False)])
 def test_qwen3_4b_batch_matches_single_steps(qwen, m, big):
     # M sequences with histories of 1 .. 300 positions (one to five chunks
-    # of attention, one to two chunk groups), stepped together and alone;
+    # of attention, one to two chunk groups), stepped together and alone
+    # (up to 16 sequences the qkv GEMM runs in the attention's launch);
     # with `big` one state holds 600 positions (more than eight chunks: the
     # attention's chunk partials go through the separate combine kernel)
     model = qwen
