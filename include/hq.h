@@ -264,7 +264,9 @@ int hq_prefill(const hq_model* model, const hq_state* state, const int32_t* toke
  * of count structs; every state's capacity must be <= max_capacity, the
  * capacity the workspace was sized for: hq_decode_batch_workspace_bytes(
  * model, max_capacity) bytes, 256-byte aligned, zero-filled before first use
- * (its counters are left at zero by every call).  A full cache sets
+ * (its tickets are left at zero by every call; a step counter in it advances
+ * by one per call and tags the values the step's launches hand to their last
+ * blocks, so a workspace zero-filled again starts over).  A full cache sets
  * HQ_STEP_FULL and a bad token HQ_STEP_BAD_TOKEN in that state's status.
  * Shapes: those hq_prefill takes, with at most 64 query heads and a hidden
  * size of at most 4096 (the workspace size is 0 and the call HQ_ERR_ARG
