@@ -332,41 +332,84 @@ static int run_rows(int mode, RowParams p, int rows, hipStream_t s)
 
 // ---- batched decode step ----------------------------------------------------------
 
-// The step's table into the workspace, and the step counter one up (the
-// GEMM tails' entries of this step carry it).
-__global__ void batch_table_kernel(BatchTable t, BatchTable* dst, uint32_t* step_ctr)
+// The start of a batched step in one launch: block 0 copies the step's
+// table into the workspace and advances the step counter; block m decodes
+// sequence m's embedding row into x (a token outside the vocabulary is
+// flagged and replaced by 0, a full cache flagged, as the single step's
+// embedding kernel does) and runs the first layer's input RMSNorm and
+// quantization on it (the
+// row kernel's NORM mode: 256 strided fmaf partials, halving tree, the
+// maximum over the four waves, quant_i8, de-interleaved row, act = amax/127).
+template <int NPT>
+__global__ __launch_bounds__(kBlock) void batch_begin_kernel(BatchTable t, BatchTable* dst, uint32_t* step_ctr,
+                                                             const uint8_t* emb, const float* emb_scales, int vocab,
+                                                             int hidden, float* x, const float* gamma, float eps,
+                                                             int8_t* q, int kq, float* act)
 {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(&t);
-    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
-    for (int i = threadIdx.x; i < int(sizeof(BatchTable) / 4); i += blockDim.x) d[i] = src[i];
-    if (threadIdx.x == 0) *step_ctr += 1u;
-}
-
-// Block m: the embedding row of sequence m's current token (a token outside
-// the vocabulary is flagged and replaced by 0, a full cache flagged), as
-// embedding_kernel does for one sequence.
-__global__ __launch_bounds__(kBlock) void batch_embed_kernel(const uint8_t* emb, const float* emb_scales, int vocab,
-                                                             int hidden, const BatchTable* T, float* x)
-{
+    __shared__ float red[kBlock];
+    __shared__ float wmax[kBlock / kWave];
     const int m = blockIdx.x;
-    int t = *T->token[m];
-    const int pos = *T->position[m];
-    if (threadIdx.x == 0 && (pos < 0 || pos >= T->capacity[m])) atomicOr(T->status[m], HQ_STEP_FULL);
-    if (t < 0 || t >= vocab) {
-        if (threadIdx.x == 0) atomicOr(T->status[m], HQ_STEP_BAD_TOKEN);
-        t = 0;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    if (m == 0) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(&t);
+        uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+        for (int i = tid; i < int(sizeof(BatchTable) / 4); i += kBlock) d[i] = src[i];
+        if (tid == 0) *step_ctr += 1u;
     }
-    const int half = hidden >> 1;
-    const uint8_t* row = emb + size_t(t) * size_t(half);
-    const float s = emb_scales[t];
+    int tok = *t.token[m];
+    const int pos = *t.position[m];
+    if (tid == 0 && (pos < 0 || pos >= t.capacity[m])) atomicOr(t.status[m], HQ_STEP_FULL);
+    if (tok < 0 || tok >= vocab) {
+        if (tid == 0) atomicOr(t.status[m], HQ_STEP_BAD_TOKEN);
+        tok = 0;
+    }
+    const uint8_t* row = emb + size_t(tok) * size_t(hidden >> 1);
+    const float sc = emb_scales[tok];
     float* xr = x + size_t(m) * hidden;
-    for (int j = threadIdx.x; j < half; j += kBlock) {
-        const uint8_t b = row[j];
-        const int lo = int(int8_t(uint8_t(b << 4))) >> 4;
-        const int hi = int(int8_t(b)) >> 4;
-        xr[2 * j] = float(lo) * s;
-        xr[2 * j + 1] = float(hi) * s;
+    float v[NPT], gam[NPT];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+        const int i = tid + kBlock * j;
+        if (i < hidden) {
+            const uint8_t byte = row[i >> 1];
+            const int nib = (i & 1) ? int(int8_t(byte)) >> 4 : int(int8_t(uint8_t(byte << 4))) >> 4;
+            v[j] = float(nib) * sc;
+            gam[j] = gamma[i];
+            xr[i] = v[j];
+            ss = __builtin_fmaf(v[j], v[j], ss);
+        } else {
+            v[j] = 0.0f;
+            gam[j] = 0.0f;
+        }
     }
+    red[tid] = ss;
+    lds_sync();
+    const float r2 = (red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]);
+    const float total = wave_tree_sum64_all(r2);
+    const float r = __builtin_sqrtf(total / float(hidden) + eps);
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+        v[j] = tid + kBlock * j < hidden ? (v[j] / r) * gam[j] : 0.0f;
+        amax = fmaxf(amax, fabsf(v[j]));
+    }
+    amax = wave_max64_all(amax);
+    if (lane == 0) wmax[tid / kWave] = amax;
+    lds_sync();
+    amax = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kBlock / kWave; ++w) amax = fmaxf(amax, wmax[w]);
+    amax = fmaxf(amax, 1e-5f);
+    const float inv = 127.0f / amax;
+    int8_t* qr = q + size_t(m) * kq;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+        const int i = tid + kBlock * j;
+        if (i < hidden) qr[deint_offset(i)] = quant_i8(v[j], inv);
+    }
+    if (tid == 0) act[m] = amax / 127.0f;
 }
 
 // Block (b, m): logits [b*kArgPer, ...) of sequence m copied to its state's
@@ -658,9 +701,15 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
     const long long time_stride = (long long)KV * D;
     auto ok = [] { return hipGetLastError() == hipSuccess; };
     uint32_t* step_ctr = reinterpret_cast<uint32_t*>(ws + L.step_ctr);
-    hipLaunchKernelGGL(batch_table_kernel, dim3(1), dim3(kBlock), 0, s, t, table, step_ctr);
-    hipLaunchKernelGGL(batch_embed_kernel, dim3(M), dim3(kBlock), 0, s, m->embedding, m->embedding_scales, m->vocab,
-                       H, table, x);
+    // the table, the embedding rows and the first layer's input rows
+    if (H <= kBlock * 10)
+        hipLaunchKernelGGL((batch_begin_kernel<10>), dim3(M), dim3(kBlock), 0, s, t, table, step_ctr, m->embedding,
+                           m->embedding_scales, m->vocab, H, x, m->layer[0].input_norm, m->eps, q8, gemm_padded_k(H),
+                           act);
+    else
+        hipLaunchKernelGGL((batch_begin_kernel<16>), dim3(M), dim3(kBlock), 0, s, t, table, step_ctr, m->embedding,
+                           m->embedding_scales, m->vocab, H, x, m->layer[0].input_norm, m->eps, q8, gemm_padded_k(H),
+                           act);
     if (!ok()) return HQ_ERR_LAUNCH;
     RowParams rp{};
     rp.eps = m->eps;
@@ -688,7 +737,7 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
         rp.gate_up = nullptr;
         rp.gamma = Ly.input_norm;
         rp.k = H;
-        if ((l == 0 || !tails) && (e = run_rows(l == 0 ? ROW_NORM : ROW_RESID_NORM, rp, M, s))) return e;
+        if (l > 0 && !tails && (e = run_rows(ROW_RESID_NORM, rp, M, s))) return e;
         // the qkv GEMM; q/k head norms, RoPE and the K/V write of each
         // sequence inside the attention kernel; its output rows combined and
         // quantized for o (the GEMM and the attention in one launch where the
