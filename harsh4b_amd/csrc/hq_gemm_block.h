@@ -62,10 +62,9 @@ __device__ __forceinline__ uint32_t tail_epoch(const GemmTail& t)
     return (*t.epoch_ctr << 8) | uint32_t(t.epoch_id);
 }
 
-
 // Row s of a tail launch, by threads 0-255 of one block (the others only
-// take the barriers): once every block's entry of the row is current (each
-// block stores its outputs before its tail begins; blocks start in index
+// take the barriers): once every tile block's entry of the row is current
+// (the tile blocks come first in index order and blocks start in index
 // order, so the blocks a tail waits for are running or done), the same
 // operations as the row kernel's RESID_NORM mode: x + GEMM output into the
 // residual, RMSNorm (256 strided fmaf partials, halving tree), the
