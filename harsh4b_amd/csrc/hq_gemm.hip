@@ -21,7 +21,9 @@
 // A block owns RG groups of 16 rows over the whole K; its W waves split K
 // (each a contiguous range of double steps, all of its loads in flight at
 // once) and their int32 partial tiles meet in LDS, so no split of K crosses
-// blocks: no atomics, no arrival tickets, no zeroed workspace.
+// blocks: no atomics, no arrival tickets, no zeroed workspace.  (The
+// batched decode step's launches with tails hand their outputs to extra
+// blocks through {value, epoch} entries in its workspace: hq_gemm_block.h.)
 #include "hq_gemm_block.h"
 
 namespace hq {
