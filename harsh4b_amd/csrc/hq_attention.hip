@@ -245,6 +245,15 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
                 vc_s[lane] = h0;
                 vc_s[lane + 64] = h1;
             }
+        } else if constexpr (QLL) {
+            // a position outside the cache writes no K/V, but its rows'
+            // entries are still awaited: this sequence's tail then starts
+            // only after every qkv tile block of the launch has published,
+            // i.e. has finished reading the q8/act rows the tail overwrites
+            if (split == nsplit - 1 && wave < 2) {
+                float x0, x1;
+                raw2(size_t(a.kv_heads * G + wave * a.kv_heads + g), x0, x1);
+            }
         }
     }
     if (plain_q)

@@ -326,12 +326,16 @@ __device__ __forceinline__ int8_t quant_i8(float v, float inv)
 //
 // A launch's blocks hand values to its last blocks as 64-bit entries, the
 // value's bits in the low word and the launch's epoch in the high word,
-// with agent-scope stores and loads (no fences): an entry is current when
-// its epoch is not older than the launch's.
+// with agent-scope stores and loads (no fences).  The epoch is
+// (step << 8) | launch id, the step counter running 1 .. kEpochSteps - 1:
+// the step's first kernel clears every entry (epoch 0) when the counter
+// wraps, so an entry's epoch equals the launch's only when the launch itself
+// wrote it, however long the workspace lives.
+constexpr uint32_t kEpochSteps = 1u << 23;
 
 __device__ __forceinline__ bool tail_ready(uint64_t v, uint32_t ep)
 {
-    return int32_t(uint32_t(v >> 32) - ep) >= 0;
+    return uint32_t(v >> 32) == ep;
 }
 __device__ __forceinline__ uint64_t tail_load(const uint64_t* p)
 {

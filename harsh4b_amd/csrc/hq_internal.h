@@ -144,7 +144,7 @@ int gemm_swiglu_blocks(int n);
 // gamma, quantization into q / act), as the RESID_NORM row kernel does.
 struct GemmTail {
     uint64_t* ll;               // [m, n]
-    const uint32_t* epoch_ctr;  // the step counter (bumped by the step's first kernel)
+    const uint32_t* epoch_ctr;  // the step counter (advanced, and wrapped, by the step's first kernel)
     int epoch_id;               // 0 .. 255, unique per launch within a step
     float* x;                   // [m, n] residual rows, updated
     const float* gamma;         // [n]

@@ -333,7 +333,10 @@ static int run_rows(int mode, RowParams p, int rows, hipStream_t s)
 // ---- batched decode step ----------------------------------------------------------
 
 // The start of a batched step in one launch: block 0 copies the step's
-// table into the workspace and advances the step counter; block m decodes
+// table into the workspace and advances the step counter (when the counter
+// wraps past kEpochSteps - 1, or holds a value outside 0 .. kEpochSteps - 1,
+// it first clears the `entry_words` 16-byte words of {value, epoch} entries
+// at `entries` and restarts the count at 1); block m decodes
 // sequence m's embedding row into x (a token outside the vocabulary is
 // flagged and replaced by 0, a full cache flagged, as the single step's
 // embedding kernel does) and runs the first layer's input RMSNorm and
@@ -342,7 +345,7 @@ static int run_rows(int mode, RowParams p, int rows, hipStream_t s)
 // maximum over the four waves, quant_i8, de-interleaved row, act = amax/127).
 template <int NPT>
 __global__ __launch_bounds__(kBlock) void batch_begin_kernel(BatchTable t, BatchTable* dst, uint32_t* step_ctr,
-                                                             const uint8_t* emb, const float* emb_scales, int vocab,
+                                                             uint4* entries, size_t entry_words, const uint8_t* emb, const float* emb_scales, int vocab,
                                                              int hidden, float* x, const float* gamma, float eps,
                                                              int8_t* q, int kq, float* act)
 {
@@ -355,7 +358,12 @@ __global__ __launch_bounds__(kBlock) void batch_begin_kernel(BatchTable t, Batch
         const uint32_t* src = reinterpret_cast<const uint32_t*>(&t);
         uint32_t* d = reinterpret_cast<uint32_t*>(dst);
         for (int i = tid; i < int(sizeof(BatchTable) / 4); i += kBlock) d[i] = src[i];
-        if (tid == 0) *step_ctr += 1u;
+        const uint32_t c = *step_ctr + 1u;
+        const bool wrap = c >= kEpochSteps || c == 0u;
+        if (wrap)
+            for (size_t i = tid; i < entry_words; i += kBlock) entries[i] = make_uint4(0, 0, 0, 0);
+        __syncthreads();   // every thread has read the counter
+        if (tid == 0) *step_ctr = wrap ? 1u : c;
     }
     int tok = *t.token[m];
     const int pos = *t.position[m];
@@ -509,6 +517,7 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.arg_blocks = (V + kBatchArgPer - 1) / kBatchArgPer;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t at = off; off += al256p(bytes); return at; };
+    L.step_ctr = take(4);   // first: the step counter sits at offset 0 (include/hq.h)
     L.x = take(size_t(B) * H * 4);
     L.q8 = take(size_t(gemm_padded_m(B)) * L.kp);
     L.act = take(size_t(B) * 4);
@@ -529,12 +538,13 @@ static BatchLayout batch_layout(const hq_model* m, int max_capacity)
     L.tickets = take(size_t(B) * ticket_words(L.arg_blocks) * 4);
     L.pmax = take(size_t(gemm_swiglu_blocks(I)) * B * 4);
     L.table = take(sizeof(BatchTable));
+    // the {value, epoch} entries, contiguous to the end (cleared together
+    // when the step counter wraps)
     L.ll = take(size_t(B) * std::max(std::max(H, I), L.qkv_rows) * 8);
     L.ll_part = take(size_t(B) * attention_workspace_floats(m->heads, L.max_chunks, D) * 8);
     L.ll_out = take(size_t(B) * L.qd * 8);
     L.ll_max = take(size_t(B) * 8 * 8);
     L.pmax_ll = take(size_t(gemm_swiglu_blocks(I)) * B * 8);
-    L.step_ctr = take(4);
     L.total = off;
     return L;
 }
@@ -701,15 +711,17 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
     const long long time_stride = (long long)KV * D;
     auto ok = [] { return hipGetLastError() == hipSuccess; };
     uint32_t* step_ctr = reinterpret_cast<uint32_t*>(ws + L.step_ctr);
+    uint4* entries = reinterpret_cast<uint4*>(ws + L.ll);
+    const size_t entry_words = (L.total - L.ll) / 16;
     // the table, the embedding rows and the first layer's input rows
     if (H <= kBlock * 10)
-        hipLaunchKernelGGL((batch_begin_kernel<10>), dim3(M), dim3(kBlock), 0, s, t, table, step_ctr, m->embedding,
-                           m->embedding_scales, m->vocab, H, x, m->layer[0].input_norm, m->eps, q8, gemm_padded_k(H),
-                           act);
+        hipLaunchKernelGGL((batch_begin_kernel<10>), dim3(M), dim3(kBlock), 0, s, t, table, step_ctr, entries,
+                           entry_words, m->embedding, m->embedding_scales, m->vocab, H, x, m->layer[0].input_norm,
+                           m->eps, q8, gemm_padded_k(H), act);
     else
-        hipLaunchKernelGGL((batch_begin_kernel<16>), dim3(M), dim3(kBlock), 0, s, t, table, step_ctr, m->embedding,
-                           m->embedding_scales, m->vocab, H, x, m->layer[0].input_norm, m->eps, q8, gemm_padded_k(H),
-                           act);
+        hipLaunchKernelGGL((batch_begin_kernel<16>), dim3(M), dim3(kBlock), 0, s, t, table, step_ctr, entries,
+                           entry_words, m->embedding, m->embedding_scales, m->vocab, H, x, m->layer[0].input_norm,
+                           m->eps, q8, gemm_padded_k(H), act);
     if (!ok()) return HQ_ERR_LAUNCH;
     RowParams rp{};
     rp.eps = m->eps;
@@ -767,7 +779,7 @@ extern "C" int hq_decode_batch(const hq_model* m, const hq_state* states, int co
             a.ll_out = reinterpret_cast<uint64_t*>(ws + L.ll_out);
             a.ll_max = reinterpret_cast<uint64_t*>(ws + L.ll_max);
             a.epoch_ctr = step_ctr;
-            a.epoch_id = 4 * l;   // (epoch ids rise in launch order: the entries share L.ll)
+            a.epoch_id = 4 * l;   // (unique per launch of the step: the launches share L.ll)
             a.qkv_ll = reinterpret_cast<uint64_t*>(ws + L.ll);
         }
         hipError_t fe = hipErrorNotSupported;

@@ -264,9 +264,13 @@ int hq_prefill(const hq_model* model, const hq_state* state, const int32_t* toke
  * of count structs; every state's capacity must be <= max_capacity, the
  * capacity the workspace was sized for: hq_decode_batch_workspace_bytes(
  * model, max_capacity) bytes, 256-byte aligned, zero-filled before first use
- * (its tickets are left at zero by every call; a step counter in it advances
- * by one per call and tags the values the step's launches hand to their last
- * blocks, so a workspace zero-filled again starts over).  A full cache sets
+ * (its tickets are left at zero by every call).  Its first 4 bytes hold a
+ * uint32 step counter that advances by one per call and tags the values the
+ * step's launches hand to their last blocks; a launch accepts only values
+ * tagged with its own step and launch.  The counter runs 1 .. 2^23 - 1: the
+ * call that would pass 2^23 - 1 (or finds the counter outside that range)
+ * first clears every tagged value and restarts at 1, so the workspace can
+ * serve any number of calls.  A full cache sets
  * HQ_STEP_FULL and a bad token HQ_STEP_BAD_TOKEN in that state's status.
  * Shapes: those hq_prefill takes, with at most 64 query heads and a hidden
  * size of at most 4096 (the workspace size is 0 and the call HQ_ERR_ARG

@@ -133,3 +133,60 @@ def test_qwen3_4b_batch_matches_single_steps(qwen, m, big):
     for st in B:
         model.decode_greedy(st, 2)
     _compare(model, A, B, f"M={m} greedy")
+
+
+def _step_counter(model, cap):
+    """The batched workspace's step counter (its first 4 bytes)."""
+    return model._batch_workspaces[cap][:4].view(torch.int32)
+
+
+def test_qwen3_4b_batch_step_counter_wrap(qwen):
+    # A step accepts only the values its own launches tagged: an M = 16 step
+    # leaves tagged values in rows 0-15; the counter is then set two short of
+    # its period, an M = 8 step runs at the last count, and the next M = 16
+    # step wraps: it must clear the old rows 8-15 (tagged at count 1, the
+    # count the wrap restarts at) before any launch waits on them.  Then the
+    # workspace is zero-filled with its counter set to 2^23 (outside the
+    # period), and an M = 8 and an M = 16 step run from it.  Every step equals M single
+    # steps bit for bit.  (Before the counter had a period, a tag older than
+    # 2^23 steps counted as current.)
+    period = 1 << 23
+    model = qwen
+    rng = np.random.default_rng(23)
+    cap = 96
+    model._batch_workspaces.pop(cap, None)   # a fresh zero-filled workspace
+    lengths = [1, 70, 5, 33, 64, 2, 9, 80, 17, 3, 65, 40, 12, 7, 50, 26]
+    A, B = [], []
+    for n in lengths:
+        pr = [int(t) for t in rng.integers(0, 151936, n)]
+        for group in (A, B):
+            st = model.new_state(cap)
+            model.prefill(pr, st)
+            group.append(st)
+
+    def step(m, tag):
+        nxt = [int(t) for t in rng.integers(0, 151936, m)]
+        model.forward_tokens(nxt, A[:m])
+        for t, st in zip(nxt, B[:m]):
+            model.forward_token(t, st)
+        _compare(model, A[:m], B[:m], tag)
+
+    step(16, "count 1")
+    ctr = _step_counter(model, cap)
+    assert int(ctr.item()) == 1
+    ctr.fill_(period - 2)
+    step(8, "last count")
+    assert int(_step_counter(model, cap).item()) == period - 1
+    step(16, "wrap")
+    assert int(_step_counter(model, cap).item()) == 1
+    step(8, "after wrap")
+    assert int(_step_counter(model, cap).item()) == 2
+
+    # a zero-filled workspace whose counter reads 2^23 (outside the period)
+    ws = model._batch_workspaces[cap]
+    ws.zero_()
+    _step_counter(model, cap).fill_(period)
+    step(8, "outside the period, M = 8")
+    assert int(_step_counter(model, cap).item()) == 1
+    step(16, "outside the period, M = 16")
+    assert int(_step_counter(model, cap).item()) == 2
