@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.gpu_util import assert_bits_equal, to_host
+from tests.gpu_util import assert_bits_equal, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -190,3 +190,60 @@ def test_qwen3_4b_batch_step_counter_wrap(qwen):
     assert int(_step_counter(model, cap).item()) == 1
     step(16, "outside the period, M = 16")
     assert int(_step_counter(model, cap).item()) == 2
+
+
+@pytest.fixture(scope="module")
+def qwen_oracle(qwen):
+    from harsh4b_amd.synthetic import host_arrays
+    return oracle.OracleModel(qwen.config, host_arrays(qwen))
+
+
+@pytest.mark.parametrize("m,cap", [(8, 512), (16, 512), (32, 512), (8, 700)])
+def test_qwen3_4b_batch_matches_oracle(qwen, qwen_oracle, m, cap):
+    # The full-size batched step against the oracle directly, sequence by
+    # sequence (8 KV heads x 4 query heads, hidden 2560): each sequence gets
+    # its own N(0,1) fp16 cache of a ragged length (0 .. cap - 2 positions,
+    # chunk edges included), then one batched step with given tokens and one
+    # greedy batched step.  M = 8 and 16 run the qkv GEMM inside the
+    # attention's launch, M = 32 apart from it; capacity 512 keeps the
+    # attention's combine in the launch tails (at most 8 chunks), 700 sends
+    # it through the combine kernel.  Logits, greedy tokens and the K/V rows
+    # written must equal the oracle's bits.
+    model, ref = qwen, qwen_oracle
+    rng = np.random.default_rng(5000 + m + cap)
+    contexts = [int(v) for v in rng.integers(0, cap - 2, m)]
+    edges = [0, 1, 63, 64, 65, cap - 2]
+    contexts[:len(edges)] = edges[:m]
+    layers, kv, d = model.config["num_hidden_layers"], model.config["num_key_value_heads"], 128
+    base = {name: rng.standard_normal((layers, cap + 2 * m, kv, d)).astype(np.float16) for name in ("keys", "values")}
+    A, R = [], []
+    for i, ctx in enumerate(contexts):
+        st = model.new_state(cap)
+        rs = ref.new_state(cap)
+        for name in ("keys", "values"):
+            cache = base[name][:, 2 * i:2 * i + ctx]
+            getattr(st, name)[:, :ctx] = to_dev(cache)
+            getattr(rs, name)[:, :ctx] = cache.view(np.uint16)
+        st.device_position.fill_(ctx)
+        st.position = ctx
+        rs.position = ctx
+        A.append(st)
+        R.append(rs)
+    torch.cuda.synchronize()
+    toks = [int(t) for t in rng.integers(0, 151936, m)]
+    for step in range(2):
+        if step == 0:
+            model.forward_tokens(toks, A)
+        else:
+            model.decode_greedy_batch(A, 1, use_graph=False)
+        for i, (st, rs) in enumerate(zip(A, R)):
+            rtok = ref.forward_token(toks[i], rs)
+            tag = f"M={m} cap={cap} step {step} seq {i} ctx {contexts[i] + step}"
+            assert_bits_equal(to_host(st.logits), rs.logits, f"{tag} logits")
+            assert model.greedy_token(st) == rtok, tag
+            p = contexts[i] + step
+            assert_bits_equal(to_host(st.keys).view(np.uint16)[:, p], rs.keys[:, p], f"{tag} keys")
+            assert_bits_equal(to_host(st.values).view(np.uint16)[:, p], rs.values[:, p], f"{tag} values")
+            toks[i] = rtok
+        for st in A:
+            st.check_status()
