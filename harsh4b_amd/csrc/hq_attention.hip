@@ -956,6 +956,431 @@ hipError_t launch_attention(const AttnParams& a, bool step_mode, hipStream_t s)
     }
 }
 
+// ---- the drop-in GQA decode in one launch ------------------------------------------
+//
+// hq_gqa_decode's kernel: block i < nc * kv is chunk item (chunk c = i / kv,
+// kv head g = i % kv); the launch's last blocks combine.  An item block
+// copies its chunk's K and V rows (64 rows of 2D bytes each) straight into
+// LDS with global->LDS loads (no register round trip), loads its kv head's
+// G query heads into registers meanwhile, and computes, in the spec order
+// of or_gqa_decode_split: the scores (16 partial fmaf chains of D/16 dims,
+// the 16-lane halving tree, times 1 / sqrt(D)), the chunk's max m, e_t =
+// exp(s_t - m) and l = the 64-slot tree, and o[d] = the fmaf chain of e_t *
+// v_t[d] over ascending t.  A one-chunk context finishes there (out = o *
+// (1 / l) through the combine's operations); otherwise the item publishes
+// (m, l, o[0..D-1]) per query head as 32-bit words holding the value's bits
+// XOR kGqaKey (a signalling-NaN pattern no arithmetic result carries, so a
+// published word is never 0) with agent-scope stores.  A combine block
+// (256 / D query heads, one thread per (head, dim) chain) waits for those
+// words -- one lane per head first watches the last chunk's last word (the
+// last items start last), then every thread polls its own words -- and runs
+// the spec's combine over ascending chunks: M = max m_c, a_c = exp(m_c - M),
+// L = fmaf(a_c, l_c, L), O = fmaf(a_c, o_c[d], O), out = O * (1 / L); it
+// then stores 0 over every word it read.  The words therefore start and end
+// every call at zero: the workspace must be zero-filled before its first
+// use, and calls that share a workspace must not overlap.  Every wait is
+// bounded (kGqaSpinLimit rounds), so the launch always ends.
+constexpr uint32_t kGqaKey = 0x7FA5A5A5u;
+constexpr unsigned kGqaSpinLimit = 1u << 22;
+
+__device__ __forceinline__ void gqa_word_store(uint32_t* p, float v)
+{
+    __hip_atomic_store(p, f32_bits(v) ^ kGqaKey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t gqa_word_load(const uint32_t* p)
+{
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void gqa_word_clear(uint32_t* p)
+{
+    __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The value of word *p once it is published (bounded wait).
+__device__ __forceinline__ float gqa_word_wait(const uint32_t* p, unsigned& budget)
+{
+    uint32_t w = gqa_word_load(p);
+    while (w == 0u && budget != 0u) {
+        __builtin_amdgcn_s_sleep(1);
+        if (--budget == 0u) break;
+        w = gqa_word_load(p);
+    }
+    return bits_f32(w ^ kGqaKey);
+}
+
+constexpr int kFlashThreads = 512;   // threads of a gqa_flash_kernel block (8 waves)
+
+template <int D, int GMAX>
+struct FlashLds {
+    alignas(16) uint16_t k[kAttnChunk * D];   // the chunk's K rows [t][d]
+    alignas(16) uint16_t v[kAttnChunk * D];   // and V rows
+    alignas(16) float e[GMAX][kAttnChunk];    // scores, then exp terms
+    alignas(16) float q[GMAX * D];            // the kv head's query rows
+    float m[GMAX], l[GMAX];
+};
+
+struct FlashParams {
+    const float* q;           // [kv * G, D]
+    const uint16_t* keys;     // [context, kv, D] fp16
+    const uint16_t* values;
+    uint32_t* words;          // published partials (zero between calls), nc4 = nc rounded up to 4,
+                              // U = combine units per head: o [kv * G][nc4 / 4][D][4], then
+                              // m [kv * G][U][nc4], then l [kv * G][U][nc4] (one copy per unit)
+    float* out;               // [kv * G, D]
+    long long time_stride;    // elements per position (kv * D)
+    int n, nc, kv, G;
+};
+
+// DPL consecutive halves of an LDS row as fp32.
+template <int DPL>
+__device__ __forceinline__ void lds_halves(const uint16_t* p, float (&k)[DPL])
+{
+    if constexpr (DPL == 8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { k[2 * j] = f16_to_f32(uint16_t(w[j])); k[2 * j + 1] = f16_to_f32(uint16_t(w[j] >> 16)); }
+    } else if constexpr (DPL == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        k[0] = f16_to_f32(uint16_t(v.x)); k[1] = f16_to_f32(uint16_t(v.x >> 16));
+        k[2] = f16_to_f32(uint16_t(v.y)); k[3] = f16_to_f32(uint16_t(v.y >> 16));
+    } else if constexpr (DPL == 2) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+        k[0] = f16_to_f32(uint16_t(v)); k[1] = f16_to_f32(uint16_t(v >> 16));
+    } else {
+        k[0] = f16_to_f32(*p);
+    }
+}
+
+template <int D>
+constexpr int flash_units_per_head() { return D == 128 ? 2 : 1; }
+
+template <int D, int GMAX>
+__device__ void flash_item(const FlashParams& a, FlashLds<D, GMAX>& S, int c, int g)
+{
+    constexpr int C = kAttnChunk;
+    constexpr int T = kFlashThreads;
+    constexpr int NW = T / kWave;                        // waves
+    constexpr int DPL = D / 16;                          // dims per score lane
+    constexpr int HSTEP = T / D;                         // heads between a thread's V chains
+    constexpr int PAIRS = (GMAX * D + T - 1) / T;
+    constexpr int REPS = C / (T / 16);                   // score positions per 16-lane group
+    constexpr int RPI = 1024 / (2 * D);                  // K rows per 1 KB copy instruction
+    constexpr int LPR = 2 * D / 16;                      // lanes per row in a copy
+    constexpr int NINS = C / RPI;                        // copy instructions per matrix
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid & (kWave - 1);
+    const int G = a.G;
+    const int t0 = c * C;
+    const int tn = min(C, a.n - t0);
+    // The kv head's G query rows, then K rows, then V rows, straight into
+    // LDS, all by global->LDS copies (a wave's loads complete in issue
+    // order, and the compiler tracks none of these, so its own waits do not
+    // hold the scores back for V).  K/V instruction `ins` moves rows RPI*ins
+    // .. +RPI-1, lane i row RPI*ins + i/LPR, bytes 16(i%LPR)..; rows past the
+    // context re-read the last one (never used).  The scores run once K is
+    // in, while V is still arriving.
+    {
+        const int qbytes = G * D * 4;
+        const float* qb = a.q + size_t(g) * G * D;
+        for (int ins = wave; ins * 1024 < qbytes; ins += NW)
+            dma16(qb, uint32_t(min(ins * 1024 + lane * 16, qbytes - 16)), lds_addr(S.q) + uint32_t(ins) * 1024u);
+    }
+    const int nq = wave * 1024 < G * D * 4 ? 1 : 0;   // this wave's q copies (G * D * 4 <= 4 KB < NW KB)
+    const uint16_t* kb = a.keys + size_t(t0) * size_t(a.time_stride) + size_t(g) * D;
+    const uint16_t* vb = a.values + size_t(t0) * size_t(a.time_stride) + size_t(g) * D;
+    auto copy_off = [&](int ins) {
+        const int row = min(RPI * ins + lane / LPR, tn - 1);
+        return uint32_t(size_t(row) * size_t(a.time_stride) * 2u) + uint32_t(lane % LPR) * 16u;
+    };
+    for (int ins = wave; ins < NINS; ins += NW) dma16(kb, copy_off(ins), lds_addr(S.k) + uint32_t(ins) * 1024u);
+    for (int ins = wave; ins < NINS; ins += NW) dma16(vb, copy_off(ins), lds_addr(S.v) + uint32_t(ins) * 1024u);
+    // this wave's q and K copies are done when at most its V copies are
+    // outstanding (memory operations complete in issue order)
+    constexpr int VMAX = (NINS + NW - 1) / NW;
+    static_assert(VMAX <= 2, "wait_vm_le covers up to two outstanding copies");
+    static_assert(GMAX * D * 4 <= NW * 1024, "one q copy per wave at most");
+    (void)nq;
+    wait_vm_le(wave < NINS ? (NINS - 1 - wave) / NW + 1 : 0);
+    lds_sync();
+    // this lane's DPL dims of every query head (a head past G repeats G - 1)
+    const int l16 = tid & 15, grp = tid >> 4;
+    float qr[GMAX][DPL];
+#pragma unroll
+    for (int h = 0; h < GMAX; ++h)
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) qr[h][j] = S.q[min(h, G - 1) * D + l16 * DPL + j];
+    // scores, 16 lanes per position.  Every lane computes every head and
+    // row (a head past G repeats head G - 1, a row past the context repeats
+    // the last one; neither is stored), so no branch splits the REPS x GMAX
+    // independent fmaf chains and trees; lane 0 of each row stores.
+    const float scale = 1.0f / __builtin_sqrtf(float(D));
+    float dot[REPS][GMAX];
+#pragma unroll
+    for (int rep = 0; rep < REPS; ++rep) {
+        float k[DPL];
+        lds_halves<DPL>(S.k + (grp + (T / 16) * rep) * D + l16 * DPL, k);
+#pragma unroll
+        for (int h = 0; h < GMAX; ++h) {
+            float pp = 0.0f;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) pp = __builtin_fmaf(qr[h][j], k[j], pp);
+            dot[rep][h] = pp;
+        }
+    }
+#pragma unroll
+    for (int rep = 0; rep < REPS; ++rep)
+#pragma unroll
+        for (int h = 0; h < GMAX; ++h) dot[rep][h] = row_tree_sum16(dot[rep][h]);
+    if (l16 == 0) {
+#pragma unroll
+        for (int rep = 0; rep < REPS; ++rep) {
+            const int i = grp + (T / 16) * rep;
+#pragma unroll
+            for (int h = 0; h < GMAX; ++h) S.e[h][i] = i < tn ? dot[rep][h] * scale : -__builtin_inff();
+        }
+    }
+    lds_sync();
+    // chunk statistics, one wave per head
+    for (int h = wave; h < G; h += NW) {
+        const float sc = S.e[h][lane];
+        const float m = wave_max64_all(sc);
+        const float e = lane < tn ? spec_expf(sc - m) : 0.0f;
+        const float l = wave_tree_sum64(e);
+        S.e[h][lane] = e;
+        if (lane == 0) { S.m[h] = m; S.l[h] = l; }
+    }
+    wait_all_memory();   // this wave's V copies have landed
+    lds_sync();
+    // V: thread (h0, d) runs the chains of heads h0, h0 + HSTEP, ...; the
+    // exp terms are read four positions at a time
+    const int d = tid % D, h0 = tid / D;
+    float o[PAIRS];
+#pragma unroll
+    for (int r = 0; r < PAIRS; ++r) o[r] = 0.0f;
+    int i = 0;
+    for (; i + 8 <= tn; i += 8) {
+        float v[8];
+        float4 e[PAIRS][2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = f16_to_f32(S.v[(i + j) * D + d]);
+#pragma unroll
+        for (int r = 0; r < PAIRS; ++r) {
+            const float* er = &S.e[min(h0 + HSTEP * r, GMAX - 1)][i];
+            e[r][0] = *reinterpret_cast<const float4*>(er);
+            e[r][1] = *reinterpret_cast<const float4*>(er + 4);
+        }
+#pragma unroll
+        for (int r = 0; r < PAIRS; ++r) {
+            o[r] = __builtin_fmaf(e[r][0].x, v[0], o[r]);
+            o[r] = __builtin_fmaf(e[r][0].y, v[1], o[r]);
+            o[r] = __builtin_fmaf(e[r][0].z, v[2], o[r]);
+            o[r] = __builtin_fmaf(e[r][0].w, v[3], o[r]);
+            o[r] = __builtin_fmaf(e[r][1].x, v[4], o[r]);
+            o[r] = __builtin_fmaf(e[r][1].y, v[5], o[r]);
+            o[r] = __builtin_fmaf(e[r][1].z, v[6], o[r]);
+            o[r] = __builtin_fmaf(e[r][1].w, v[7], o[r]);
+        }
+    }
+    for (; i < tn; ++i) {
+        const float v = f16_to_f32(S.v[i * D + d]);
+#pragma unroll
+        for (int r = 0; r < PAIRS; ++r) o[r] = __builtin_fmaf(S.e[min(h0 + HSTEP * r, GMAX - 1)][i], v, o[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < PAIRS; ++r) {
+        const int h = h0 + HSTEP * r;
+        if (h >= G) continue;
+        const int qh = g * G + h;
+        if (a.nc == 1) {
+            // the combine's operations over the one chunk
+            const float al = spec_expf(S.m[h] - S.m[h]);
+            const float L = __builtin_fmaf(al, S.l[h], 0.0f);
+            const float O = __builtin_fmaf(al, o[r], 0.0f);
+            a.out[size_t(qh) * D + d] = O * (1.0f / L);
+        } else {
+            const size_t nc4 = size_t((a.nc + 3) & ~3), H = size_t(a.kv) * G;
+            uint32_t* ow = a.words + (size_t(qh) * nc4 + (c & ~3)) * D + size_t(d) * 4;
+            gqa_word_store(ow + (c & 3), o[r]);
+            // the last chunk also publishes 0.0 into its group's padding slots
+            if (c == a.nc - 1)
+                for (int p = (c & 3) + 1; p < 4; ++p) gqa_word_store(ow + p, 0.0f);
+            // m and l once per combine unit of the head: each unit clears
+            // the copy it reads
+            constexpr int U = flash_units_per_head<D>();
+            if (d < U) {
+                gqa_word_store(a.words + H * nc4 * D + (size_t(qh) * U + d) * nc4 + c, S.m[h]);
+                gqa_word_store(a.words + H * nc4 * (D + U) + (size_t(qh) * U + d) * nc4 + c, S.l[h]);
+            }
+        }
+    }
+}
+
+// Combine blocks: wave 0 of each runs one unit -- (query head, half of its
+// dims) for D = 128, a query head for D <= 64 (lanes past D run the chunk
+// roles only); the other waves leave at once, so the units' loads and
+// clears issue from as many CUs as there are units.  Per batch of 64
+// chunks, lane c holds chunk c's m_c and l_c, so M is one wave max and a_c
+// = exp(m_c - M) is computed in lane c; the chain reads a_c and l_c from
+// lane c (readlane), with no LDS and no barrier.  A batch's words are
+// fetched in one burst (the lane's o_c[d] and its m_c, l_c), the
+// unpublished ones polled again, and cleared once held.  Chunks past the
+// context enter the chain as a_c = 0, l_c = 0, o_c = 0: fmaf(0, 0, x)
+// returns x, and neither L nor O is ever -0 (their terms' zeros are +0
+// sums), so the padding leaves the bits unchanged.  With more than one
+// batch M comes from a first pass over every m_c.
+constexpr int kFlashCB = 64;   // chunks per batch: one per lane
+
+
+template <int D>
+__device__ void flash_combine(const FlashParams& a, int unit)
+{
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    constexpr int NG = kFlashCB / 4;          // chunk groups per batch
+    const int lane = threadIdx.x & (kWave - 1);
+    const int hraw = unit / flash_units_per_head<D>();
+    const int half = unit % flash_units_per_head<D>();
+    const int d = half * kWave + lane;        // this lane's dim (a chain when d < D)
+    const bool chain = d < D;
+    const int nc = a.nc;
+    const size_t nc4 = size_t((nc + 3) & ~3), H = size_t(a.kv) * a.G;
+    uint32_t* obase = a.words + size_t(hraw) * nc4 * D;              // [nc4 / 4][D][4]
+    constexpr int U = flash_units_per_head<D>();
+    uint32_t* mbase = a.words + H * nc4 * D + size_t(unit) * nc4;    // this unit's copy [nc4]
+    uint32_t* lbase = a.words + H * nc4 * (D + U) + size_t(unit) * nc4;
+    unsigned budget = kGqaSpinLimit;
+    float M = -__builtin_inff();
+    if (nc > kFlashCB) {
+        float mm = -__builtin_inff();
+        for (int c = lane; c < nc; c += kWave) mm = fmaxf(mm, gqa_word_wait(mbase + c, budget));
+        M = wave_max64_all(mm);
+    }
+    float L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += kFlashCB) {
+        const int nb = min(kFlashCB, nc - c0);
+        const int ngrp = (nb + 3) >> 2;          // chunk groups of the batch
+        // every load unconditional, through buffer descriptors that end at
+        // the batch's last chunk (group): a load past one returns 0 without
+        // touching memory and a store there is dropped.  Group g4's four
+        // chunks of dim d are one 16-byte word of the lane, at a constant
+        // scalar offset; a group's padding slots past the context hold a
+        // published 0.0 (written by the last chunk's item), groups past the
+        // batch are set to 0.0 here, and lanes past D (D < 64) read dim 0's
+        // words and discard them.
+        const __amdgpu_buffer_rsrc_t ro = raw_rsrc(obase + size_t(c0) * D, ngrp * D * 16);
+        const __amdgpu_buffer_rsrc_t rm = raw_rsrc(mbase + c0, nb * 4);
+        const __amdgpu_buffer_rsrc_t rl = raw_rsrc(lbase + c0, nb * 4);
+        const uint32_t vo = uint32_t(chain ? d : 0) * 16u;
+        // first the batch's m_c and l_c, one chunk per lane (two loads per
+        // round): an item publishes them with its o words, so once every
+        // chunk's are in, the o burst below rarely meets an empty word
+        const bool mine = lane < nb;             // lane c's chunk
+        uint32_t mw = 0u, lw = 0u;
+        while (true) {
+            mw = mw != 0u ? mw : __builtin_amdgcn_raw_buffer_load_b32(rm, lane * 4, 0, kAgentSC1);
+            lw = lw != 0u ? lw : __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, kAgentSC1);
+            mw = mine ? mw : f32_bits(-__builtin_inff()) ^ kGqaKey;
+            lw = mine ? lw : kGqaKey;
+            if (!__builtin_amdgcn_ballot_w64((mw == 0u) | (lw == 0u)) || budget == 0u) break;   // (wave-uniform)
+            __builtin_amdgcn_s_sleep(1);
+            --budget;
+        }
+        v4u ow[NG];
+#pragma unroll
+        for (int g4 = 0; g4 < NG; ++g4) ow[g4] = __builtin_amdgcn_raw_buffer_load_b128(ro, vo, g4 * D * 16, kAgentSC1);
+#pragma unroll
+        for (int g4 = 0; g4 < NG; ++g4)
+            if (g4 >= ngrp) ow[g4] = v4u{kGqaKey, kGqaKey, kGqaKey, kGqaKey};   // (wave-uniform)
+        // poll what was not published yet (a published word keeps its value
+        // for the rest of the call, so the whole burst is simply re-read;
+        // the padding entries set above are nonzero and stay so)
+        while (budget != 0u) {
+            bool pending = false;
+#pragma unroll
+            for (int g4 = 0; g4 < NG; ++g4)
+                pending |= (ow[g4][0] == 0u) | (ow[g4][1] == 0u) | (ow[g4][2] == 0u) | (ow[g4][3] == 0u);
+            if (!pending) break;
+            __builtin_amdgcn_s_sleep(1);
+            --budget;
+#pragma unroll
+            for (int g4 = 0; g4 < NG; ++g4) {
+                const v4u w = __builtin_amdgcn_raw_buffer_load_b128(ro, vo, g4 * D * 16, kAgentSC1);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ow[g4][j] = ow[g4][j] != 0u ? ow[g4][j] : w[j];
+            }
+        }
+        const float mc = bits_f32(mw ^ kGqaKey);
+        if (nc <= kFlashCB) M = wave_max64_all(mc);
+        const float ac = mine ? spec_expf(mc - M) : 0.0f;
+        const float lc = bits_f32(lw ^ kGqaKey);
+#pragma unroll
+        for (int c = 0; c < kFlashCB; ++c) {
+            const float al = bits_f32(__builtin_amdgcn_readlane(f32_bits(ac), c));
+            L = __builtin_fmaf(al, bits_f32(__builtin_amdgcn_readlane(f32_bits(lc), c)), L);
+            O = __builtin_fmaf(al, bits_f32(ow[c >> 2][c & 3] ^ kGqaKey), O);
+            // (the broadcasts stay next to their use: hoisted, 128 of them
+            // would not fit the scalar registers)
+            if ((c & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+        // the words go back to 0 (each is read by this lane alone -- m_c and
+        // l_c are this unit's own copies -- and the first pass over m_c
+        // above is done)
+        if (chain) {
+#pragma unroll
+            for (int g4 = 0; g4 < NG; ++g4)
+                __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, ro, vo, g4 * D * 16, kAgentSC1);
+        }
+        if (mine) {
+            __builtin_amdgcn_raw_buffer_store_b32(0u, rm, lane * 4, 0, kAgentSC1);
+            __builtin_amdgcn_raw_buffer_store_b32(0u, rl, lane * 4, 0, kAgentSC1);
+        }
+    }
+    if (chain) a.out[size_t(hraw) * D + d] = O * (1.0f / L);
+}
+
+template <int D, int GMAX>
+__global__ __launch_bounds__(kFlashThreads) void gqa_flash_kernel(FlashParams a)
+{
+    __shared__ FlashLds<D, GMAX> lds;
+    const int items = a.nc * a.kv;
+    const int b = blockIdx.x;
+    if (b < items) flash_item<D, GMAX>(a, lds, b / a.kv, b % a.kv);   // (block-uniform)
+    else if (threadIdx.x < kWave) flash_combine<D>(a, b - items);
+}
+
+template <int D, int GMAX>
+static void launch_flash(const FlashParams& a, hipStream_t s)
+{
+    const int H = a.kv * a.G;
+    const int blocks = a.nc * a.kv + (a.nc > 1 ? H * flash_units_per_head<D>() : 0);
+    hipLaunchKernelGGL((gqa_flash_kernel<D, GMAX>), dim3(blocks), dim3(kFlashThreads), 0, s, a);
+}
+
+// head_dim 16/32/64/128, groups <= 8 (checked by the caller)
+static hipError_t launch_gqa_flash(const float* query, const uint16_t* keys, const uint16_t* values, uint32_t* words,
+                                   float* output, int context, int kv_heads, int groups, int head_dim, hipStream_t s)
+{
+    FlashParams a{};
+    a.q = query;
+    a.keys = keys;
+    a.values = values;
+    a.words = words;
+    a.out = output;
+    a.time_stride = (long long)kv_heads * head_dim;
+    a.n = context;
+    a.nc = (context + kAttnChunk - 1) / kAttnChunk;
+    a.kv = kv_heads;
+    a.G = groups;
+    switch (head_dim) {
+    case 16: launch_flash<16, 8>(a, s); break;
+    case 32: launch_flash<32, 8>(a, s); break;
+    case 64: launch_flash<64, 8>(a, s); break;
+    default:
+        if (groups <= 4) launch_flash<128, 4>(a, s);
+        else launch_flash<128, 8>(a, s);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace hq
 
 using namespace hq;
@@ -964,9 +1389,11 @@ extern "C" size_t hq_gqa_workspace_bytes(int score_stride, int kv_heads, int gro
 {
     if (score_stride <= 0 || kv_heads <= 0 || groups <= 0 || head_dim <= 0) return 0;
     const int nc = (score_stride + kAttnChunk - 1) / kAttnChunk;
-    // a 256-byte header (reserved), then the chunk partials: one workspace
+    // a 256-byte header (reserved), then the chunk partials of whole groups
+    // of four chunks (D + 2 words per query head and chunk, and up to two
+    // more for the combine units' own copies of m and l): one workspace
     // serves every context up to score_stride
-    return 256 + attention_workspace_floats(kv_heads * groups, nc, head_dim) * 4;
+    return 256 + attention_workspace_floats(kv_heads * groups, (nc + 3) & ~3, head_dim + 2) * 4;
 }
 
 // Checks and launch shared by hq_gqa_decode and hq_gqa_decode_noalloc.
@@ -986,20 +1413,9 @@ static int gqa_check(const float* query, const uint16_t* keys, const uint16_t* v
 static int gqa_launch(const float* query, const uint16_t* keys, const uint16_t* values, void* workspace,
                       float* output, int context, int kv_heads, int groups, int head_dim, hipStream_t stream)
 {
-    const int nc = (context + kAttnChunk - 1) / kAttnChunk;
-    AttnParams a{};
-    a.q = query;
-    a.keys = const_cast<uint16_t*>(keys);
-    a.values = const_cast<uint16_t*>(values);
-    a.time_stride = kv_heads * head_dim;
-    a.context = context;
-    a.kv_heads = kv_heads;
-    a.groups = groups;
-    a.head_dim = head_dim;
-    a.max_chunks = nc;
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
-    a.out = output;
-    const hipError_t e = launch_attention(a, false, stream);
+    uint32_t* words = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + 256);
+    const hipError_t e = launch_gqa_flash(query, keys, values, words, output, context, kv_heads, groups, head_dim,
+                                          stream);
     return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }
 

@@ -235,6 +235,14 @@ __device__ __forceinline__ int read_i(const int* p)
 }
 // Wait until every memory operation this thread issued has completed.
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+// Wait until at most n (0..2) of this wave's vector memory loads are
+// outstanding (they complete in issue order); n is wave-uniform.
+__device__ __forceinline__ void wait_vm_le(int n)
+{
+    if (n >= 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 
 // A pointer every lane holds the same value of, as a scalar (SGPR) value:
 // loads through it take a 32-bit per-lane offset.
@@ -246,6 +254,19 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p)
     const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
     return reinterpret_cast<const T*>((uint64_t(hi) << 32) | lo);
 }
+
+// A raw buffer resource over [p, p + bytes) (gfx9 layout, stride 0): loads
+// through it take a 32-bit lane offset plus a scalar offset, so a burst of
+// loads at scalar distances from one lane address holds one VGPR of
+// address; a load at or past `bytes` returns 0 and touches no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p, int bytes = 0x7fffffff)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform_ptr(p)), 0,
+                                             __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+// Cache-policy bit of a buffer access that is coherent at agent scope (the
+// bits of an agent-scope atomic load or store).
+constexpr int kAgentSC1 = 16;
 
 // LDS byte address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_addr(const void* p)

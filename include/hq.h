@@ -69,9 +69,9 @@ int hq_quantize_activation(const float* x, int n, int8_t* q, float* act_scale, v
 int hq_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps, void* stream);
 
 /* ------------------------------------------- GQA decode attention --
- * Fused single-token GQA attention (score, softmax and V accumulation in
- * one kernel; past 64 positions a second kernel combines the 64-position
- * chunks).  Replaces litespark_gqa_decode (cpu_kernels/
+ * Fused single-token GQA attention: score, softmax and V accumulation in
+ * one launch (per 64-position chunk, with the chunks' combine in the same
+ * launch).  Replaces litespark_gqa_decode (cpu_kernels/
  * litespark_int4.cpp:160-171, bound at cpu_lightspark.py:102-111) with the
  * same argument list and meaning:
  * query fp32 [kv_heads*groups, head_dim], heads ordered [kv_head, group];
@@ -82,10 +82,12 @@ int hq_rmsnorm(const float* x, const float* gamma, float* y, int n, float eps, v
  * [kv_heads*groups, score_stride] (the caller passes state.capacity,
  * cpu_lightspark.py:405), so context <= score_stride.  `workspace` takes the
  * place of that scratch: at least hq_gqa_workspace_bytes(score_stride, ...)
- * bytes, 256-byte aligned; it needs no initialisation (a call writes every
- * chunk partial it reads), and one workspace serves every call with the
- * same or a smaller score_stride.  Calls sharing a workspace must not
- * overlap.  head_dim in {16, 32, 64, 128}; groups <= 8; context >= 1;
+ * bytes, 256-byte aligned, zero-filled before its first use: a call hands
+ * the chunk partials between its blocks through words that are nonzero once
+ * written, and clears every word it used before it returns, so the
+ * workspace is zero again after each call; one workspace serves every call
+ * with the same or a smaller score_stride.  Calls sharing a workspace must
+ * not overlap.  head_dim in {16, 32, 64, 128}; groups <= 8; context >= 1;
  * keys and values 16-byte aligned. */
 size_t hq_gqa_workspace_bytes(int score_stride, int kv_heads, int groups, int head_dim);
 int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* values,
@@ -99,10 +101,10 @@ int hq_gqa_decode(const float* query, const uint16_t* keys, const uint16_t* valu
  * the workspace is a 4 MiB file-scope device array that each GPU holds until
  * the process ends, so the call returns HQ_ERR_ARG when
  * hq_gqa_workspace_bytes(context, kv_heads, groups, head_dim) exceeds 4 MiB
- * (32 query heads of 128 dims: context <= 16128).  Every call on a GPU shares
- * that GPU's array: calls that overlap on one GPU race.  The array needs no
- * clearing (a call writes every chunk partial it reads); no hipMalloc,
- * hipFree or memset is called. */
+ * (32 query heads of 128 dims: context <= 15872).  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU race.  The array starts
+ * zero-filled and every call leaves it zero (as hq_gqa_decode leaves its
+ * workspace); no hipMalloc, hipFree or memset is called. */
 int hq_gqa_decode_noalloc(const float* query, const uint16_t* keys, const uint16_t* values,
                           float* output, int context, int kv_heads, int groups, int head_dim,
                           int score_stride, void* stream);
