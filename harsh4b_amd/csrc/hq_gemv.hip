@@ -125,6 +125,32 @@ __device__ __forceinline__ int wave_row(const GemvParams& p, int tile, int wave,
     }
 }
 
+// The epilogue operands of this lane's row of a tile (lane r < RPW
+// finishes row r of its wave): the row scale (SwiGLU: gate and up scales)
+// and, for EPI_RESIDUAL, the residual value.  Loaded with the tile's
+// weights, so the epilogue waits for no memory round trip of its own;
+// clamped (unconditional) loads, a row past the matrix re-reads the last.
+struct EpiOperands {
+    float s0, s1, x;
+};
+template <int LPR, int EPI>
+__device__ __forceinline__ EpiOperands load_epi(const GemvParams& p, int tile, int wave, int lane)
+{
+    EpiOperands e{0.0f, 0.0f, 0.0f};
+    bool ok;
+    const int r = wave_row<LPR, EPI>(p, tile, wave, lane % (kWave / LPR), ok);
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int gr = min(r, p.half_rows - 1);
+        e.s0 = p.ws[gr];
+        e.s1 = p.ws[p.half_rows + gr];
+    } else {
+        const int rr = min(r, p.rows - 1);
+        e.s0 = p.ws[rr];
+        if constexpr (EPI == EPI_RESIDUAL) e.x = p.out[rr];
+    }
+    return e;
+}
+
 template <int MAXC, int LPR>
 __device__ __forceinline__ void load_tile(const uint8_t* wrow, int li, int nchunks, uint4 (&wv)[MAXC])
 {
@@ -169,6 +195,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     const uint8_t* wrow = p.w + size_t(valid ? row : 0) * size_t(K >> 1);
     uint4 wv[MAXC];
     load_tile<MAXC, LPR>(wrow, li, nchunks, wv);
+    EpiOperands eo = load_epi<LPR, EPI>(p, tile, wave, lane);
     // keep the scheduler from sinking the weight loads below the first use
     // of the activations: the HBM stream must start before any wait
     __builtin_amdgcn_sched_barrier(0);
@@ -184,11 +211,13 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
         // 3. prefetch the next tile (persistent), dot products of this one
         const int next = tile + int(gridDim.x);
         uint4 wn[PERSIST ? MAXC : 1];
+        EpiOperands en{};
         if constexpr (PERSIST) {
             if (next < ntiles) {
                 bool nvalid;
                 const int nrow = wave_row<LPR, EPI>(p, next, wave, rsel, nvalid);
                 load_tile<MAXC, LPR>(p.w + size_t(nvalid ? nrow : 0) * size_t(K >> 1), li, nchunks, wn);
+                en = load_epi<LPR, EPI>(p, next, wave, lane);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -238,8 +267,8 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
                 const int gr = wave_row<LPR, EPI>(p, tile, wave, lane, ok);
                 if (ok) {
                     const int ur = p.half_rows + gr;
-                    const float g = (float(acc) * act) * p.ws[gr];
-                    const float u = (float(acc_up) * act) * p.ws[ur];
+                    const float g = (float(acc) * act) * eo.s0;
+                    const float u = (float(acc_up) * act) * eo.s1;
                     if (p.acc_out) { p.acc_out[gr] = acc; p.acc_out[ur] = acc_up; }
                     if (p.out_aux) { p.out_aux[gr] = g; p.out_aux[ur] = u; }
                     const float t = 1.0f + spec_expf(-g);
@@ -250,13 +279,13 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
             bool ok;
             const int r = wave_row<LPR, EPI>(p, tile, wave, lane, ok);
             if (ok) {
-                const float v = (float(acc) * act) * p.ws[r];
+                const float v = (float(acc) * act) * eo.s0;
                 if (p.acc_out) p.acc_out[r] = acc;
                 if constexpr (EPI == EPI_STORE) {
                     p.out[r] = v;
                 } else if constexpr (EPI == EPI_RESIDUAL) {
                     if (p.out_aux) p.out_aux[r] = v;
-                    p.out[r] = p.out[r] + v;
+                    p.out[r] = eo.x + v;
                 } else {   // EPI_ARGMAX
                     p.out[r] = v;
                     if (argmax_better(v, r, best_v, best_i)) { best_v = v; best_i = r; }
@@ -267,6 +296,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
         if (next >= ntiles) break;
 #pragma unroll
         for (int j = 0; j < MAXC; ++j) wv[j] = wn[j];
+        eo = en;
         tile = next;
     }
 
