@@ -65,6 +65,15 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="CPU time of each decode baseline run (the GEMV runs take a quarter of it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--batch-fill", action="store_true",
+                    help="batched workload: fill each sequence's cache with N(0,1) K/V instead of prefilling "
+                         "its prompt (the PMC runs then see only the decode step's kernels)")
+    ap.add_argument("--pmc-kernels", nargs=5, metavar=("MFMA_DIR", "FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR",
+                                                       "COPY_WRITE_DIR"),
+                    help="fold rocprofv3 --pmc runs of one workload into per-kernel MFMA utilisation, int8 "
+                         "TOP/s and HBM bytes (MFMA_DIR: SQ_INSTS_VALU_MFMA_MOPS_I8, SQ_VALU_MFMA_BUSY_CYCLES, "
+                         "GRBM_GUI_ACTIVE; FETCH_DIR: FETCH_SIZE; WRITE_DIR: WRITE_SIZE; COPY_*: the same "
+                         "counters over --workload copy)")
     ap.add_argument("--batch-sizes", default="8,16,32",
                     help="batched: comma-separated M values; value is the largest M's rate")
     ap.add_argument("--no-configs", action="store_true",
@@ -195,6 +204,62 @@ def time_layers(lib, model, state, launches, reps, torch):
     return e0.elapsed_time(e1) / (reps * launches)
 
 
+def body_gemv_metric(cfg, per_kind_ms, layers_ms):
+    """The body-GEMV bandwidth as the metric is defined: the packed body
+    weight bytes of one token (1,816,657,920 at Qwen3-4B) over the summed
+    durations of the token's body-GEMV kernels.  Those are separate kernels
+    only in the five-kernels-per-layer form (36 x qkv, o, gate_up, down, each
+    with its fused norm/quant prologue and epilogue, timed from graphs of
+    each kind's 36 launches); in the fused step they share one persistent
+    launch with attention, norms and hand-offs, and the weight stream cannot
+    be timed apart, so that launch's figure (body bytes over its whole time,
+    a lower bound) is given beside it."""
+    from harsh4b_amd.config import body_bytes
+    L = int(cfg["num_hidden_layers"])
+    nbytes = body_bytes(cfg)
+    us = L * sum(per_kind_ms.values()) * 1e3
+    gbs = nbytes / (us * 1e-6) / 1e9
+    fused_gbs = nbytes / (layers_ms * 1e-3) / 1e9
+    return {"bytes_per_token": nbytes, "us_per_token": round(us, 2), "achieved": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "kernels": "gemv_kernel x 144 per token (five-kernels-per-layer form)",
+            "fused_step": {"us_per_token": round(layers_ms * 1e3, 2), "achieved": round(fused_gbs, 1),
+                           "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
+                           "note": "body weight bytes / the persistent layer kernel's whole time (attention, "
+                                   "norms and hand-offs included)"}}
+
+
+def sampled_case(model, prompt, steps, warmup, seed):
+    """The same decode with the reference runner's default stochastic
+    sampler (temperature 0.7, top-k 40, top-p 0.9, repetition penalty 1.08;
+    cpu_lightspark.py:706-726) on the GPU: a fresh state prefilled with the
+    prompt, `warmup` sampled steps, then `steps` timed with HIP events."""
+    import numpy as np
+    import torch
+    from types import SimpleNamespace
+    from harsh4b_amd.lightspark import sample_logits
+    policy = SimpleNamespace(argmax=False, temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.08)
+    generator = np.random.default_rng(seed)
+    state = model.new_state(len(prompt) + warmup + steps + 4)
+    model.prefill(prompt, state)
+    generated = [sample_logits(state.logits, [], policy, generator)]
+    generated += model.decode_sampled(state, warmup, policy, generator, generated)
+    state.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(state.stream)
+    generated += model.decode_sampled(state, steps, policy, generator, generated)
+    e1.record(state.stream)
+    torch.cuda.synchronize()
+    state.check_status()
+    tok_s = steps / (e0.elapsed_time(e1) / 1e3)
+    return {"workload": "configs[2] with the reference runner's default stochastic sampler on the GPU "
+                        f"(temperature 0.7, top-k 40, top-p 0.9, repetition penalty 1.08, seed {seed})",
+            "tok_s": round(tok_s, 2), "steps": steps, "warmup": warmup,
+            "vs_baseline": round(tok_s / PUBLISHED_SAMPLED_TOK_S, 2),
+            "baseline": f"{PUBLISHED_SAMPLED_TOK_S} tok/s (the reference's published default-sampler decode rate)"}
+
+
 def cpu_info():
     """CPU model, logical CPUs this process may run on, and the host's
     physical cores (distinct physical id / core id pairs)."""
@@ -240,11 +305,17 @@ def cpu_runs(run, seconds, unit, sample, kind="port"):
             else "scalar", **cpu_info()}
 
 
+CPU_WARMUP_TOKENS = 8   # the reference's decode rate skips 8 warm-up tokens (cpu_lightspark.py:735, 882-890)
+
+
 def oracle_decode_rate(ref, state, ctx, seconds, token=1000):
-    """tok/s of the oracle decoding from a cache of `ctx` positions (the
-    position is reset before the run, so every run sees the same context)."""
+    """tok/s of the oracle decoding from a cache of `ctx` positions after
+    CPU_WARMUP_TOKENS untimed tokens (the position is reset before the run,
+    so every run sees the same context); the state's capacity must leave
+    room for the warm-up and the timed tokens."""
     state.position = ctx
-    token = ref.forward_token(token, state)      # warm-up step (page-in, thread spin-up)
+    for _ in range(CPU_WARMUP_TOKENS):
+        token = ref.forward_token(token, state)
     n, t0 = 0, time.perf_counter()
     while True:
         token = ref.forward_token(token, state)
@@ -378,14 +449,15 @@ def batched_step_bytes(config, m, context):
     return weights + lm_head + m * per_seq
 
 
-def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None):
+def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None, fill=False):
     """batched greedy decode of M independent sequences (M in
     `sizes`) at context `ctx` (each prefilled with its own random ctx-token
-    prompt), one hq_decode_batch step per token of every sequence, replayed
-    from a HIP graph.  Per M: the step time, sequence-tokens/s, the step's
-    HBM bytes over its time (weights once per step + M K/V caches), and the
-    ratio to M batch-1 decode steps of the same model at the same context.
-    The largest M gives the case's value and roofline."""
+    prompt, or with `fill` given N(0,1) K/V in its cache), one hq_decode_batch
+    step per token of every sequence, replayed from a HIP graph.  Per M: the
+    step time, sequence-tokens/s, the step's HBM bytes over its time (weights
+    once per step + M K/V caches), and the ratio to M batch-1 decode steps of
+    the same model at the same context.  The largest M gives the case's value
+    and roofline."""
     import numpy as np
     import torch
     cfg = model.config
@@ -394,6 +466,12 @@ def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None):
 
     def prompt(i):
         return [int(t) for t in np.random.default_rng(4 + i).integers(0, vocab, ctx)]
+
+    def start(st, i):
+        if fill:
+            fill_long(st, ctx, torch)
+        else:
+            model.prefill(prompt(i), st)
 
     def timed(fn):
         torch.cuda.synchronize()
@@ -407,7 +485,7 @@ def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None):
 
     # batch 1 at the same context: the rate M independent steps would have
     one = model.new_state(cap)
-    model.prefill(prompt(0), one)
+    start(one, 0)
     model.decode_greedy(one, warmup)
     t1 = timed(lambda: model.decode_greedy(one, steps, check_status=False))
     one.check_status()
@@ -419,7 +497,7 @@ def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None):
         states = []
         for i in range(m):
             st = model.new_state(cap)
-            model.prefill(prompt(i), st)
+            start(st, i)
             states.append(st)
         model.decode_greedy_batch(states, warmup)          # captures the batched step
         t = timed(lambda: model.decode_greedy_batch(states, steps, check_status=False))
@@ -440,7 +518,8 @@ def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None):
     top_m = sizes[-1]
     top = per_m[top_m]
     res = {"workload": f"configs[3]: batched decode of M = {'/'.join(map(str, sizes))} sequences at context "
-                       f"{ctx}, each with its own fp16 KV cache, greedy; value at M = {top_m}",
+                       f"{ctx}, each with its own fp16 KV cache ({'N(0,1) K/V' if fill else 'prefilled prompt'}), "
+                       f"greedy; value at M = {top_m}",
            "value": top["tok_s"], "unit": "sequence-tok/s", "steps": steps, "warmup": warmup,
            "ms_per_step": top["ms_per_step"],
            "roofline": {"kernel": f"whole batched step (hq_decode_batch), M={top_m}", "bound": "hbm",
@@ -465,7 +544,8 @@ def bench_batched(args):
         raise SystemExit("--batch-sizes needs positive integers")
     print(f"# building random Qwen3-4B int4 model (seed {args.seed})", file=sys.stderr, flush=True)
     model = random_model(QWEN3_4B, seed=args.seed)
-    case = batched_case(model, ctx, sizes, steps, warmup, 0 if args.no_cpu_baseline else args.cpu_seconds)
+    case = batched_case(model, ctx, sizes, steps, warmup, 0 if args.no_cpu_baseline else args.cpu_seconds,
+                        fill=args.batch_fill)
     top_m = sizes[-1]
     result = {"metric": f"batched greedy decode sequence-tokens/s (configs[3], M={top_m}, context {ctx})",
               "value": case["value"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -611,7 +691,8 @@ def layer_case(cfg, per_kind_ms, layers_ms, ref_arrays, cpu_seconds):
     sum of the four standalone GEMV kernels (timed from graphs of each kind's
     36 launches), and the layer kernel's per-layer share (its attention and
     hand-offs included).  CPU: the oracle's fused quant + GEMV over layer 0's
-    four matrices."""
+    four matrices of each layer in turn (all 36, so the host's caches do not
+    hold the weights)."""
     L = int(cfg["num_hidden_layers"])
     alg = algorithmic_bytes(cfg)
     nbytes = sum(alg.values())
@@ -631,21 +712,24 @@ def layer_case(cfg, per_kind_ms, layers_ms, ref_arrays, cpu_seconds):
         import numpy as np
         import oracle
         rng = np.random.default_rng(7)
-        mats = []
-        for name in ("qkv", "o", "gate_up", "down"):
-            w, s = ref_arrays[name][0], ref_arrays[name + "_scales"][0]
-            mats.append((rng.standard_normal(2 * w.shape[1]).astype(np.float32), w, s))
+        layers = []
+        for li in range(L):
+            mats = []
+            for name in ("qkv", "o", "gate_up", "down"):
+                w, s = ref_arrays[name][li], ref_arrays[name + "_scales"][li]
+                mats.append((rng.standard_normal(2 * w.shape[1]).astype(np.float32), w, s))
+            layers.append(mats)
 
         def run(sec):
             n, t0 = 0, time.perf_counter()
             while time.perf_counter() - t0 < sec or n < 4:
-                for x, w, s in mats:
+                for x, w, s in layers[n % L]:
                     oracle.quant_int4_gemv(x, w, s)
                 n += 1
             el = time.perf_counter() - t0
             return n * nbytes / el / 1e9, f"{n} layers in {el:.1f} s ({el / n * 1e3:.2f} ms per layer)"
         res["cpu_baseline"] = cpu_runs(run, cpu_seconds, "GB/s", "fused quant + GEMV of the four body matrices "
-                                                                   "of layer 0")
+                                                                   f"of each of the {L} layers in turn")
     return res
 
 
@@ -735,7 +819,7 @@ def long_case(args, model, lib, cfg, ref, cpu_seconds, short):
                                   "note": f"extra K/V bytes read at context {context} over context {short[0]} "
                                           "/ the extra layer-kernel time"}}
     if cpu_seconds and ref is not None:
-        rs = oracle_state_from(ref, state, context - 1, context + 64)
+        rs = oracle_state_from(ref, state, context - 1, context + CPU_WARMUP_TOKENS + 256)
         res["cpu_baseline"] = cpu_runs(lambda sec: oracle_decode_rate(ref, rs, context - 1, sec), cpu_seconds,
                                        "tok/s", f"decode steps of the same model at context {context}, "
                                                 "OpenMP over GEMV rows (oracle/hq_oracle.c)")
@@ -799,6 +883,21 @@ def pmc_counter(directory, counter):
     return {k: (len(v), sum(v) / len(v)) for k, v in rows.items()}
 
 
+def pmc_durations(directory):
+    """Mean dispatch duration (ns, from the rows' timestamps) of each kernel
+    in a rocprofv3 CSV output directory -> {kernel: ns}."""
+    import csv
+    seen = {}
+    for f in Path(directory).rglob("*counter_collection.csv"):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                seen[(r["Kernel_Name"], r["Dispatch_Id"])] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    per = {}
+    for (k, _), ns in seen.items():
+        per.setdefault(k, []).append(ns)
+    return {k: sum(v) / len(v) for k, v in per.items()}
+
+
 def pmc_summary(args):
     """HBM traffic per launch of the layer kernel from two rocprofv3 --pmc
     runs of --workload layers (FETCH_SIZE, then WRITE_SIZE; KiB per
@@ -830,6 +929,52 @@ def pmc_summary(args):
                                 "ratio": round(traffic / alg, 4)}]}, indent=1), flush=True)
 
 
+MI355X_CLOCK_GHZ = 2.4   # peak engine clock: MFMA utilisation against it is a lower bound
+
+
+def pmc_kernels(args):
+    """Per-kernel counters of one workload from rocprofv3 --pmc runs: MFMA
+    utilisation (SQ_VALU_MFMA_BUSY_CYCLES, summed over the SIMDs, / (the
+    dispatch's duration x the 2.4 GHz peak clock x 1024 SIMDs)), int8 MFMA
+    ops per dispatch (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512) and per second of the
+    dispatch, and HBM bytes per dispatch (FETCH_SIZE, WRITE_SIZE scaled by a
+    256 MiB copy's readings).  Durations are those of the counter runs
+    (dispatches serialized by the profiler)."""
+    mfma_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir = args.pmc_kernels
+    copy_bytes = 256 << 20
+
+    def copy_kib(d, counter):
+        for k, (_, v) in pmc_counter(d, counter).items():
+            if "copyBuffer" in k or "copy" in k.lower():
+                return v
+        raise SystemExit(f"no copy kernel in {d}")
+    ff = copy_bytes / (copy_kib(cfetch_dir, "FETCH_SIZE") * 1024)
+    wf = copy_bytes / (copy_kib(cwrite_dir, "WRITE_SIZE") * 1024)
+    mops = pmc_counter(mfma_dir, "SQ_INSTS_VALU_MFMA_MOPS_I8")
+    busy = pmc_counter(mfma_dir, "SQ_VALU_MFMA_BUSY_CYCLES")
+    dur = pmc_durations(mfma_dir)
+    fetch, write = pmc_counter(fetch_dir, "FETCH_SIZE"), pmc_counter(write_dir, "WRITE_SIZE")
+    simds = 256 * 4
+    rows = []
+    for k in sorted(mops, key=lambda n: -mops[n][0] * dur.get(n, 0.0)):
+        n = mops[k][0]
+        ns = dur.get(k, 0.0)
+        r = {"kernel": k[:120], "dispatches": n, "us": round(ns / 1e3, 2), "int8_ops": round(mops[k][1] * 512)}
+        if ns > 0:
+            r["int8_TOPS"] = round(mops[k][1] * 512 / ns / 1e3, 2)
+            if k in busy:
+                r["mfma_util"] = round(busy[k][1] / (ns * MI355X_CLOCK_GHZ * simds), 5)
+        if k in fetch:
+            r["hbm_read_bytes"] = round(fetch[k][1] * 1024 * ff)
+        if k in write:
+            r["hbm_write_bytes"] = round(write[k][1] * 1024 * wf)
+        if ns > 0 and "hbm_read_bytes" in r and "hbm_write_bytes" in r:
+            r["hbm_GBs"] = round((r["hbm_read_bytes"] + r["hbm_write_bytes"]) / ns, 1)
+        rows.append(r)
+    print(json.dumps({"calibration": {"fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+                      "kernels": rows[:24]}, indent=1), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -838,6 +983,9 @@ def main():
         sys.exit(2)
     if args.pmc_summary:
         pmc_summary(args)
+        return
+    if args.pmc_kernels:
+        pmc_kernels(args)
         return
     if args.workload == "layers":
         bench_layers(args)
@@ -977,17 +1125,16 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_at(context),
                      "algorithmic_bytes": eng_bytes, "context": context,
                      "us_per_launch": round(layers_ms * 1e3, 2)},
-        "body_gemv": {"bytes_per_token": body_bytes(cfg), "us_per_token": round(layers_ms * 1e3, 2),
-                      "achieved": round(body_gbs, 1), "unit": "GB/s",
-                      "frac": round(body_gbs / HBM_PEAK_GBS, 4),
-                      "note": "body weight bytes / layer-kernel time (its attention, norms and "
-                              "hand-offs included)"},
+        "body_gemv": body_gemv_metric(cfg, per_kind_ms, layers_ms),
         "per_layer_kernels": {k: {"us_per_launch": round(per_kind_ms[k] * 1e3, 3),
                                   "GB/s": round(alg[k] / (per_kind_ms[k] * 1e-3) / 1e9, 1)}
                               for k in kinds},
     }
     if prefill_info:
         result["prefill"] = prefill_info
+    if args.workload == "decode" and not args.no_configs:
+        result["sampled"] = sampled_case(model, prompt, args.steps, args.warmup, args.seed)
+        print(f"# sampled decode: {result['sampled']['tok_s']} tok/s", file=sys.stderr, flush=True)
     ref = arrays = None
     if not args.no_cpu_baseline:
         import oracle
@@ -1001,7 +1148,7 @@ def main():
                    "configs[1]": layer_case(cfg, per_kind_ms, layers_ms, arrays, cpu_s / 4),
                    "configs[4]": long_case(args, model, lib, cfg, ref, cpu_s, (context, layers_ms))}
         print("# configs[3]", file=sys.stderr, flush=True)
-        configs["configs[3]"] = batched_case(model, 256, [8, 32], 16, 2, cpu_s / 4, ref)
+        configs["configs[3]"] = batched_case(model, 256, [8, 16, 32], 16, 2, cpu_s / 4, ref)
         result["configs"] = configs
         att = attention_case(args, torch)
         print(f"# hq_gqa_decode at context 4096: {att['us_per_call']:.2f} us, {att['achieved']:.0f} GB/s",
@@ -1010,7 +1157,9 @@ def main():
                                "layer_kernel_marginal_ctx4096": configs["configs[4]"]["attention_marginal"]}
     if ref is not None:
         print("# timing the CPU oracle baseline", file=sys.stderr, flush=True)
-        rs = oracle_state_from(ref, state, args.ctx, state.capacity)
+        # room for the warm-up and about 2000 timed tokens: the sample is
+        # bounded by --cpu-seconds, not by the state
+        rs = oracle_state_from(ref, state, args.ctx, args.ctx + CPU_WARMUP_TOKENS + 2048)
         result["cpu_baseline"] = cpu_baseline(ref, rs, args.ctx, cpu_s)
     print(json.dumps(result), flush=True)
 
