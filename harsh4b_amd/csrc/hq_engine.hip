@@ -704,9 +704,10 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         const bool more = l + 1 < p.L;
         const hq_layer& Ly = S.lay[l];
         const hq_layer& Ln = S.lay[more ? l + 1 : l];
-        // this layer's first GQA item: its K/V copies land while the qkv
-        // GEMV and its hand-off run
-        if (is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<true>(p, l, pos);
+        // the first layer's first GQA item: its K/V copies land while the
+        // qkv GEMV and its hand-off run (later layers issue theirs at the end
+        // of the layer before)
+        if (l == 0 && is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<true>(p, l, pos);
         // ---- P1: qkv
         wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 1), budget, p.status);
         if (ww == 0) TRACE(l, 16);
@@ -781,6 +782,13 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         }
         block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 23);
+        // the next layer's first GQA item: its K/V copies (cached positions
+        // only; the current position's row comes from the qkv hand-off) are
+        // issued now, while the layer's own attention and its combine staging
+        // are done with S.kv.  The next wait that covers them (memory
+        // operations complete in issue order) is the next layer's qkv dot,
+        // a residual hand-off and an RMSNorm prologue later.
+        if (more && is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<true>(p, l + 1, pos);
         if (more) load_window(4 * (l + 1), budget, p.status);
         load_rows<kOLPR, kOC, kPaceO>(wo, so, Ln.o, Ln.o_scales, R.h0, more ? R.h1 : R.h0 + 1, more ? qd : 32, ww);
     }
