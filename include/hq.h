@@ -150,13 +150,17 @@ int hq_sample_token(const float* logits, int n, const int32_t* generated, int n_
  *   output[m, n] = ((float)sum_k W[n,k] * x[m,k] * act_scales[m]) * scales[n]
  * x int8 [m, width]; act_scales fp32 [m]; output fp32 [m, rows];
  * acc_out (nullable) int32 [m, rows].  The products run on int8 MFMA
- * (v_mfma_i32_16x16x64_i8) with the K dimension split across blocks; the
- * split partial sums meet in `workspace` (hq_gemm_workspace_bytes(m, rows,
- * width) bytes, 16-byte aligned, zero-filled before its first use).  A call
- * leaves its accumulator and counter regions at zero again, so a workspace
- * may be reused by later calls of the same (m, rows, width); give calls of
- * other shapes their own workspace.  width % 32 == 0, weights 16-byte
- * aligned, 1 <= m. */
+ * (v_mfma_i32_16x16x64_i8); a block owns whole rows over the whole K (its
+ * waves split K and add their int32 partial tiles in LDS), so no partial
+ * sum crosses blocks.  `workspace` (hq_gemm_workspace_bytes(m, rows, width)
+ * bytes, 16-byte aligned, zero-filled before its first use) holds the
+ * activations re-laid out for the MFMA operands: m rows padded to a
+ * multiple of 16, width padded to a multiple of 256 columns, even/odd
+ * columns de-interleaved per 8, then (hq_quant_int4_gemm) the m activation
+ * scales.  A call never writes the padding, which must stay zero, so a
+ * workspace may be reused by later calls of the same m and width; give
+ * calls of other shapes their own workspace.  width % 32 == 0, weights
+ * 16-byte aligned, 1 <= m. */
 size_t hq_gemm_workspace_bytes(int m, int rows, int width);
 int hq_int4_i8_gemm(const int8_t* x, const float* act_scales, const uint8_t* weights,
                     const float* scales, float* output, int m, int rows, int width,
