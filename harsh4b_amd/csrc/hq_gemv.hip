@@ -6,11 +6,16 @@
 // Restates cpu_kernels/litespark_int4.cpp:22-76 (reference repository):
 // acc[n] = sum_k W[n,k] * x[k] in int32, out[n] = ((float)acc * act) * s[n].
 //
-// Kernel shape (256 threads = 32 lane groups of 8):
-//   * each block owns RB output rows; a row is read by 8*KP lanes
-//     (KP = 32/RB K-parts), each lane loading whole 16-byte chunks
-//     (32 int4 values) with 128-bit loads, so the 8 lanes of a group read
-//     128 contiguous bytes of one row;
+// Two kernel shapes share the prologue and the dot products:
+//   * gemv_kernel: 256-thread blocks of RB rows (the gate_up GEMV with
+//     SwiGLU, the LM head with argmax, persistent over its tiles);
+//   * gemv_rr_kernel: one block per CU with an equal share of the rows, one
+//     wave tile each (the reference-ABI entry points and the qkv, o and
+//     down step GEMVs);
+// and in both:
+//   * a row is read by LPR lanes, each lane loading whole 16-byte chunks
+//     (32 int4 values) with 128-bit loads, so the lanes of a row read
+//     LPR*16 contiguous bytes of it per load;
 //   * all weight loads of a lane are issued before the activation prologue,
 //     so the HBM stream is in flight while the block quantizes x;
 //   * the prologue writes x as int8 into LDS, de-interleaved per 8 columns
@@ -351,6 +356,173 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(GemvParams p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-range GEMV: one block per CU.  The rows are cut into wave tiles of
+// RPW = 64/LPR rows, and block b owns tiles [b*tpb, (b+1)*tpb) (tpb = the
+// tiles per block, ceil(tiles / CUs)), one tile per wave, so every CU
+// streams the same number of rows and no wave loads a row it does not
+// finish.  Each lane holds its C chunks of the row in registers, issued
+// before the activation prologue (wider rows walk further batches of C
+// chunks after the first).  The prologue (quantization, or RMSNorm then
+// quantization, with exactly gemv_kernel's arithmetic) runs on waves 0-3,
+// element i on thread i % 256; the other waves only meet its barriers.
+
+// Waves 0-3 load the activations (element tid + 256*j, clamped); the other
+// waves load element 0 (one cache line), so every wave issues the same
+// unconditional loads ahead of its weight loads.
+template <int XJ, int PRO>
+__device__ __forceinline__ void rr_load_activation(const GemvParams& p, ActRegs<XJ, PRO>& a)
+{
+    if constexpr (PRO != PRO_I8) {
+        const int K = p.width;
+        const int tid = int(threadIdx.x);
+#pragma unroll
+        for (int j = 0; j < XJ; ++j) {
+            const int i = tid < kBlock ? min(tid + kBlock * j, K - 1) : 0;
+            a.x[j] = p.xf[i];
+            if constexpr (PRO == PRO_RMSNORM) a.g[j] = p.gamma[i];
+        }
+    }
+}
+
+template <int XJ, int PRO>
+__device__ __forceinline__ float rr_prologue(const GemvParams& p, ActRegs<XJ, PRO>& a, uint8_t* xs, float* red)
+{
+    const int tid = int(threadIdx.x);
+    const int K = p.width;
+    if constexpr (PRO == PRO_I8) {
+        for (int i = tid; i < K; i += int(blockDim.x)) xs[xq_offset(i)] = uint8_t(p.xq[i]);
+        return p.act_scale;
+    } else {
+        const bool pro = tid < kBlock;
+        if constexpr (PRO == PRO_RMSNORM) {
+            // the spec's 256 strided partials and halving tree
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < XJ; ++j)
+                if (pro && tid + kBlock * j < K) ss = __builtin_fmaf(a.x[j], a.x[j], ss);
+            if (pro) red[tid] = ss;
+            lds_sync();
+            const int l = tid & (kWave - 1);
+            const float total = wave_tree_sum64_all((red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]));
+            lds_sync();   // red is written again below
+            const float r = __builtin_sqrtf(total / float(K) + p.eps);
+#pragma unroll
+            for (int j = 0; j < XJ; ++j) a.x[j] = (a.x[j] / r) * a.g[j];
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < XJ; ++j)
+            if (pro && tid + kBlock * j < K) amax = fmaxf(amax, fabsf(a.x[j]));
+        amax = wave_max64_all(amax);
+        if (pro && (tid & (kWave - 1)) == 0) red[tid / kWave] = amax;
+        lds_sync();
+        amax = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-5f);
+        const float inv = 127.0f / amax;
+        const bool write_q = p.q_out != nullptr && blockIdx.x == 0;
+        if (pro) {
+#pragma unroll
+            for (int j = 0; j < XJ; ++j) {
+                const int i = tid + kBlock * j;
+                if (i < K) {
+                    const int8_t q = quant_i8(a.x[j], inv);
+                    xs[xq_offset(i)] = uint8_t(q);
+                    if (write_q) p.q_out[i] = q;
+                }
+            }
+        }
+        const float act = amax / 127.0f;
+        if (p.act_out != nullptr && blockIdx.x == 0 && tid == 0) *p.act_out = act;
+        return act;
+    }
+}
+
+template <int LPR, int C, int XJ, int PRO, int EPI>
+__global__ __launch_bounds__(1024) void gemv_rr_kernel(GemvParams p, int tpb)
+{
+    static_assert(EPI == EPI_STORE || EPI == EPI_RESIDUAL, "row-range epilogues: store, residual");
+    constexpr int RPW = kWave / LPR;
+    extern __shared__ __align__(16) uint8_t xs[];
+    __shared__ float red[kBlock];
+
+    const int tid = int(threadIdx.x);
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
+    const int li = lane % LPR;
+    const int K = p.width;
+    const int nchunks = K >> 5;
+    // this wave's tile: rows row0 .. row0+RPW-1 (the last tile of the
+    // matrix may hold fewer: its missing rows re-read the matrix's last row)
+    const int row0 = (int(blockIdx.x) * tpb + wave) * RPW;
+    const int row = min(row0 + lane / LPR, p.rows - 1);
+
+    // 1. activation loads, then the weights of the first C chunks of the
+    // row, then the epilogue operands of the row lane r < RPW finishes.
+    // The prologue waves issue their weight loads once the activations
+    // have arrived: issued behind the block's weight loads, the activation
+    // loads wait for them in the memory pipeline and the prologue ends
+    // after the weights (K 2560 -> 9728 rows, 8 lanes per row: 5.69 -> 5.11 us
+    // per call).
+    ActRegs<XJ, PRO> areg;
+    rr_load_activation<XJ, PRO>(p, areg);
+    const uint8_t* wrow = p.w + size_t(row) * size_t(K >> 1);
+    uint4 wv[C];
+    if (__builtin_amdgcn_readfirstlane(wave) < 4) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    load_tile<C, LPR>(wrow, li, nchunks, wv);
+    const int erow = min(row0 + lane % RPW, p.rows - 1);
+    const float es = p.ws[erow];
+    float ex = 0.0f;
+    if constexpr (EPI == EPI_RESIDUAL) ex = p.out[erow];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. activations -> LDS while the weights stream
+    const float act = rr_prologue<XJ, PRO>(p, areg, xs, red);
+    lds_sync();
+
+    // 3. dot products (rows wider than C*LPR chunks take more batches)
+    int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        const int c = li + j * LPR;
+        if (c < nchunks) {
+            if (j & 1) dot_chunk(wv[j], xs + c * 32, a2, a3);
+            else dot_chunk(wv[j], xs + c * 32, a0, a1);
+        }
+    }
+    for (int base = C * LPR; base < nchunks; base += C * LPR) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) wv[j] = load_w16(wrow + size_t(min(base + li + j * LPR, nchunks - 1)) * 16);
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const int c = base + li + j * LPR;
+            if (c < nchunks) {
+                if (j & 1) dot_chunk(wv[j], xs + c * 32, a2, a3);
+                else dot_chunk(wv[j], xs + c * 32, a0, a1);
+            }
+        }
+    }
+    const int part = (a0 + a1) + (a2 + a3);
+
+    // 4. epilogue: lane r < RPW finishes row row0 + r
+    int acc = 0;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int t = row_isum<LPR>(part, r) >> 4;
+        if (lane == r) acc = t;
+    }
+    const int r = row0 + lane;
+    if (lane < RPW && r < p.rows) {
+        const float v = (float(acc) * act) * es;
+        if (p.acc_out) p.acc_out[r] = acc;
+        if constexpr (EPI == EPI_STORE) {
+            p.out[r] = v;
+        } else {
+            if (p.out_aux) p.out_aux[r] = v;
+            p.out[r] = ex + v;
+        }
+    }
+}
+
 // Plain fallback for the reference-signature entry when the fast path's
 // layout conditions (width % 32 == 0, 16-byte aligned rows) do not hold:
 // one wave per row, byte loads, same integer result and epilogue.
@@ -486,18 +658,78 @@ static hipError_t launch_xj(const GemvParams& p, int blocks, hipStream_t s)
 
 constexpr int kMaxWidth = 40 * kBlock;   // 10240: register-resident activation limit
 
-// Lanes per row of each step GEMV (rows per 256-thread tile = 4 * 64 / LPR),
-// chosen so every lane streams 3..10 chunks and the launch fills the chip:
-//   qkv      K 2560  16 lanes/row  5 chunks/lane  384 tiles
-//   o        K 4096  32 lanes/row  4 chunks/lane  320 tiles
-//   gate_up  K 2560   8 lanes/row 10 chunks/lane  608 tiles (16 gate/up pairs)
-//   down     K 9728  32 lanes/row 10 chunks/lane  320 tiles
-//   LM head  K 2560   8 lanes/row 10 chunks/lane 4748 tiles, persistent:
+// Compute units of the current device (cached per device; 0 on error).
+static int device_cus()
+{
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = -1;
+        cus[dev] = n;
+    }
+    return cus[dev] > 0 ? cus[dev] : 0;
+}
+
+// gemv_rr_kernel grid: tiles of 64/LPR rows, tpb = ceil(tiles / CUs) per
+// block, one per wave, at least 4 (the prologue's waves) and at most 16, so
+// one block per CU from 4 * CUs up to 16 * CUs tiles.  Returns the blocks
+// (0 when the device cannot be queried).
+static int rr_blocks(int rows, int lpr, int& tpb)
+{
+    const int cus = device_cus();
+    if (cus == 0) return 0;
+    const int rpw = kWave / lpr;
+    const int tiles = (rows + rpw - 1) / rpw;
+    tpb = min(16, max(4, (tiles + cus - 1) / cus));
+    return (tiles + tpb - 1) / tpb;
+}
+
+template <int LPR, int C, int XJ, int PRO, int EPI>
+static hipError_t launch_rr(const GemvParams& p, hipStream_t s)
+{
+    int tpb = 0;
+    const int blocks = rr_blocks(p.rows, LPR, tpb);
+    if (blocks == 0) return hipErrorInvalidDevice;
+    hipLaunchKernelGGL((gemv_rr_kernel<LPR, C, XJ, PRO, EPI>), dim3(blocks), dim3(tpb * kWave),
+                       size_t(p.width), s, p, tpb);
+    return hipGetLastError();
+}
+
+template <int LPR, int C, int PRO, int EPI>
+static hipError_t launch_rr_xj(const GemvParams& p, hipStream_t s)
+{
+    if (PRO == PRO_I8) return launch_rr<LPR, C, 1, PRO, EPI>(p, s);
+    if (p.width <= 10 * kBlock) return launch_rr<LPR, C, 10, PRO, EPI>(p, s);
+    if (p.width <= 16 * kBlock) return launch_rr<LPR, C, 16, PRO, EPI>(p, s);
+    return launch_rr<LPR, C, 40, PRO, EPI>(p, s);
+}
+
+// Lanes per row of the reference-ABI GEMVs by row width: every lane holds
+// up to 10 chunks of its row (rows past 64 * 10 chunks take further
+// batches).
+template <int PRO>
+static hipError_t launch_rr_width(const GemvParams& p, hipStream_t s)
+{
+    const int chunks = p.width >> 5;
+    if (chunks <= 10 * 8) return launch_rr_xj<8, 10, PRO, EPI_STORE>(p, s);
+    if (chunks <= 10 * 16) return launch_rr_xj<16, 10, PRO, EPI_STORE>(p, s);
+    if (chunks <= 10 * 32) return launch_rr_xj<32, 10, PRO, EPI_STORE>(p, s);
+    return launch_rr_xj<64, 10, PRO, EPI_STORE>(p, s);
+}
+
+// Step GEMV layouts (the five-kernels-per-layer form):
+//   qkv      K 2560  gemv_rr_kernel, 16 lanes/row, 5 chunks/lane   256 blocks
+//   o        K 4096  gemv_rr_kernel, 32 lanes/row, 4 chunks/lane   256 blocks
+//   down     K 9728  gemv_rr_kernel, 64 lanes/row, 5 chunks/lane   256 blocks
+//            (qkv 5.19 -> 4.39 us, o 4.63 -> 4.21, down 8.00 -> 7.52 against
+//            gemv_kernel's 256-thread tiles)
+//   gate_up  K 2560  gemv_kernel, 8 lanes/row, 10 chunks/lane, 608 tiles (16 gate/up pairs)
+//   LM head  K 2560  gemv_kernel, 8 lanes/row, 10 chunks/lane, 4748 tiles, persistent:
 //            2 blocks per CU loop over the tiles
-constexpr int kQkvLPR = 16, kOLPR = 32, kGateLPR = 8, kDownLPR = 32, kHeadLPR = 8;
+constexpr int kGateLPR = 8, kHeadLPR = 8;
 constexpr int kPersistBlocks = 512;   // LM head: 39.0 us; 256 / 768 / 1024 blocks measured 47.4 / 40.2 / 45.4
-constexpr int kDefaultLPR = 32;
-constexpr int kDefaultRB = 4 * (kWave / kDefaultLPR);
 
 static int rows_per_tile(int lpr) { return 4 * (kWave / lpr); }
 static bool lm_head_persistent(int width) { return width <= 10 * kHeadLPR * 32; }
@@ -505,11 +737,12 @@ static bool lm_head_persistent(int width) { return width <= 10 * kHeadLPR * 32; 
 int step_gemv_blocks(StepGemv kind, int rows, int half_rows, int width)
 {
     auto tiles = [](int n, int per) { return (n + per - 1) / per; };
+    int tpb = 0;
     switch (kind) {
-    case StepGemv::Qkv: return tiles(rows, rows_per_tile(kQkvLPR));
-    case StepGemv::OResidual: return tiles(rows, rows_per_tile(kOLPR));
+    case StepGemv::Qkv: return rr_blocks(rows, 16, tpb);
+    case StepGemv::OResidual: return rr_blocks(rows, 32, tpb);
     case StepGemv::GateUpSwiglu: return tiles(half_rows, rows_per_tile(kGateLPR) / 2);
-    case StepGemv::DownResidual: return tiles(rows, rows_per_tile(kDownLPR));
+    case StepGemv::DownResidual: return rr_blocks(rows, 64, tpb);
     case StepGemv::LmHead: {
         const int t = tiles(rows, rows_per_tile(kHeadLPR));
         if (!lm_head_persistent(width)) return t;
@@ -523,10 +756,10 @@ hipError_t launch_step_gemv(StepGemv kind, const GemvParams& p, hipStream_t s)
 {
     const int blocks = step_gemv_blocks(kind, p.rows, p.half_rows, p.width);
     switch (kind) {
-    case StepGemv::Qkv: return launch_xj<kQkvLPR, 5, PRO_RMSNORM, EPI_STORE>(p, blocks, s);
-    case StepGemv::OResidual: return launch_xj<kOLPR, 4, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
+    case StepGemv::Qkv: return launch_rr_xj<16, 5, PRO_RMSNORM, EPI_STORE>(p, s);
+    case StepGemv::OResidual: return launch_rr_xj<32, 4, PRO_QUANT, EPI_RESIDUAL>(p, s);
     case StepGemv::GateUpSwiglu: return launch_xj<kGateLPR, 10, PRO_RMSNORM, EPI_SWIGLU>(p, blocks, s);
-    case StepGemv::DownResidual: return launch_xj<kDownLPR, 10, PRO_QUANT, EPI_RESIDUAL>(p, blocks, s);
+    case StepGemv::DownResidual: return launch_rr_xj<64, 5, PRO_QUANT, EPI_RESIDUAL>(p, s);
     case StepGemv::LmHead:
         if (lm_head_persistent(p.width))   // one weight batch per tile
             return launch_xj<kHeadLPR, 10, PRO_RMSNORM, EPI_ARGMAX, true>(p, blocks, s);
@@ -555,14 +788,7 @@ extern "C" int hq_int4_i8_gemv(const int8_t* x, const uint8_t* weights, const fl
         GemvParams p{};
         p.w = weights; p.ws = scales; p.rows = rows; p.width = width;
         p.xq = x; p.act_scale = activation_scale; p.out = output;
-        // lanes per row as in hq_quant_int4_gemv: up to 10 chunks per lane
-        const int chunks = width >> 5;
-        if (chunks <= 10 * 8)
-            e = launch<8, 10, 1, PRO_I8, EPI_STORE>(p, (rows + rows_per_tile(8) - 1) / rows_per_tile(8), s);
-        else if (chunks <= 10 * 16)
-            e = launch<16, 10, 1, PRO_I8, EPI_STORE>(p, (rows + rows_per_tile(16) - 1) / rows_per_tile(16), s);
-        else
-            e = launch<kDefaultLPR, 8, 1, PRO_I8, EPI_STORE>(p, (rows + kDefaultRB - 1) / kDefaultRB, s);
+        e = launch_rr_width<PRO_I8>(p, s);
     } else {
         const int per = kBlock / kWave;
         hipLaunchKernelGGL(gemv_generic_kernel, dim3((rows + per - 1) / per), dim3(kBlock), 0, s,
@@ -586,17 +812,9 @@ extern "C" int hq_quant_int4_gemv(const float* x, const uint8_t* weights, const 
     p.w = weights; p.ws = scales; p.rows = rows; p.width = width;
     p.xf = x; p.out = output; p.q_out = q_out; p.act_out = act_scale_out; p.acc_out = acc_out;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // lanes per row so that each lane streams up to 10 chunks of its row:
-    // fewer, fuller blocks each redo the quantization prologue (K 2560 ->
-    // 9728 rows: 6.3 us with 32 lanes per row, 1216 blocks)
-    const int chunks = width >> 5;
-    hipError_t e;
-    if (chunks <= 10 * 8)
-        e = launch_xj<8, 10, PRO_QUANT, EPI_STORE>(p, (rows + rows_per_tile(8) - 1) / rows_per_tile(8), s);
-    else if (chunks <= 10 * 16)
-        e = launch_xj<16, 10, PRO_QUANT, EPI_STORE>(p, (rows + rows_per_tile(16) - 1) / rows_per_tile(16), s);
-    else
-        e = launch_xj<kDefaultLPR, 10, PRO_QUANT, EPI_STORE>(p, (rows + kDefaultRB - 1) / kDefaultRB, s);
+    // one block per CU, each with the same number of rows (the prologue is
+    // done once per CU)
+    const hipError_t e = launch_rr_width<PRO_QUANT>(p, s);
     return e == hipSuccess ? HQ_OK : HQ_ERR_LAUNCH;
 }
 

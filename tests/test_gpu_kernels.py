@@ -69,6 +69,22 @@ def test_gemv_unaligned_weights_take_generic_path():
     assert_bits_equal(to_host(out), oracle.int4_i8_gemv(x, packed, s, 0.5, rows, width), "unaligned")
 
 
+@pytest.mark.parametrize("rows,width", [(9728, 2560), (1001, 4096), (300, 20480), (7, 32768), (5000, 64)])
+def test_gemv_int8_row_range_shapes(rows, width):
+    # the reference-signature entry over the lane layouts of every width
+    # class, rows that leave the last wave tile partly empty, and rows wider
+    # than one batch of chunks per lane (32768: two batches)
+    ls = lightspark()
+    rng = np.random.default_rng(rows + 3 * width)
+    w = random_int4(rng, rows, width)
+    packed = oracle.pack_int4(w)
+    x = rng.integers(-127, 128, size=width, dtype=np.int8)
+    s = rng.uniform(0.005, 0.02, rows).astype(np.float32)
+    p = ls.LiteSparkProjection(to_dev(packed), to_dev(s))
+    got = to_host(ls.int4_i8_gemv(to_dev(x), p, 0.0071))
+    assert_bits_equal(got, oracle.int4_i8_gemv(x, packed, s, 0.0071, rows, width), "row-range gemv")
+
+
 QUANT_SHAPES = [(9728, 2560), (6144, 2560), (2560, 4096), (2560, 9728), (19456, 2560),
                 (1000, 2560), (64, 64), (33, 10240), (8191, 4096)]
 
