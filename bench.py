@@ -82,14 +82,15 @@ def parse():
                     help="print the traffic summary of rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE output "
                          "directories of --workload layers and --workload copy runs")
     ap.add_argument("--workload", choices=("decode", "sampled", "sample", "long", "batched", "gemv", "copy",
-                                           "layers"),
+                                           "layers", "attention"),
                     default="decode",
                     help="decode: configs[2] (the reported line); sampled: the same decode with the "
                          "reference runner's default stochastic sampler (temperature 0.7, top-k 40, "
                          "top-p 0.9, repetition penalty 1.08) on the GPU; sample: that sampler alone, per "
                          "top-k; long: configs[4], the same decode "
                          "at context 4096 over an N(0,1) fp16 KV cache; batched: configs[3], the "
-                         "body GEMMs of M = 8/16/32 sequences on int8 MFMA against M GEMVs; gemv: "
+                         "body GEMMs of M = 8/16/32 sequences on int8 MFMA against M GEMVs; attention: the "
+                         "standalone hq_gqa_decode at --ctx (default 4096); gemv: "
                          "configs[0], one fused quant + int4 GEMV 2560 -> 9728 over rotating weight "
                          "copies; copy: a plain 256 MiB device-to-device copy, the calibration kernel "
                          "of the PMC traffic counters; layers: the layer kernel alone, launched "
@@ -779,6 +780,23 @@ def attention_case(args, torch, context=4096):
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def bench_attention(args):
+    """The standalone hq_gqa_decode at one layer's shape and context --ctx
+    (default 4096) as its own JSON line (for rocprofv3 runs of that kernel
+    alone)."""
+    import torch
+    ctx = args.ctx if args.ctx is not None else 4096
+    res = attention_case(args, torch, context=ctx)
+    print(json.dumps({"metric": "standalone fused GQA decode (hq_gqa_decode) HBM GB/s", "value": res["achieved"],
+                      "unit": "GB/s", "n_gpus": 1, "steps": max(2, args.gemv_reps) * 36, "warmup": 36,
+                      "us_per_call": res["us_per_call"], "higher_is_better": True, "dtype": "fp16/f32",
+                      "data": "synthetic: N(0,1) fp16 K/V, 32 query / 8 kv heads x 128",
+                      "config": {"workload": f"hq_gqa_decode at context {ctx}, 36 distinct caches"},
+                      "roofline": {"kernel": res["kernel"], "bound": "hbm", "achieved": res["achieved"],
+                                   "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": res["frac"], "traffic": None,
+                                   "algorithmic_bytes": res["algorithmic_bytes"]}}), flush=True)
+
+
 def long_case(args, model, lib, cfg, ref, cpu_seconds, short):
     """the batch-1 decode at context 4096 over an N(0,1) fp16 KV
     cache: the layer kernel at the line's context (roofline with the K/V
@@ -1001,6 +1019,9 @@ def main():
         return
     if args.workload == "batched":
         bench_batched(args)
+        return
+    if args.workload == "attention":
+        bench_attention(args)
         return
     import numpy as np
     import torch
