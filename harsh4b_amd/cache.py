@@ -64,6 +64,12 @@ def slug(name: str) -> str:
     return name.replace(".", "_")
 
 
+def identity_digest(identity: dict) -> str:
+    """The 16-hex-digit directory name of an identity record
+    (cpu_lightspark.py:242)."""
+    return hashlib.sha256(json.dumps(identity, sort_keys=True).encode()).hexdigest()[:16]
+
+
 def cache_identity(model_path) -> tuple[str, dict]:
     """Identity record and directory digest of a checkpoint's cache
     (cpu_lightspark.py:232-243): the cache of model_path lives in
@@ -78,8 +84,7 @@ def cache_identity(model_path) -> tuple[str, dict]:
         "format": CACHE_FORMAT,
         "embedding": EMBEDDING_FORMAT,
     }
-    digest = hashlib.sha256(json.dumps(identity, sort_keys=True).encode()).hexdigest()[:16]
-    return digest, identity
+    return identity_digest(identity), identity
 
 
 def _load_npy(path: Path, dtype, shape: tuple, what: str) -> np.ndarray:

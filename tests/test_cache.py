@@ -144,3 +144,76 @@ def test_model_from_cache_decodes_like_oracle(forward_golden, tmp_path):
         assert_bits_equal(to_host(logits), rs.logits, f"logits step {i}")
     st.check_status()
     torch.cuda.synchronize()
+
+
+# ---- a cache written by the reference's own converter -----------------------------
+# tests/golden/ref_cache/ was written by the reference's _convert_projection,
+# _convert_embedding, _cache_identity and _atomic_json (cpu_lightspark.py:149-243,
+# 574-610) on a 2-layer synthetic LATTICE model, and ref_cache_forward.npz holds the
+# reference's forward_token logits over it (tests/golden/make_cache_golden.py).
+from pathlib import Path  # noqa: E402
+
+REF_CACHE = Path(__file__).resolve().parent / "golden" / "ref_cache"
+
+
+@pytest.fixture(scope="module")
+def ref_cache_golden():
+    with np.load(REF_CACHE.parent / "ref_cache_forward.npz", allow_pickle=False) as f:
+        g = {k: f[k] for k in f.files}
+    g["config"] = json.loads(bytes(g["config_json"]).decode())
+    g["identity"] = json.loads(bytes(g["identity_json"]).decode())
+    g["norms"] = {str(name): g[f"norm_{i}"] for i, name in enumerate(g["norm_names"])}
+    return g
+
+
+def test_reference_written_cache_manifest_and_files(ref_cache_golden):
+    g = ref_cache_golden
+    manifest = cache.read_manifest(REF_CACHE)
+    assert manifest["identity"] == g["identity"]
+    # the reference's directory digest of that identity record
+    assert cache.identity_digest(g["identity"]) == bytes(g["digest"]).decode()
+    arrays = cache.read_cache(REF_CACHE, g["config"])
+    # fused q|k|v and gate|up rows, each part the file the reference wrote
+    q = np.load(REF_CACHE / "model_layers_1_self_attn_q_proj.int4.npy", allow_pickle=False)
+    v = np.load(REF_CACHE / "model_layers_1_self_attn_v_proj.int4.npy", allow_pickle=False)
+    np.testing.assert_array_equal(arrays["qkv"][1][:q.shape[0]], q)
+    np.testing.assert_array_equal(arrays["qkv"][1][-v.shape[0]:], v)
+    up = np.load(REF_CACHE / "model_layers_0_mlp_up_proj.scales.npy", allow_pickle=False)
+    np.testing.assert_array_equal(arrays["gate_up_scales"][0][-up.shape[0]:], up)
+    assert arrays["embedding"].shape == (512, 64) and arrays["embedding_scales"].dtype == np.float32
+
+
+def test_oracle_on_reference_written_cache_matches_reference_forward(ref_cache_golden):
+    import oracle
+    g = ref_cache_golden
+    arrays = {k: [np.ascontiguousarray(a) for a in v] if isinstance(v, list) else np.ascontiguousarray(v)
+              for k, v in cache.read_cache(REF_CACHE, g["config"]).items()}
+    arrays.update(cache.read_norms(g["norms"], g["config"]))
+    arrays["rope_cos"], arrays["rope_sin"] = g["rope_cos"], g["rope_sin"]
+    m = oracle.OracleModel(g["config"], arrays)
+    st = m.new_state(len(g["tokens"]), kv_f32=True)
+    for i, t in enumerate(g["tokens"]):
+        assert m.forward_token(int(t), st) == g["greedy"][i]
+        # only reduction order differs (qk-norm, softmax, exp): a few ulp
+        np.testing.assert_allclose(st.logits, g["logits"][i], rtol=0, atol=2e-6)
+
+
+@pytest.mark.gpu
+def test_gpu_decode_from_reference_written_cache(ref_cache_golden):
+    torch = pytest.importorskip("torch")
+    import oracle
+    from harsh4b_amd.synthetic import host_arrays
+    from tests.gpu_util import assert_bits_equal, to_host
+    g = ref_cache_golden
+    print("\n[gpu] reference-written cache -> device model", flush=True)
+    model = cache.load_litespark_cache(REF_CACHE, g["norms"], config=g["config"])
+    ref = oracle.OracleModel(g["config"], host_arrays(model))
+    n = len(g["tokens"])
+    st, rs = model.new_state(n), ref.new_state(n)
+    for i, t in enumerate(g["tokens"]):
+        logits = model.forward_token(int(t), st)
+        tok = model.greedy_token(st)
+        assert tok == ref.forward_token(int(t), rs) == int(g["greedy"][i])
+        assert_bits_equal(to_host(logits), rs.logits, f"logits step {i}")
+    st.check_status()
+    torch.cuda.synchronize()
