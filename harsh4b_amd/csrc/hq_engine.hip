@@ -704,10 +704,13 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         const bool more = l + 1 < p.L;
         const hq_layer& Ly = S.lay[l];
         const hq_layer& Ln = S.lay[more ? l + 1 : l];
-        // the first layer's first GQA item: its K/V copies land while the
-        // qkv GEMV and its hand-off run (later layers issue theirs at the end
-        // of the layer before)
-        if (l == 0 && is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<true>(p, l, pos);
+        // the first layer's first attention item (GQA or per head): its K/V
+        // copies land while the qkv GEMV and its hand-off run (later layers
+        // issue theirs at the end of the layer before)
+        if (l == 0 && is_copy_wave(opaque_tid() / kWave)) {
+            prefetch_first_item<true>(p, l, pos);
+            prefetch_first_item<false>(p, l, pos);
+        }
         // ---- P1: qkv
         wait_lds_geq(&S.xq_seq, kIWaves * (3 * l + 1), budget, p.status);
         if (ww == 0) TRACE(l, 16);
@@ -721,9 +724,6 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 17);
         if (ww == kWWaves - 1) TRACE(l, 47);
-        // this layer's first per-head attention item: its K/V copies land
-        // while the qkv rows are handed on
-        if (is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<false>(p, l, pos);
         // ---- P2: the block's attention items (all waves)
         attention_phase(p, Ly, l, pos, slot_of(p, set, l), base + 5u * uint32_t(l) + 2u, budget);
         if (att_blk) load_window(4 * l + 1, budget, p.status);
@@ -782,13 +782,20 @@ __device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int po
         }
         block_sync();   // results in S.res
         if (ww == 0) TRACE(l, 23);
-        // the next layer's first GQA item: its K/V copies (cached positions
-        // only; the current position's row comes from the qkv hand-off) are
-        // issued now, while the layer's own attention and its combine staging
-        // are done with S.kv.  The next wait that covers them (memory
-        // operations complete in issue order) is the next layer's qkv dot,
-        // a residual hand-off and an RMSNorm prologue later.
-        if (more && is_copy_wave(opaque_tid() / kWave)) prefetch_first_item<true>(p, l + 1, pos);
+        // the next layer's first attention item (GQA or per head): its K/V
+        // copies (cached positions only; the current position's row comes
+        // from the qkv hand-off) are issued now, while the layer's own
+        // attention and its combine staging are done with S.kv.  The next
+        // wait that covers them (memory operations complete in issue order)
+        // is the next layer's qkv dot, a residual hand-off and an RMSNorm
+        // prologue later.  (Per-head items' copies issued after the qkv dot
+        // instead held the item block's polls of the qkv rows behind them:
+        // 36 layers 711.5 -> 706.5 us per launch at context 70, 739.5 ->
+        // 721.7 at 136, 801.5 -> 742.2 at 256.)
+        if (more && is_copy_wave(opaque_tid() / kWave)) {
+            prefetch_first_item<true>(p, l + 1, pos);
+            prefetch_first_item<false>(p, l + 1, pos);
+        }
         if (more) load_window(4 * (l + 1), budget, p.status);
         load_rows<kOLPR, kOC, kPaceO>(wo, so, Ln.o, Ln.o_scales, R.h0, more ? R.h1 : R.h0 + 1, more ? qd : 32, ww);
     }
@@ -847,14 +854,11 @@ __device__ __forceinline__ void prefetch_group(const EngineParams& p, int l, int
 __device__ __forceinline__ int gqa_group(int nc, int kv_heads, int nb);
 __device__ __forceinline__ int item_slot(int b, int NB, int G);
 
-// The copies of this block's first attention item of layer l (copy waves):
-// GQA items (GQA true: more than kGroup chunks, up to three per item) at the
-// start of the layer, so they land while the qkv GEMV and its hand-off run;
-// per-head items (GQA false) after the qkv dot, so they land while its
-// hand-off runs (issued before it, an item block's weight waves took the
-// qkv input about 0.5 us later than the other blocks': 36 layers at context
-// 64, 719 -> 707 us per launch; GQA items issued late: 1143 -> 1167 us at
-// 4096).
+// The copies of this block's first attention item of layer l (copy waves),
+// GQA items (GQA true: more than kGroup chunks, up to three per item) and
+// per-head items (GQA false) alike: issued at the end of layer l - 1 (layer
+// 0: at its start), so they land while the qkv GEMV and its hand-off run
+// and none is still queued when the item polls for its qkv rows.
 // Items as in attention_phase.
 template <bool GQA>
 __device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l, int pos)
