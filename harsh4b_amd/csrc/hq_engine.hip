@@ -233,7 +233,7 @@ __device__ __forceinline__ void ibar(int& seq, unsigned& budget, int32_t* status
 #ifdef HQ_ENGINE_TRACE
 #define TRACE(l, point)                                                                          \
     do {                                                                                         \
-        if ((opaque_tid() & (kWave - 1)) == 0 && (l) >= kTraceL0 && (l) < kTraceL0 + 4)          \
+        if ((l) >= kTraceL0 && (l) < kTraceL0 + 4)                                               \
             S.trace[((l) - kTraceL0) * kTracePoints + (point)] = uint32_t(wall_clock64());       \
     } while (0)
 #else
@@ -669,8 +669,12 @@ __device__ __forceinline__ void prefetch_first_item(const EngineParams& p, int l
 
 __device__ __forceinline__ bool block_has_item(const EngineParams& p, int pos);
 
-__device__ void weight_role(const EngineParams& p, const Rows& R, int ww, int pos, uint32_t base, int set,
-                            unsigned& budget)
+// (Both roles are forced inline: compiled out of line, as the traced build's
+// larger code was, the role function took the kernel parameters through
+// scratch memory and spilled, and its timestamps no longer showed the
+// untraced kernel's timing.)
+__device__ __forceinline__ void weight_role(const EngineParams& p, const Rows& R, int ww, int pos, uint32_t base,
+                                            int set, unsigned& budget)
 {
     const int H = p.H, I = p.I;
     const int qd = p.heads * kD;
@@ -1583,8 +1587,8 @@ __device__ __forceinline__ void publish_rows(uint32_t* dst, int n)
     for (int i = t; i < n; i += kIThreads) hs_store(dst + i, S.res[i]);
 }
 
-__device__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32_t base, int set,
-                           unsigned& budget)
+__device__ __forceinline__ void input_role(const EngineParams& p, const Rows& R, int pos, uint32_t base, int set,
+                                           unsigned& budget)
 {
     const int t0 = threadIdx.x;
     const int H = p.H;

@@ -12,7 +12,9 @@ the categories are read from inside it.  The HQ_ENGINE_TRACE build
 timestamp at every phase boundary of layers 16-19 in every block.  A layer's
 critical path is a chain of these points, and each segment between two
 points goes to one category:
-  - body GEMV: the weight waves' dot products;
+  - GEMV dots (weights in registers): the weight waves' dot products over
+    weights already loaded (their streaming overlaps the other segments, so
+    this is not the reference's body-GEMV time, which includes the loads);
   - attention: an attention item, from its inputs to its output;
   - norm + quant: the RMSNorm and quantization prologues;
   - hand-off: the cross-block hand-offs (watching a vector's last entry,
@@ -50,27 +52,28 @@ TRACE_BLOCKS = 1024                                  # blocks the trace buffer h
 # A layer's critical path: (from point, to point, category, what).  Points
 # 25-29 are taken in the blocks that ran an attention item; "end" is the
 # next layer's point 0.
+DOTS = "GEMV dots (weights in registers)"
 SEGMENTS = [
     (0, 2, "hand-off", "x (layer input): watch + read"),
     (2, 3, "norm + quant", "RMSNorm + quant, qkv input"),
     (3, 16, "sync", "qkv input -> weight waves"),
-    (16, 4, "body GEMV", "qkv (dot, rows to the input waves)"),
+    (16, 4, DOTS, "qkv (dot, rows to the input waves)"),
     (4, 25, "hand-off", "qkv rows -> attention items"),
     (25, 29, "attention", "attention item (norms, RoPE, scores, softmax, V)"),
     (29, 6, "hand-off", "attention output: watch"),
     (6, 7, "hand-off", "attention output: read + quant"),
     (7, 18, "sync", "o input -> weight waves"),
-    (18, 8, "body GEMV", "o (dot, rows to the input waves)"),
+    (18, 8, DOTS, "o (dot, rows to the input waves)"),
     (8, 9, "hand-off", "x + o (residual): watch"),
     (9, 32, "hand-off", "x + o (residual): read"),
     (32, 10, "norm + quant", "RMSNorm + quant, gate_up input"),
     (10, 20, "sync", "gate_up input -> weight waves"),
-    (20, 11, "body GEMV", "gate_up + SwiGLU (dot, rows to the input waves)"),
+    (20, 11, DOTS, "gate_up + SwiGLU (dot, rows to the input waves)"),
     (11, 12, "hand-off", "SwiGLU output: watch"),
     (12, 42, "hand-off", "SwiGLU output: read + max"),
     (42, 44, "norm + quant", "quant, down input"),
     (44, 22, "sync", "down input -> weight waves"),
-    (22, 14, "body GEMV", "down (dot, rows to the input waves)"),
+    (22, 14, DOTS, "down (dot, rows to the input waves)"),
     (14, "end", "hand-off", "residual store -> next layer"),
 ]
 ATTENTION_POINTS = {25, 26, 27, 28, 29, 48, 49, 50, 51, 52, 53}
@@ -88,7 +91,7 @@ GQA_SEGMENTS[GQA_SEGMENTS.index((6, 7, "hand-off", "attention output: read + qua
     (55, 56, "attention", "combine (M, a_c, L/O chains)"),
     (56, 6, "hand-off", "attention output: watch"),
 ]
-CATEGORIES = ["body GEMV", "attention", "norm + quant", "hand-off", "sync"]
+CATEGORIES = [DOTS, "attention", "norm + quant", "hand-off", "sync"]
 
 
 def _model_and_state(ctx, seed, extra):
