@@ -101,7 +101,13 @@ struct EngineParams {
     int capacity;
     const int32_t* position;
     int32_t* status;
-    float* x;                 // residual stream: embedding in, final out
+    float* x;                 // residual stream: layer input in (unless token is set), final out
+    // nullable: layer 0's input is row *token of the int4 embedding (the
+    // step's embedding lookup, folded into the launch); x is then only written
+    const int32_t* token;
+    const uint8_t* emb;       // [vocab, H/2] packed int4
+    const float* emb_scales;  // [vocab]
+    int vocab;
     uint32_t* hs;             // hand-off words: 2 sets x L layers x hs_layer words
     int hs_layer;             // words per layer: x3 [H], x5 [H], qkv [qkv_rows], att [heads*D], act [I]
     uint32_t* epoch;
@@ -1595,7 +1601,25 @@ __device__ __forceinline__ void input_role(const EngineParams& p, const Rows& R,
     const int qd = p.heads * kD;
     const int nown = R.h1 - R.h0;
     int bseq = 0;   // input-barrier count
-    float xown = t0 < nown ? p.x[R.h0 + t0] : 0.0f;
+    // layer 0's input: x, or the embedding row of the current token
+    // (element i: nibble i of the row, low nibble first, times its scale,
+    // as the embedding kernel computes it; an out-of-range token flags the
+    // status and reads row 0)
+    int tok = 0;
+    if (p.token != nullptr) {
+        tok = *p.token;
+        if (tok < 0 || tok >= p.vocab) {
+            if (blockIdx.x == 0 && t0 == 0) atomicOr(p.status, HQ_STEP_BAD_TOKEN);
+            tok = 0;
+        }
+    }
+    auto layer_input = [&](int i) -> float {
+        if (p.token == nullptr) return p.x[i];
+        const uint8_t b = p.emb[size_t(tok) * size_t(H >> 1) + size_t(i >> 1)];
+        const int v = (i & 1) ? int(int8_t(b)) >> 4 : int(int8_t(uint8_t(b << 4))) >> 4;
+        return float(v) * p.emb_scales[tok];
+    };
+    float xown = t0 < nown ? layer_input(R.h0 + t0) : 0.0f;
 
 #pragma unroll 1
     for (int l = 0; l < p.L; ++l) {
@@ -1613,7 +1637,7 @@ __device__ __forceinline__ void input_role(const EngineParams& p, const Rows& R,
             float xin[kHidNPT];
             if (l == 0) {
 #pragma unroll
-                for (int j = 0; j < kHidNPT; ++j) xin[j] = t + kIThreads * j < H ? p.x[t + kIThreads * j] : 0.0f;
+                for (int j = 0; j < kHidNPT; ++j) xin[j] = t + kIThreads * j < H ? layer_input(t + kIThreads * j) : 0.0f;
             } else {
                 watch_last(x5_prev, H, budget, p.status);
                 TRACE(l, 1);
@@ -1853,9 +1877,15 @@ size_t engine_handoff_bytes(const hq_model* m)
 }
 
 hipError_t launch_engine(const hq_model* m, const hq_state* st, uint32_t* hs, uint32_t* epoch,
-                         uint64_t* part, int max_chunks, int nb, uint32_t* trace, hipStream_t s)
+                         uint64_t* part, int max_chunks, int nb, uint32_t* trace, bool embed, hipStream_t s)
 {
     EngineParams p{};
+    if (embed) {
+        p.token = st->token;
+        p.emb = m->embedding;
+        p.emb_scales = m->embedding_scales;
+        p.vocab = m->vocab;
+    }
     p.layers = m->device_layer;
     p.L = m->layers;
     p.H = m->hidden;

@@ -174,8 +174,10 @@ int engine_blocks(const hq_model* m);
 // Bytes of hand-off words the kernel needs in the workspace (zero-filled
 // before the first launch): two sets of one slot per layer.
 size_t engine_handoff_bytes(const hq_model* m);
+// embed: layer 0's input is the embedding row of *st->token (the step's
+// lookup folded into the launch) instead of st->x.
 hipError_t launch_engine(const hq_model* m, const hq_state* st, uint32_t* hs, uint32_t* epoch,
-                         uint64_t* part, int max_chunks, int nb, uint32_t* trace, hipStream_t s);
+                         uint64_t* part, int max_chunks, int nb, uint32_t* trace, bool embed, hipStream_t s);
 // HQ_ENGINE_TRACE builds: bytes of phase timestamps kept after the step
 // workspace proper (0 otherwise).
 size_t engine_trace_bytes(const hq_model* m);

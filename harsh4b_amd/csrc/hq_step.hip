@@ -10,7 +10,9 @@
 //   3. int8 quant -> o GEMV -> residual add                  (:442-445)
 //   4. RMSNorm(post) -> quant -> gate_up GEMV -> SwiGLU      (:447-455)
 //   5. int8 quant -> down GEMV -> residual add               (:456-459)
-// preceded by the embedding row decode (:429) and followed by the final
+// preceded by the embedding row decode (:429; inside the persistent
+// kernel's first layer when that runs, else its own kernel) and followed by
+// the final
 // RMSNorm -> quant -> tied LM head GEMV -> argmax (:461-466, :704-705),
 // whose last block also writes the greedy token and advances the position.
 // Token and position live in device memory, so a captured graph of this
@@ -133,19 +135,26 @@ static hipError_t layer_gemv(const hq_model* m, const hq_state* st, int l, StepG
 // The decoder layers of a step: the persistent layer kernel when the model
 // carries a device layer table and fits its limits, else five kernels per
 // layer.
-static hipError_t enqueue_layers(const hq_model* m, const hq_state* st, hipStream_t s)
+static bool engine_runs(const hq_model* m)
+{
+    return m->device_layer && !(m->flags & HQ_MODEL_PER_LAYER_KERNELS) && engine_fits(m) && engine_blocks(m) > 0;
+}
+
+// embed: the layer kernel takes layer 0's input from the embedding row of
+// the state's token (only when it runs; the per-layer kernels read st->x).
+static hipError_t enqueue_layers(const hq_model* m, const hq_state* st, bool embed, hipStream_t s)
 {
     const StepLayout Ly = step_layout(m, st->capacity);
     char* ws = static_cast<char*>(st->workspace);
     const size_t kv_layer = size_t(st->capacity) * size_t(Ly.kv_size);
     hipError_t e = hipSuccess;
-    const int nb = (m->device_layer && !(m->flags & HQ_MODEL_PER_LAYER_KERNELS) && engine_fits(m))
-                       ? engine_blocks(m) : 0;
+    const int nb = engine_runs(m) ? engine_blocks(m) : 0;
     if (nb > 0) {
         e = launch_engine(m, st, reinterpret_cast<uint32_t*>(ws + Ly.ll_off),
                           reinterpret_cast<uint32_t*>(ws + Ly.epoch_off),
                           reinterpret_cast<uint64_t*>(ws + Ly.eng_part_off), Ly.max_chunks, nb,
-                          engine_trace_bytes(m) ? reinterpret_cast<uint32_t*>(ws + Ly.trace_off) : nullptr, s);
+                          engine_trace_bytes(m) ? reinterpret_cast<uint32_t*>(ws + Ly.trace_off) : nullptr, embed,
+                          s);
         if (e != hipSuccess) return e;
     }
     for (int l = 0; nb == 0 && l < m->layers; ++l) {
@@ -178,11 +187,15 @@ static hipError_t enqueue_step(const hq_model* m, const hq_state* st, hipStream_
     char* ws = static_cast<char*>(st->workspace);
     const int H = m->hidden;
 
-    hipLaunchKernelGGL(embedding_kernel, dim3(1), dim3(kBlock), 0, s, m->embedding,
-                       m->embedding_scales, m->vocab, H, st->token, st->status, st->x);
+    // the embedding lookup: folded into the layer kernel when that runs
+    // (one launch and its gap fewer per token: 1244 -> 1252 tok/s at
+    // context 64), else its own kernel
+    const bool fold = engine_runs(m);
+    if (!fold) hipLaunchKernelGGL(embedding_kernel, dim3(1), dim3(kBlock), 0, s, m->embedding,
+                                  m->embedding_scales, m->vocab, H, st->token, st->status, st->x);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if ((e = enqueue_layers(m, st, s)) != hipSuccess) return e;
+    if ((e = enqueue_layers(m, st, fold, s)) != hipSuccess) return e;
 
     GemvParams p{};
     p.w = m->embedding; p.ws = m->embedding_scales; p.rows = m->vocab; p.width = H;
@@ -250,7 +263,7 @@ extern "C" int hq_step_layers(const hq_model* model, const hq_state* state, void
 {
     const int rc = validate(model, state);
     if (rc != HQ_OK) return rc;
-    return enqueue_layers(model, state, static_cast<hipStream_t>(stream)) == hipSuccess
+    return enqueue_layers(model, state, false, static_cast<hipStream_t>(stream)) == hipSuccess
                ? HQ_OK : HQ_ERR_LAUNCH;
 }
 
