@@ -450,7 +450,7 @@ def batched_step_bytes(config, m, context):
     return weights + lm_head + m * per_seq
 
 
-def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None, fill=False):
+def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None, fill=False, large_capacity=False):
     """batched greedy decode of M independent sequences (M in
     `sizes`) at context `ctx` (each prefilled with its own random ctx-token
     prompt, or with `fill` given N(0,1) K/V in its cache), one hq_decode_batch
@@ -458,7 +458,8 @@ def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None, fill=F
     step time, sequence-tokens/s, the step's HBM bytes over its time (weights
     once per step + M K/V caches), and the ratio to M batch-1 decode steps of
     the same model at the same context.  The largest M gives the case's value
-    and roofline."""
+    and roofline.  With `large_capacity`, the smallest M is timed again with
+    every state's capacity at 4096 positions."""
     import numpy as np
     import torch
     cfg = model.config
@@ -516,6 +517,30 @@ def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None, fill=F
               f"({ms / (1e3 / tok1):.2f}x the batch-1 step)", file=sys.stderr, flush=True)
         model._batch_graph = None
         del states
+    # the same M = sizes[0] with every state's capacity at 4096 positions:
+    # the step's attention tails and merged qkv + attention launch cover
+    # capacities of up to 512 positions (eight 64-position chunks, fixed when
+    # the step's graph is captured), so a larger capacity takes the separate
+    # combine, quantization and qkv kernels at any context
+    big = {}
+    if large_capacity:
+        m = sizes[0]
+        states = []
+        for i in range(m):
+            st = model.new_state(4096)
+            start(st, i)
+            states.append(st)
+        model.decode_greedy_batch(states, warmup)
+        t = timed(lambda: model.decode_greedy_batch(states, steps, check_status=False))
+        for st in states:
+            st.check_status()
+        ms = t * 1e3 / steps
+        big[m] = {"capacity": 4096, "ms_per_step": round(ms, 3), "tok_s": round(m * steps / t, 1),
+                  "step_vs_batch1_step": round(ms / (1e3 / tok1), 2)}
+        print(f"# M={m} at capacity 4096: {ms:.3f} ms/step, {m * steps / t:.1f} tok/s", file=sys.stderr,
+              flush=True)
+        model._batch_graph = None
+        del states
     top_m = sizes[-1]
     top = per_m[top_m]
     res = {"workload": f"configs[3]: batched decode of M = {'/'.join(map(str, sizes))} sequences at context "
@@ -527,6 +552,8 @@ def batched_case(model, ctx, sizes, steps, warmup, cpu_seconds, ref=None, fill=F
                         "achieved": top["achieved_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": top["hbm_frac"], "traffic": None, "algorithmic_bytes": top["bytes_per_step"]},
            "batch1_tok_s": round(tok1, 1), "per_m": per_m}
+    if big:
+        res["per_m_capacity_4096"] = big
     if cpu_seconds > 0:
         res["cpu_baseline"] = cpu_baseline_batched(model, ctx, cpu_seconds, ref)
     return res
@@ -1169,7 +1196,7 @@ def main():
                    "configs[1]": layer_case(cfg, per_kind_ms, layers_ms, arrays, cpu_s / 4),
                    "configs[4]": long_case(args, model, lib, cfg, ref, cpu_s, (context, layers_ms))}
         print("# configs[3]", file=sys.stderr, flush=True)
-        configs["configs[3]"] = batched_case(model, 256, [8, 16, 32], 16, 2, cpu_s / 4, ref)
+        configs["configs[3]"] = batched_case(model, 256, [8, 16, 32], 16, 2, cpu_s / 4, ref, large_capacity=True)
         result["configs"] = configs
         att = attention_case(args, torch)
         print(f"# hq_gqa_decode at context 4096: {att['us_per_call']:.2f} us, {att['achieved']:.0f} GB/s",

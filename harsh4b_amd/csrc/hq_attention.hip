@@ -439,7 +439,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
 // blocks wait for nobody, so they finish and the at most 8 * 32 tail blocks
 // all get a place on the chip); then the same quantization (amax floored at 1e-5,
 // quant_i8 with 127 / amax, de-interleaved, act = amax / 127).
-constexpr int kAttnTailChunks = 8;   // contexts of up to 8 chunks (max_chunks <= 8)
+constexpr int kAttnTailChunks = 8;   // chunks per combine batch (more take several batches)
 constexpr int kAttnTailParts = 8;    // tail blocks per sequence
 constexpr int kAttnTailNO = 2;       // outputs per thread: up to 2 * 2 * 8 = 32 query heads
 template <int D>
@@ -489,45 +489,70 @@ __device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
         unrolled<NO>([&](auto i) { val[i] = h0 + 2 * i < HQ ? bits_f32(uint32_t(e[i])) : 0.0f; });
     } else {
         const uint64_t* base = a.ll_part + size_t(s) * size_t(H) * a.max_chunks * pstride;
-        // m_c and l_c of the part's heads: entry tid = (head, chunk, m|l)
-        {
+        // m_c (and l_c) of the part's heads for chunks [cb, cb + NC):
+        // entry tid = (head, chunk, m|l), into ml_s
+        auto load_ml = [&](int cb, bool with_l) {
             uint64_t e[1];
-            const int hq = tid / (2 * NC), c = (tid / 2) % NC, kind = tid & 1;
-            const bool mine = hq < HQ && c < nc;
+            const int hq = tid / (2 * NC), c = cb + (tid / 2) % NC, kind = tid & 1;
+            const bool mine = hq < HQ && c < nc && (with_l || kind == 0);
             auto src = [&](auto) { return base + (size_t(hb + hq) * a.max_chunks + c) * pstride + kind; };
             e[0] = mine ? tail_load(src(0)) : ready;
             wait(e, [&](auto j) { return tail_load(src(j)); });
-            if (mine) ml_s[hq][c][kind] = bits_f32(uint32_t(e[0]));
-        }
-        // o_c[d] of this thread's heads
-        uint64_t o[NO * NC];
-        auto osrc = [&](auto j) {
-            const int i = int(j) / NC, c = int(j) % NC;
-            return base + (size_t(hb + h0 + 2 * i) * a.max_chunks + c) * pstride + 2 + d;
+            if (mine) ml_s[hq][c - cb][kind] = bits_f32(uint32_t(e[0]));
         };
-        unrolled<NO * NC>([&](auto j) {
-            o[j] = (h0 + 2 * (int(j) / NC) < HQ && int(j) % NC < nc) ? tail_load(osrc(j)) : ready;
-        });
-        wait(o, [&](auto j) { return tail_load(osrc(j)); });
-        __syncthreads();   // ml_s
-        unrolled<NO>([&](auto i) {
-            const int hq = h0 + 2 * i;
-            if (hq < HQ) {
-                float M = ml_s[hq][0][0];
-                for (int c = 1; c < nc; ++c) M = fmaxf(M, ml_s[hq][c][0]);
-                float L = 0.0f, O = 0.0f;
-                unrolled<NC>([&](auto c) {
-                    if (c < nc) {
-                        const float al = spec_expf(ml_s[hq][c][0] - M);
-                        L = __builtin_fmaf(al, ml_s[hq][c][1], L);
-                        O = __builtin_fmaf(al, bits_f32(uint32_t(o[i * NC + c])), O);
-                    }
+        // o_c[d] of this thread's heads for chunks [cb, cb + NC)
+        uint64_t o[NO * NC];
+        auto load_o = [&](int cb) {
+            auto osrc = [&](auto j) {
+                const int i = int(j) / NC, c = cb + int(j) % NC;
+                return base + (size_t(hb + h0 + 2 * i) * a.max_chunks + c) * pstride + 2 + d;
+            };
+            unrolled<NO * NC>([&](auto j) {
+                o[j] = (h0 + 2 * (int(j) / NC) < HQ && cb + int(j) % NC < nc) ? tail_load(osrc(j)) : ready;
+            });
+            wait(o, [&](auto j) { return tail_load(osrc(j)); });
+        };
+        // M = m_0, then fmaxf with m_1, m_2, ... (a first pass over every
+        // batch of NC chunks when there are more); then the L and O chains
+        // over ascending chunks, batch by batch
+        float M[NO], L[NO], O[NO];
+        unrolled<NO>([&](auto i) { L[i] = 0.0f; O[i] = 0.0f; });
+        if (nc > NC) {
+            for (int cb = 0; cb < nc; cb += NC) {
+                load_ml(cb, false);
+                __syncthreads();   // ml_s
+                unrolled<NO>([&](auto i) {
+                    const int hq = h0 + 2 * i;
+                    if (hq < HQ)
+                        for (int c = 0; c < min(NC, nc - cb); ++c)
+                            M[i] = cb + c == 0 ? ml_s[hq][0][0] : fmaxf(M[i], ml_s[hq][c][0]);
                 });
-                val[i] = O * (1.0f / L);
-            } else {
-                val[i] = 0.0f;
+                __syncthreads();   // ml_s is written again
             }
-        });
+        }
+        for (int cb = 0; cb < nc; cb += NC) {
+            load_ml(cb, true);
+            load_o(cb);
+            __syncthreads();   // ml_s
+            unrolled<NO>([&](auto i) {
+                const int hq = h0 + 2 * i;
+                if (hq < HQ) {
+                    if (nc <= NC) {
+                        M[i] = ml_s[hq][0][0];
+                        for (int c = 1; c < nc; ++c) M[i] = fmaxf(M[i], ml_s[hq][c][0]);
+                    }
+                    unrolled<NC>([&](auto c) {
+                        if (cb + c < nc) {
+                            const float al = spec_expf(ml_s[hq][c][0] - M[i]);
+                            L[i] = __builtin_fmaf(al, ml_s[hq][c][1], L[i]);
+                            O[i] = __builtin_fmaf(al, bits_f32(uint32_t(o[i * NC + c])), O[i]);
+                        }
+                    });
+                }
+            });
+            __syncthreads();   // ml_s is written again
+        }
+        unrolled<NO>([&](auto i) { val[i] = h0 + 2 * i < HQ ? O[i] * (1.0f / L[i]) : 0.0f; });
     }
     // the row's maximum: this part's, then the eight parts'
     float mx = 0.0f;
@@ -887,7 +912,7 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
     const dim3 grid(a.kv_heads, (a.max_chunks + b.cpb - 1) / b.cpb, a.batch);
     const int H = a.kv_heads * a.groups;
     if (a.ll_part && a.ll_out && a.ll_max && a.epoch_ctr && a.epoch_id >= 0 && a.epoch_id < 256 &&
-        a.max_chunks <= kAttnTailChunks && a.groups <= 4 && H % (2 * kAttnTailParts) == 0 &&
+        a.groups <= 4 && H % (2 * kAttnTailParts) == 0 &&
         H <= 2 * kAttnTailNO * kAttnTailParts && int(grid.x * grid.y * grid.z) >= kAttnTailParts * a.batch) {
         // the combine and quantization in the launch's last blocks
         if (b.cpb == 1) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1, true>), grid, dim3(kBlock), 0, s, b);
@@ -912,7 +937,7 @@ hipError_t launch_batch_qkv_attention(const int8_t* x, const float* act, const u
     const int rows = (H + 2 * a.kv_heads) * a.head_dim;
     if (!a.qkv_ll || !a.ll_part || !a.ll_out || !a.ll_max || !a.epoch_ctr || a.epoch_id < 0 || a.epoch_id >= 256 ||
         a.head_dim != 128 || !a.table || !a.qkv || !a.q8 || !a.act || a.batch < 1 || a.batch > 16 ||
-        a.max_chunks > kAttnTailChunks || a.groups > 4 || H % (2 * kAttnTailParts) != 0 ||
+        a.groups > 4 || H % (2 * kAttnTailParts) != 0 ||
         H > 2 * kAttnTailNO * kAttnTailParts || (k >> 1) > 1280 || (k & 31))
         return hipErrorNotSupported;
     AttnParams b = a;
