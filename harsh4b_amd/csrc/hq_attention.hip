@@ -100,8 +100,8 @@ __device__ __forceinline__ void poll_pair(const uint64_t* p, uint32_t ep, int32_
 // QLL: the raw projection comes as {value, epoch} entries from the qkv GEMM
 // blocks of the same launch (a.qkv_ll) instead of the qkv buffer.
 template <int D, int GMAX, bool STEP, int CPB, bool TAILS, bool QLL = false>
-__device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep, AttnLds<D, GMAX, CPB>& lds,
-                                                int bx, int by, int bz)
+__device__ __forceinline__ int attention_block(const AttnParams& a, uint32_t ep, AttnLds<D, GMAX, CPB>& lds,
+                                               int bx, int by, int bz)
 {
     constexpr int C = kAttnChunk;
     constexpr int DPL = D / 16;
@@ -130,7 +130,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
         pos = *a.position;
         if (pos < 0 || pos >= a.capacity) {
             if (g == 0 && split == 0 && tid == 0) atomicOr(a.status, HQ_STEP_FULL);
-            return;
+            return 0;
         }
         n = pos + 1;
     } else {
@@ -182,7 +182,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
     float* const out = a.out + zq;
     const int nc = (n + C - 1) / C;
     const int nsplit = (nc + CPB - 1) / CPB;
-    if (split >= nsplit) return;
+    if (split >= nsplit) return nsplit;
     const int c_begin = split * CPB;
     const int c_end = min(nc, c_begin + CPB);
     const size_t kv_off = size_t(g) * D;
@@ -401,7 +401,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
             if constexpr (TAILS) tail_store(a.ll_out + zq + size_t(g * G + h) * D + d, O * (1.0f / L), ep);
             else out[size_t(g * G + h) * D + d] = O * (1.0f / L);
         }
-        return;
+        return nsplit;
     }
 
     // several splits: publish this block's chunk partials
@@ -426,6 +426,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
     }
     // (attention_combine_kernel or batch_combine_quant_kernel, launched next
     // on the stream, or this launch's tail combines them)
+    return nsplit;
 }
 
 // Tail of a batched-step attention launch (TAILS): block (sequence s, part
@@ -440,6 +441,7 @@ __device__ __forceinline__ void attention_block(const AttnParams& a, uint32_t ep
 // all get a place on the chip); then the same quantization (amax floored at 1e-5,
 // quant_i8 with 127 / amax, de-interleaved, act = amax / 127).
 constexpr int kAttnTailChunks = 8;   // chunks per combine batch (more take several batches)
+constexpr int kAttnMaxSplits = 8;    // splits (blockIdx.y) in a batched step's attention grid
 constexpr int kAttnTailParts = 8;    // tail blocks per sequence
 constexpr int kAttnTailNO = 2;       // outputs per thread: up to 2 * 2 * 8 = 32 query heads
 template <int D>
@@ -584,7 +586,15 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
 {
     __shared__ AttnLds<D, GMAX, CPB> lds;
     const uint32_t ep = TAILS ? (*a.epoch_ctr << 8) | uint32_t(a.epoch_id) : 0u;
-    attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep, lds, int(blockIdx.x), int(blockIdx.y), int(blockIdx.z));
+    // splits y, y + gridDim.y, ... of the query (a batched step's grid
+    // holds fewer splits than its largest capacity allows: blocks walk the
+    // rest, and splits past a context exit at once)
+    for (int y = int(blockIdx.y);;) {
+        const int nsplit = attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep, lds, int(blockIdx.x), y, int(blockIdx.z));
+        y += int(gridDim.y);
+        if (y >= nsplit) break;   // (block-uniform)
+        __syncthreads();          // the block's LDS is filled again
+    }
     if constexpr (TAILS) {
         const int lin = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
         const int u = lin - int(gridDim.x * gridDim.y * gridDim.z) + kAttnTailParts * a.batch;
@@ -617,7 +627,12 @@ __global__ __launch_bounds__(kBlock) void qkv_attention_kernel(GemmParams gp, At
     const uint32_t ep = (*a.epoch_ctr << 8) | uint32_t(a.epoch_id);
     const int k = int(blockIdx.x) - tiles;
     const int gx = a.kv_heads;
-    attention_block<128, 4, false, CPB, true, true>(a, ep, lds.at, k % gx, (k / gx) % gy, k / (gx * gy));
+    for (int y = (k / gx) % gy;;) {
+        const int nsplit = attention_block<128, 4, false, CPB, true, true>(a, ep, lds.at, k % gx, y, k / (gx * gy));
+        y += gy;
+        if (y >= nsplit) break;   // (block-uniform)
+        __syncthreads();          // the block's LDS is filled again
+    }
     const int u = k - gx * gy * a.batch + kAttnTailParts * a.batch;
     if (u >= 0) attention_tail<128>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
 }
@@ -906,10 +921,11 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
         a.kv_heads * a.groups > kCombineMaxHeads || a.batch < 1)
         return hipErrorInvalidValue;
     // one chunk per block while the grid fits about one round of the chip
-    // (four 256-thread blocks per CU), else two
+    // (four 256-thread blocks per CU), else two; at most kAttnMaxSplits
+    // splits in the grid (blocks walk the further ones)
     AttnParams b = a;
-    b.cpb = a.kv_heads * a.max_chunks * a.batch <= 1024 ? 1 : 2;
-    const dim3 grid(a.kv_heads, (a.max_chunks + b.cpb - 1) / b.cpb, a.batch);
+    b.cpb = a.kv_heads * min(a.max_chunks, kAttnMaxSplits) * a.batch <= 1024 ? 1 : 2;
+    const dim3 grid(a.kv_heads, min((a.max_chunks + b.cpb - 1) / b.cpb, kAttnMaxSplits), a.batch);
     const int H = a.kv_heads * a.groups;
     if (a.ll_part && a.ll_out && a.ll_max && a.epoch_ctr && a.epoch_id >= 0 && a.epoch_id < 256 &&
         a.groups <= 4 && H % (2 * kAttnTailParts) == 0 &&
@@ -941,8 +957,8 @@ hipError_t launch_batch_qkv_attention(const int8_t* x, const float* act, const u
         H > 2 * kAttnTailNO * kAttnTailParts || (k >> 1) > 1280 || (k & 31))
         return hipErrorNotSupported;
     AttnParams b = a;
-    b.cpb = a.kv_heads * a.max_chunks * a.batch <= 1024 ? 1 : 2;
-    const int gy = (a.max_chunks + b.cpb - 1) / b.cpb;
+    b.cpb = a.kv_heads * min(a.max_chunks, kAttnMaxSplits) * a.batch <= 1024 ? 1 : 2;
+    const int gy = min((a.max_chunks + b.cpb - 1) / b.cpb, kAttnMaxSplits);
     if (a.kv_heads * gy * a.batch < kAttnTailParts * a.batch) return hipErrorNotSupported;
     GemmParams p{};
     p.m = a.batch;
