@@ -444,7 +444,7 @@ constexpr int kAttnTailChunks = 8;   // chunks per combine batch (more take seve
 constexpr int kAttnMaxSplits = 8;    // splits (blockIdx.y) in a batched step's attention grid
 constexpr int kAttnTailParts = 8;    // tail blocks per sequence
 constexpr int kAttnTailNO = 2;       // outputs per thread: up to 2 * 2 * 8 = 32 query heads
-template <int D>
+template <int D, bool BIG>
 __device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
 {
     static_assert(D == kBlock / 2, "two heads per pass of the block");
@@ -489,6 +489,49 @@ __device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
         unrolled<NO>([&](auto i) { e[i] = h0 + 2 * i < HQ ? tail_load(src(i)) : ready; });
         wait(e, [&](auto i) { return tail_load(src(i)); });
         unrolled<NO>([&](auto i) { val[i] = h0 + 2 * i < HQ ? bits_f32(uint32_t(e[i])) : 0.0f; });
+    } else if constexpr (!BIG) {
+        // every context within NC chunks (the launch checked max_chunks):
+        // one batch, straight-line code
+        const uint64_t* base = a.ll_part + size_t(s) * size_t(H) * a.max_chunks * pstride;
+        // m_c and l_c of the part's heads: entry tid = (head, chunk, m|l)
+        {
+            uint64_t e[1];
+            const int hq = tid / (2 * NC), c = (tid / 2) % NC, kind = tid & 1;
+            const bool mine = hq < HQ && c < nc;
+            auto src = [&](auto) { return base + (size_t(hb + hq) * a.max_chunks + c) * pstride + kind; };
+            e[0] = mine ? tail_load(src(0)) : ready;
+            wait(e, [&](auto j) { return tail_load(src(j)); });
+            if (mine) ml_s[hq][c][kind] = bits_f32(uint32_t(e[0]));
+        }
+        // o_c[d] of this thread's heads
+        uint64_t o[NO * NC];
+        auto osrc = [&](auto j) {
+            const int i = int(j) / NC, c = int(j) % NC;
+            return base + (size_t(hb + h0 + 2 * i) * a.max_chunks + c) * pstride + 2 + d;
+        };
+        unrolled<NO * NC>([&](auto j) {
+            o[j] = (h0 + 2 * (int(j) / NC) < HQ && int(j) % NC < nc) ? tail_load(osrc(j)) : ready;
+        });
+        wait(o, [&](auto j) { return tail_load(osrc(j)); });
+        __syncthreads();   // ml_s
+        unrolled<NO>([&](auto i) {
+            const int hq = h0 + 2 * i;
+            if (hq < HQ) {
+                float M = ml_s[hq][0][0];
+                for (int c = 1; c < nc; ++c) M = fmaxf(M, ml_s[hq][c][0]);
+                float L = 0.0f, O = 0.0f;
+                unrolled<NC>([&](auto c) {
+                    if (c < nc) {
+                        const float al = spec_expf(ml_s[hq][c][0] - M);
+                        L = __builtin_fmaf(al, ml_s[hq][c][1], L);
+                        O = __builtin_fmaf(al, bits_f32(uint32_t(o[i * NC + c])), O);
+                    }
+                });
+                val[i] = O * (1.0f / L);
+            } else {
+                val[i] = 0.0f;
+            }
+        });
     } else {
         const uint64_t* base = a.ll_part + size_t(s) * size_t(H) * a.max_chunks * pstride;
         // m_c (and l_c) of the part's heads for chunks [cb, cb + NC):
@@ -581,24 +624,32 @@ __device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
     if (qt == 0 && tid == 0) a.act[s] = amax / 127.0f;
 }
 
-template <int D, int GMAX, bool STEP, int CPB, bool TAILS = false>
+// BIG: the batched step's launch for states of more than kAttnTailChunks
+// chunks (a separate instantiation: the split walk and the batched tail
+// combine take registers that the common case would pay for in occupancy).
+template <int D, int GMAX, bool STEP, int CPB, bool TAILS = false, bool BIG = false>
 __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
 {
     __shared__ AttnLds<D, GMAX, CPB> lds;
     const uint32_t ep = TAILS ? (*a.epoch_ctr << 8) | uint32_t(a.epoch_id) : 0u;
-    // splits y, y + gridDim.y, ... of the query (a batched step's grid
-    // holds fewer splits than its largest capacity allows: blocks walk the
-    // rest, and splits past a context exit at once)
-    for (int y = int(blockIdx.y);;) {
-        const int nsplit = attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep, lds, int(blockIdx.x), y, int(blockIdx.z));
-        y += int(gridDim.y);
-        if (y >= nsplit) break;   // (block-uniform)
-        __syncthreads();          // the block's LDS is filled again
+    if constexpr (BIG) {
+        // splits y, y + gridDim.y, ... of the query (the grid holds fewer
+        // splits than the largest capacity allows: blocks walk the rest,
+        // and splits past a context exit at once)
+        for (int y = int(blockIdx.y);;) {
+            const int nsplit =
+                attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep, lds, int(blockIdx.x), y, int(blockIdx.z));
+            y += int(gridDim.y);
+            if (y >= nsplit) break;   // (block-uniform)
+            __syncthreads();          // the block's LDS is filled again
+        }
+    } else {
+        attention_block<D, GMAX, STEP, CPB, TAILS>(a, ep, lds, int(blockIdx.x), int(blockIdx.y), int(blockIdx.z));
     }
     if constexpr (TAILS) {
         const int lin = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
         const int u = lin - int(gridDim.x * gridDim.y * gridDim.z) + kAttnTailParts * a.batch;
-        if (u >= 0) attention_tail<D>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
+        if (u >= 0) attention_tail<D, BIG>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
     }
 }
 
@@ -608,7 +659,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnParams a)
 // split, sequence; gy splits) with their tails, and take the raw projection
 // from those entries.  Every block an attention block waits for has started
 // before it (blocks start in index order).  One LDS buffer serves either role.
-template <int RG, int BT, int CPB>
+template <int RG, int BT, int CPB, bool BIG>
 __global__ __launch_bounds__(kBlock) void qkv_attention_kernel(GemmParams gp, AttnParams a, int tiles, int gy)
 {
     constexpr int HMAX = 1280;
@@ -627,14 +678,19 @@ __global__ __launch_bounds__(kBlock) void qkv_attention_kernel(GemmParams gp, At
     const uint32_t ep = (*a.epoch_ctr << 8) | uint32_t(a.epoch_id);
     const int k = int(blockIdx.x) - tiles;
     const int gx = a.kv_heads;
-    for (int y = (k / gx) % gy;;) {
-        const int nsplit = attention_block<128, 4, false, CPB, true, true>(a, ep, lds.at, k % gx, y, k / (gx * gy));
-        y += gy;
-        if (y >= nsplit) break;   // (block-uniform)
-        __syncthreads();          // the block's LDS is filled again
+    if constexpr (BIG) {
+        for (int y = (k / gx) % gy;;) {
+            const int nsplit =
+                attention_block<128, 4, false, CPB, true, true>(a, ep, lds.at, k % gx, y, k / (gx * gy));
+            y += gy;
+            if (y >= nsplit) break;   // (block-uniform)
+            __syncthreads();          // the block's LDS is filled again
+        }
+    } else {
+        attention_block<128, 4, false, CPB, true, true>(a, ep, lds.at, k % gx, (k / gx) % gy, k / (gx * gy));
     }
     const int u = k - gx * gy * a.batch + kAttnTailParts * a.batch;
-    if (u >= 0) attention_tail<128>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
+    if (u >= 0) attention_tail<128, BIG>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
 }
 
 // Combine of the chunk partials when a context spans several chunks: thread
@@ -930,12 +986,26 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
     if (a.ll_part && a.ll_out && a.ll_max && a.epoch_ctr && a.epoch_id >= 0 && a.epoch_id < 256 &&
         a.groups <= 4 && H % (2 * kAttnTailParts) == 0 &&
         H <= 2 * kAttnTailNO * kAttnTailParts && int(grid.x * grid.y * grid.z) >= kAttnTailParts * a.batch) {
-        // the combine and quantization in the launch's last blocks
-        if (b.cpb == 1) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1, true>), grid, dim3(kBlock), 0, s, b);
-        else hipLaunchKernelGGL((attention_kernel<128, 4, false, 2, true>), grid, dim3(kBlock), 0, s, b);
+        // the combine and quantization in the launch's last blocks (BIG:
+        // contexts of more than kAttnTailChunks chunks, split walk)
+        if (a.max_chunks > kAttnTailChunks) {
+            if (b.cpb == 1) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1, true, true>), grid, dim3(kBlock), 0, s, b);
+            else hipLaunchKernelGGL((attention_kernel<128, 4, false, 2, true, true>), grid, dim3(kBlock), 0, s, b);
+        } else {
+            if (b.cpb == 1) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1, true>), grid, dim3(kBlock), 0, s, b);
+            else hipLaunchKernelGGL((attention_kernel<128, 4, false, 2, true>), grid, dim3(kBlock), 0, s, b);
+        }
         return hipGetLastError();
     }
-    if (b.cpb == 1) {
+    if ((a.max_chunks + b.cpb - 1) / b.cpb > kAttnMaxSplits) {   // the split walk
+        if (b.cpb == 1) {
+            if (a.groups <= 4) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1, false, true>), grid, dim3(kBlock), 0, s, b);
+            else hipLaunchKernelGGL((attention_kernel<128, 8, false, 1, false, true>), grid, dim3(kBlock), 0, s, b);
+        } else {
+            if (a.groups <= 4) hipLaunchKernelGGL((attention_kernel<128, 4, false, 2, false, true>), grid, dim3(kBlock), 0, s, b);
+            else hipLaunchKernelGGL((attention_kernel<128, 8, false, 2, false, true>), grid, dim3(kBlock), 0, s, b);
+        }
+    } else if (b.cpb == 1) {
         if (a.groups <= 4) hipLaunchKernelGGL((attention_kernel<128, 4, false, 1>), grid, dim3(kBlock), 0, s, b);
         else hipLaunchKernelGGL((attention_kernel<128, 8, false, 1>), grid, dim3(kBlock), 0, s, b);
     } else {
@@ -974,8 +1044,13 @@ hipError_t launch_batch_qkv_attention(const int8_t* x, const float* act, const u
     // step, where M = 8 gained 2.04 -> 1.93 ms)
     const int tiles = (rows + 15) / 16;
     const dim3 grid(tiles + a.kv_heads * gy * a.batch);
-    if (b.cpb == 1) hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 1>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
-    else hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 2>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
+    if (a.max_chunks > kAttnTailChunks) {   // the split walk and the batched tail combine
+        if (b.cpb == 1) hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 1, true>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
+        else hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 2, true>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
+    } else {
+        if (b.cpb == 1) hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 1, false>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
+        else hipLaunchKernelGGL((qkv_attention_kernel<1, 1, 2, false>), grid, dim3(kBlock), 0, s, p, b, tiles, gy);
+    }
     return hipGetLastError();
 }
 
