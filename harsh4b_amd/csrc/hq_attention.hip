@@ -40,14 +40,17 @@ struct ChunkTile {
     static constexpr int kPerThread = (kGroups + kBlock - 1) / kBlock;
 };
 
+// (thread `tid` of a 256-thread group: the block's thread by default)
 template <int D>
 __device__ __forceinline__ void load_chunk(const AttnParams& a, const uint16_t* keys, const uint16_t* values,
-                                           int t0, int tn, int skip_t, size_t kv_off, uint4* kreg, uint4* vreg)
+                                           int t0, int tn, int skip_t, size_t kv_off, uint4* kreg, uint4* vreg,
+                                           int tid = -1)
 {
     using T = ChunkTile<D>;
+    if (tid < 0) tid = int(threadIdx.x);
 #pragma unroll
     for (int r = 0; r < T::kPerThread; ++r) {
-        const int id = threadIdx.x + kBlock * r;
+        const int id = tid + kBlock * r;
         const int t = id / T::kGroupsPerRow;
         const int d8 = id % T::kGroupsPerRow;
         const bool ok = id < T::kGroups && t < tn && t != skip_t;
@@ -693,6 +696,318 @@ __global__ __launch_bounds__(kBlock) void qkv_attention_kernel(GemmParams gp, At
     if (u >= 0) attention_tail<128, BIG>(a, u % a.batch, u / a.batch, ep);   // (block-uniform)
 }
 
+// ---- batched step attention, one block per (sequence, kv head) -------------------
+//
+// For batches of more than 16 sequences whose states hold at most kSeqChunks
+// chunks: block (z, g) of 1024 threads runs kv head g of sequence z over its
+// whole context, four 256-thread groups side by side (group u takes chunks u,
+// u + 4), each chunk exactly as attention_block computes it (the group's K/V
+// loads go out one chunk ahead, into registers, then LDS; scores, chunk
+// statistics, V chains).  The chunk partials stay in the block's LDS, and
+// threads (head, dim) combine them over ascending chunks as the split
+// launches' tails do (M = m_0, then fmaxf with m_1, ...; a_c = exp(m_c - M);
+// L and O fmaf chains; out = O * (1 / L)).  The row's maximum |out| is
+// exchanged among the sequence's eight kv-head blocks as {value, epoch}
+// entries (bounded waits, HQ_STEP_SYNC), and each block quantizes its four
+// heads into the o GEMM's input row (amax floored at 1e-5, quant_i8 with 127
+// / amax, de-interleaved, act = amax / 127).  No chunk partial leaves the
+// CU, and no tail block waits for a place on the chip.
+constexpr int kSeqSubs = 4;                        // 256-thread groups per block
+constexpr int kSeqThreads = kSeqSubs * kBlock;
+constexpr int kSeqChunks = 8;                      // contexts of up to 8 chunks
+#ifndef HQ_SEQ_MIN_BATCH
+#define HQ_SEQ_MIN_BATCH 17
+#endif
+constexpr int kSeqMinBatch = HQ_SEQ_MIN_BATCH;     // batches that take seq_attention_kernel
+
+struct SeqAttnLds {
+    float q_s[4][128];
+    uint16_t kc_s[128];
+    uint16_t vc_s[128];
+    struct Sub {
+        alignas(16) uint16_t k_s[kAttnChunk * ChunkTile<128>::kRowHalves];
+        alignas(16) uint16_t v_s[kAttnChunk * ChunkTile<128>::kRowHalves];
+        float e_s[4][kAttnChunk];
+    } sub[kSeqSubs];
+    float m_s[4][kSeqChunks];
+    float l_s[4][kSeqChunks];
+    float al_s[4][kSeqChunks];
+    float o_s[kSeqChunks][4][128];
+    float wmax[kSeqThreads / kWave];
+    float amax;
+};
+
+__global__ __launch_bounds__(kSeqThreads) void seq_attention_kernel(AttnParams a)
+{
+    constexpr int D = 128, G = 4, C = kAttnChunk, DPL = D / 16;
+    using T = ChunkTile<D>;
+    __shared__ SeqAttnLds S;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid & (kWave - 1);
+    const int sub = tid / kBlock, st = tid % kBlock, sw = wave % (kBlock / kWave);
+    const int g = int(blockIdx.x) % a.kv_heads, z = int(blockIdx.x) / a.kv_heads;
+    const uint32_t ep = (*a.epoch_ctr << 8) | uint32_t(a.epoch_id);
+    int32_t* status = a.table->status[z];
+    // sequence z at its own position, in its own cache; a position outside
+    // the cache writes nothing and reads the cache as is
+    const int zpos = *a.table->position[z];
+    const int cap = a.table->capacity[z];
+    const int n = min(max(zpos, 0), cap - 1) + 1;
+    const bool kvnew = zpos >= 0 && zpos < cap;
+    const int pos = n - 1;
+    const size_t slab = size_t(cap) * size_t(a.kv_heads) * size_t(D);
+    uint16_t* keys = a.table->keys[z] + size_t(a.layer) * slab;
+    uint16_t* values = a.table->values[z] + size_t(a.layer) * slab;
+    const float* qkv = a.qkv + size_t(z) * size_t(a.kv_heads) * size_t(G + 2) * D;
+    const int nc = (n + C - 1) / C;               // <= kSeqChunks (checked by the launch)
+    const int cur_chunk = kvnew ? nc - 1 : -1;    // chunk holding the current position
+    const size_t kv_off = size_t(g) * D;
+
+    // a chunk's K loads go out before its V loads (a wave's loads complete
+    // in issue order); they are buffer loads, all issued on every path, so
+    // the compiler's waits count exactly the loads behind each use
+    uint4 kreg[T::kPerThread], vreg[T::kPerThread];
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const __amdgpu_buffer_rsrc_t rk = raw_rsrc(keys, int(slab * 2));
+    const __amdgpu_buffer_rsrc_t rv = raw_rsrc(values, int(slab * 2));
+    // (a row outside the chunk, or a chunk past the context: an offset past
+    // the buffer, read as 0 without a memory access)
+    auto offsets = [&](int c, uint32_t (&vo)[T::kPerThread]) {
+        const int t0 = c * C;
+        const int tn = min(C, n - t0);   // (<= 0 past the context)
+        const int skip_t = c == cur_chunk ? pos - t0 : -1;
+#pragma unroll
+        for (int r = 0; r < T::kPerThread; ++r) {
+            const int id = st + kBlock * r;
+            const int t = id / T::kGroupsPerRow;
+            const int d8 = id % T::kGroupsPerRow;
+            const bool ok = id < T::kGroups && t < tn && t != skip_t;
+            vo[r] = ok ? uint32_t((size_t(t0 + t) * a.time_stride + kv_off + size_t(d8) * 8) * 2) : 0x80000000u;
+        }
+    };
+    auto load_m = [&](const __amdgpu_buffer_rsrc_t& rs, const uint32_t (&vo)[T::kPerThread], uint4 (&reg)[T::kPerThread]) {
+#pragma unroll
+        for (int r = 0; r < T::kPerThread; ++r) {
+            const v4u w = __builtin_amdgcn_raw_buffer_load_b128(rs, vo[r], 0, 0);
+            reg[r] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    };
+    // registers -> LDS for one matrix (the current position's row comes
+    // from kc_s / vc_s)
+    auto to_lds = [&](int c, int tn, const uint4 (&reg)[T::kPerThread], const uint16_t* cur, uint16_t* dst) {
+#pragma unroll
+        for (int r = 0; r < T::kPerThread; ++r) {
+            const int id = st + kBlock * r;
+            const int t = id / T::kGroupsPerRow;
+            const int d8 = id % T::kGroupsPerRow;
+            if (id < T::kGroups && t < tn) {
+                uint4 w = reg[r];
+                if (c == cur_chunk && c * C + t == pos) w = *reinterpret_cast<const uint4*>(cur + d8 * 8);
+                *reinterpret_cast<uint4*>(dst + t * T::kRowHalves + d8 * 8) = w;
+            }
+        }
+    };
+    // ---- query heads and the current position's k/v ----------------------
+    // Every wave loads its operands first (waves 0-3 query head `wave`, wave
+    // 4 the k row, wave 5 the v row, the others query head 0 unused), then
+    // its group's first chunk; every load is issued on every path, so the
+    // waits the compiler places count exactly the loads behind each use.
+    const int heads = a.kv_heads * G;
+    const int prow = wave < G ? g * G + wave : wave == G ? heads + g : wave == G + 1 ? heads + a.kv_heads + g : g * G;
+    const float x0 = qkv[size_t(prow) * D + lane];
+    const float x1 = qkv[size_t(prow) * D + lane + 64];
+    const float* nw = wave == G ? a.k_norm : a.q_norm;
+    const float nw0 = nw[lane], nw1 = nw[lane + 64];
+    const float c0 = a.rope_cos[size_t(pos) * (D / 2) + lane];
+    const float s0 = a.rope_sin[size_t(pos) * (D / 2) + lane];
+    // Only the first chunk's K rows go out now.  A wave whose loads find the
+    // CU's memory pipe full stalls at the load instruction, so a wave that
+    // issued its V rows as well would reach its next computation only once
+    // most of the launch's K/V bytes had arrived; the V rows go out once
+    // the K rows are in LDS, and the scores run while they stream.
+    uint32_t vo[T::kPerThread];
+    offsets(sub, vo);
+    load_m(rk, vo, kreg);
+    if (wave <= G) {
+        float p = __builtin_fmaf(x0, x0, 0.0f);
+        p = __builtin_fmaf(x1, x1, p);
+        const float ss = wave_tree_sum64_all(p);
+        const float r = __builtin_sqrtf(ss / float(D) + a.eps);
+        const float y0 = (x0 / r) * nw0;
+        const float y1 = (x1 / r) * nw1;
+        const float r0 = y0 * c0 - y1 * s0;
+        const float r1 = y1 * c0 + y0 * s0;
+        if (wave < G) {
+            S.q_s[wave][lane] = r0;
+            S.q_s[wave][lane + 64] = r1;
+        } else if (kvnew) {
+            const uint16_t h0 = f32_to_f16(r0);
+            const uint16_t h1 = f32_to_f16(r1);
+            // (buffer stores: flat ones would make the compiler's waits
+            // for the chunk loads conservative)
+            const uint32_t o = uint32_t((size_t(pos) * a.time_stride + kv_off + lane) * 2);
+            __builtin_amdgcn_raw_buffer_store_b16(h0, rk, o, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(h1, rk, o + 128, 0, 0);
+            S.kc_s[lane] = h0;
+            S.kc_s[lane + 64] = h1;
+        }
+    } else if (wave == G + 1 && kvnew) {
+        const uint16_t h0 = f32_to_f16(x0);
+        const uint16_t h1 = f32_to_f16(x1);
+        const uint32_t o = uint32_t((size_t(pos) * a.time_stride + kv_off + lane) * 2);
+        __builtin_amdgcn_raw_buffer_store_b16(h0, rv, o, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(h1, rv, o + 128, 0, 0);
+        S.vc_s[lane] = h0;
+        S.vc_s[lane + 64] = h1;
+    }
+    lds_sync();
+
+    const int grp = st >> 4;        // 16 lane groups for the scores
+    const int l16 = st & 15;
+    const float scale = 1.0f / __builtin_sqrtf(float(D));
+    float qr[G][DPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) qr[h][j] = S.q_s[h][l16 * DPL + j];
+    const int d = st % D;
+    const int h0 = st / D;          // V chains: heads h0 and h0 + 2
+    auto& B = S.sub[sub];
+    const int rounds = (nc + kSeqSubs - 1) / kSeqSubs;
+
+    // every group passes the same barriers, with or without a chunk; the
+    // barriers order LDS only (lds_sync), so loads in flight stay in flight
+#pragma unroll 1
+    for (int rd = 0; rd < rounds; ++rd) {
+        const int c = sub + kSeqSubs * rd;
+        const bool mine = c < nc;   // (group-uniform)
+        const int t0 = c * C;
+        const int tn = mine ? min(C, n - t0) : 0;
+        if (mine) to_lds(c, tn, kreg, S.kc_s, B.k_s);
+        load_m(rv, vo, vreg);   // this chunk's V rows
+        lds_sync();
+        if (mine) {
+            // scores, 16 lanes per position
+#pragma unroll
+            for (int rep = 0; rep < C / 16; ++rep) {
+                const int i = grp + 16 * rep;
+                if (i < tn) {
+                    float k[DPL];
+                    const uint16_t* kr = B.k_s + i * T::kRowHalves + l16 * DPL;
+#pragma unroll
+                    for (int j = 0; j < DPL; ++j) k[j] = f16_to_f32(kr[j]);
+#pragma unroll
+                    for (int h = 0; h < G; ++h) {
+                        float pp = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < DPL; ++j) pp = __builtin_fmaf(qr[h][j], k[j], pp);
+                        const float dot = row_tree_sum16(pp);
+                        if (l16 == 0) B.e_s[h][i] = dot * scale;
+                    }
+                } else if (l16 == 0) {
+#pragma unroll
+                    for (int h = 0; h < G; ++h) B.e_s[h][i] = -__builtin_inff();
+                }
+            }
+        }
+        if (mine) to_lds(c, tn, vreg, S.vc_s, B.v_s);
+        offsets(c + kSeqSubs, vo);   // the group's next chunk (past the context: nothing)
+        load_m(rk, vo, kreg);
+        lds_sync();
+        if (mine) {
+            // chunk softmax statistics, one wave of the group per head
+            const int h = sw;
+            const float sc = B.e_s[h][lane];
+            const float m = wave_max64_all(sc);
+            const float e = (lane < tn) ? spec_expf(sc - m) : 0.0f;
+            const float l = wave_tree_sum64(e);
+            B.e_s[h][lane] = e;
+            if (lane == 0) { S.m_s[h][c] = m; S.l_s[h][c] = l; }
+        }
+        lds_sync();
+        if (mine) {
+            // V chains over ascending positions, eight LDS reads ahead
+            float o_acc[2] = {0.0f, 0.0f};
+            int i = 0;
+            for (; i + 8 <= tn; i += 8) {
+                float v[8], e[2][8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    v[j] = f16_to_f32(B.v_s[(i + j) * T::kRowHalves + d]);
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) e[r][j] = B.e_s[h0 + 2 * r][i + j];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) o_acc[r] = __builtin_fmaf(e[r][j], v[j], o_acc[r]);
+            }
+            for (; i < tn; ++i) {
+                const float v = f16_to_f32(B.v_s[i * T::kRowHalves + d]);
+#pragma unroll
+                for (int r = 0; r < 2; ++r) o_acc[r] = __builtin_fmaf(B.e_s[h0 + 2 * r][i], v, o_acc[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 2; ++r) S.o_s[c][h0 + 2 * r][d] = o_acc[r];
+        }
+        lds_sync();
+    }
+
+    // ---- combine over ascending chunks, thread (head, dim) -----------------
+    // (a_c once per (head, chunk): thread h * 8 + c)
+    if (tid < G * kSeqChunks) {
+        const int h = tid / kSeqChunks, c = tid % kSeqChunks;
+        float M = S.m_s[h][0];
+        for (int j = 1; j < nc; ++j) M = fmaxf(M, S.m_s[h][j]);
+        if (c < nc) S.al_s[h][c] = spec_expf(S.m_s[h][c] - M);
+    }
+    lds_sync();
+    float val = 0.0f;
+    if (tid < G * D) {
+        const int h = tid / D, dd = tid % D;
+        float L = 0.0f, O = 0.0f;
+        for (int c = 0; c < nc; ++c) {
+            const float al = S.al_s[h][c];
+            L = __builtin_fmaf(al, S.l_s[h][c], L);
+            O = __builtin_fmaf(al, S.o_s[c][h][dd], O);
+        }
+        val = O * (1.0f / L);
+    }
+    // ---- the row's maximum over the sequence's kv-head blocks, then quant --
+    float mx = wave_max64_all(fabsf(val));   // (threads past G * D hold 0)
+    if (lane == 0) S.wmax[wave] = mx;
+    lds_sync();
+    if (wave == 0) {
+        uint64_t* mrow = a.ll_max + size_t(z) * kAttnTailParts;
+        if (lane == 0) {
+            float qm = S.wmax[0];
+            for (int w = 1; w < kSeqThreads / kWave; ++w) qm = fmaxf(qm, S.wmax[w]);
+            tail_store(mrow + g, qm, ep);
+        }
+        // lane q < 8 waits for block q's maximum
+        const bool mine = lane < kAttnTailParts;
+        uint64_t e = mine ? tail_load(mrow + lane) : (uint64_t(ep) << 32);
+        unsigned spins = 0;
+        while (__builtin_amdgcn_ballot_w64(!tail_ready(e, ep))) {   // (wave-uniform)
+            if (++spins == kTailSpinLimit) {
+                if (lane == 0) atomicOr(status, HQ_STEP_SYNC);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            if (!tail_ready(e, ep)) e = tail_load(mrow + lane);
+        }
+        float am = mine ? bits_f32(uint32_t(e)) : 0.0f;
+        am = wave_max64_all(am);
+        if (lane == 0) S.amax = fmaxf(am, 1e-5f);
+    }
+    lds_sync();
+    const float amax = S.amax;
+    const float inv = 127.0f / amax;
+    if (tid < G * D) a.q8[size_t(z) * a.kp + xq_offset(g * G * D + tid)] = quant_i8(val, inv);
+    if (g == 0 && tid == 0) a.act[z] = amax / 127.0f;
+}
+
+
 // Combine of the chunk partials when a context spans several chunks: thread
 // (blockIdx.x * kBlock + tid) is output element (query head hh, dim d) of
 // query z = blockIdx.y.  Same arithmetic as the single-chunk combine above:
@@ -979,6 +1294,12 @@ hipError_t launch_batch_attention(const AttnParams& a, hipStream_t s)
     // one chunk per block while the grid fits about one round of the chip
     // (four 256-thread blocks per CU), else two; at most kAttnMaxSplits
     // splits in the grid (blocks walk the further ones)
+    if (a.batch >= kSeqMinBatch && a.kv_heads == kAttnTailParts && a.groups == 4 && a.max_chunks <= kSeqChunks &&
+        a.ll_max && a.epoch_ctr && a.epoch_id >= 0 && a.epoch_id < 256) {
+        // one block per (sequence, kv head), the combine and quantization in it
+        hipLaunchKernelGGL(seq_attention_kernel, dim3(a.batch * a.kv_heads), dim3(kSeqThreads), 0, s, a);
+        return hipGetLastError();
+    }
     AttnParams b = a;
     b.cpb = a.kv_heads * min(a.max_chunks, kAttnMaxSplits) * a.batch <= 1024 ? 1 : 2;
     const dim3 grid(a.kv_heads, min((a.max_chunks + b.cpb - 1) / b.cpb, kAttnMaxSplits), a.batch);

@@ -169,7 +169,7 @@ def test_gqa_known_answer(kat):
     np.testing.assert_allclose(got, kat["gqa_expected"], rtol=5e-3, atol=5e-3)
 
 
-@pytest.mark.parametrize("ctx", [1, 2, 63, 64, 65, 129, 300, 4096])
+@pytest.mark.parametrize("ctx", [1, 2, 63, 64, 65, 129, 300, 4096, 4161, 9000])
 def test_gqa_qwen_shape_bit_exact(ctx):
     ls = lightspark()
     rng = np.random.default_rng(ctx)
