@@ -698,7 +698,7 @@ __global__ __launch_bounds__(kBlock) void qkv_attention_kernel(GemmParams gp, At
 
 // ---- batched step attention, one block per (sequence, kv head) -------------------
 //
-// For batches of more than 16 sequences whose states hold at most kSeqChunks
+// For batches of more than 8 sequences whose states hold at most kSeqChunks
 // chunks: block (z, g) of 1024 threads runs kv head g of sequence z over its
 // whole context, four 256-thread groups side by side (group u takes chunks u,
 // u + 4), each chunk exactly as attention_block computes it (the group's K/V
@@ -716,7 +716,7 @@ constexpr int kSeqSubs = 4;                        // 256-thread groups per bloc
 constexpr int kSeqThreads = kSeqSubs * kBlock;
 constexpr int kSeqChunks = 8;                      // contexts of up to 8 chunks
 #ifndef HQ_SEQ_MIN_BATCH
-#define HQ_SEQ_MIN_BATCH 17
+#define HQ_SEQ_MIN_BATCH 9
 #endif
 constexpr int kSeqMinBatch = HQ_SEQ_MIN_BATCH;     // batches that take seq_attention_kernel
 
@@ -1342,6 +1342,7 @@ hipError_t launch_batch_qkv_attention(const int8_t* x, const float* act, const u
 {
     const int H = a.kv_heads * a.groups;
     const int rows = (H + 2 * a.kv_heads) * a.head_dim;
+    if (a.batch >= kSeqMinBatch) return hipErrorNotSupported;   // (seq_attention_kernel's batches)
     if (!a.qkv_ll || !a.ll_part || !a.ll_out || !a.ll_max || !a.epoch_ctr || a.epoch_id < 0 || a.epoch_id >= 256 ||
         a.head_dim != 128 || !a.table || !a.qkv || !a.q8 || !a.act || a.batch < 1 || a.batch > 16 ||
         a.groups > 4 || H % (2 * kAttnTailParts) != 0 ||
