@@ -115,7 +115,8 @@ size_t attention_workspace_floats(int heads, int max_chunks, int head_dim);
 // The batched step's qkv GEMM (x: the de-interleaved input rows, act their
 // scales; w, ws: the qkv matrix, k = hidden) and attention in one launch,
 // with the attention's tails (a.ll_part ...) and the raw projection as
-// entries in a.qkv_ll, for up to 16 sequences.  Returns
+// entries in a.qkv_ll, for up to 16 sequences (batches that take the
+// per-(sequence, kv head) attention excepted).  Returns
 // hipErrorNotSupported, having launched nothing, when the shapes do not
 // allow it (the caller then runs gemm_run and launch_batch_attention).
 hipError_t launch_batch_qkv_attention(const int8_t* x, const float* act, const uint8_t* w, const float* ws, int k,

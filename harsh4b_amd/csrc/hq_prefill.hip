@@ -25,9 +25,11 @@
 // batch and a per-sequence argmax that feeds each greedy token back on the
 // device: M forward_token steps (cpu_lightspark.py:424-468) sharing every
 // weight read, bit-identical to them.  Where the shapes allow, each layer is
-// four launches (up to 16 sequences; five beyond): the qkv GEMM and the
-// attention in one (separate beyond 16), the attention's last blocks
-// combining and quantizing each sequence's row; the o GEMM, whose last
+// four launches (up to 8 sequences; five beyond): the qkv GEMM and the
+// attention in one (separate beyond 8, where one attention block per
+// sequence and kv head combines and, with the sequence's other kv-head
+// blocks, quantizes the row), the attention's last blocks combining and
+// quantizing each sequence's row; the o GEMM, whose last
 // blocks add the residual and run the post-attention norm and
 // quantization; the gate_up GEMM with SwiGLU, whose last blocks quantize
 // the down input; the down GEMM, whose last blocks add the residual and run
