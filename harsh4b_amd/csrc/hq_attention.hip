@@ -613,12 +613,28 @@ __device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
         for (int w = 1; w < kBlock / kWave; ++w) qm = fmaxf(qm, wmax_s[w]);
         tail_store(a.ll_max + size_t(s) * kAttnTailParts + qt, qm, ep);
     }
-    uint64_t qe[kAttnTailParts];
-    unrolled<kAttnTailParts>([&](auto q) { qe[q] = tail_load(a.ll_max + size_t(s) * kAttnTailParts + q); });
-    wait(qe, [&](auto q) { return tail_load(a.ll_max + size_t(s) * kAttnTailParts + q); });
-    float amax = bits_f32(uint32_t(qe[0]));
-    unrolled<kAttnTailParts - 1>([&](auto q) { amax = fmaxf(amax, bits_f32(uint32_t(qe[q + 1]))); });
-    amax = fmaxf(amax, 1e-5f);
+    // lane q < 8 of wave 0 waits for part q's maximum (one poll per part
+    // and round: polled by every thread, the 2048 reads of each entry per
+    // round held the exchange back), then the block reads it from LDS
+    __shared__ float amax_s;
+    if (tid < kWave) {
+        const bool mine = lane < kAttnTailParts;
+        const uint64_t* mrow = a.ll_max + size_t(s) * kAttnTailParts;
+        uint64_t e = mine ? tail_load(mrow + lane) : uint64_t(ep) << 32;
+        unsigned spins = 0;
+        while (__builtin_amdgcn_ballot_w64(!tail_ready(e, ep))) {   // (wave-uniform)
+            if (++spins == kTailSpinLimit) {
+                if (lane == 0) atomicOr(status, HQ_STEP_SYNC);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            if (!tail_ready(e, ep)) e = tail_load(mrow + lane);
+        }
+        const float am = wave_max64_all(mine ? bits_f32(uint32_t(e)) : 0.0f);   // (order-free)
+        if (lane == 0) amax_s = fmaxf(am, 1e-5f);
+    }
+    __syncthreads();
+    const float amax = amax_s;
     const float inv = 127.0f / amax;
     int8_t* qr = a.q8 + size_t(s) * a.kp;
     unrolled<NO>([&](auto i) {
