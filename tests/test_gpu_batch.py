@@ -192,6 +192,41 @@ def test_qwen3_4b_batch_step_counter_wrap(qwen):
     assert int(_step_counter(model, cap).item()) == 2
 
 
+@pytest.mark.parametrize("m", [8, 32])
+def test_qwen3_4b_batch_full_state_spares_the_rest(qwen, m):
+    # One sequence of the batch sits at its cache's capacity on the device
+    # (the host's capacity check passed, as a C-ABI caller's could): its
+    # status gets HQ_STEP_FULL and it writes no K/V row, and every other
+    # sequence's step equals its single step bit for bit (M = 8: the qkv
+    # GEMM and the attention in one launch; M = 32: one attention block per
+    # sequence and kv head).
+    from harsh4b_amd import _native
+    model = qwen
+    rng = np.random.default_rng(700 + m)
+    lengths = [int(v) for v in rng.integers(1, 200, m)]
+    lengths[0] = 64
+    A, B = [], []
+    for n in lengths:
+        pr = [int(t) for t in rng.integers(0, 151936, n)]
+        for group in (A, B):
+            st = model.new_state(n + 4)
+            model.prefill(pr, st)
+            group.append(st)
+    full = 3
+    A[full].device_position.fill_(A[full].capacity)
+    keys0, values0 = to_host(A[full].keys).copy(), to_host(A[full].values).copy()
+    nxt = [int(t) for t in rng.integers(0, 151936, m)]
+    model.forward_tokens(nxt, A)
+    for t, st in zip(nxt, B):
+        model.forward_token(t, st)
+    A[full].synchronize()
+    assert int(A[full].status.item()) & _native.HQ_STEP_FULL
+    assert_bits_equal(to_host(A[full].keys).view(np.uint16), keys0.view(np.uint16), "full state's keys")
+    assert_bits_equal(to_host(A[full].values).view(np.uint16), values0.view(np.uint16), "full state's values")
+    keep = [i for i in range(m) if i != full]
+    _compare(model, [A[i] for i in keep], [B[i] for i in keep], f"M={m} beside a full state")
+
+
 @pytest.fixture(scope="module")
 def qwen_oracle(qwen):
     from harsh4b_amd.synthetic import host_arrays
