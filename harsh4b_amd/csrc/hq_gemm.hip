@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
 }
 
 template <int RG, int W, int BT, int DS, int CPT, int HMAX, bool SWIGLU = false, int TAIL = 0>
-__global__ __launch_bounds__(kWave * W) void gemm_lds_kernel(GemmParams p)
+__global__ __launch_bounds__(kWave * W, (W == 4 && BT == 2) ? 3 : 1) void gemm_lds_kernel(GemmParams p)
 {
     __shared__ __align__(16) uint8_t a_s[16 * RG * (HMAX + 16)];
     gemm_lds_block<RG, W, BT, DS, CPT, HMAX, SWIGLU, TAIL>(p, a_s);
