@@ -636,9 +636,8 @@ __device__ void attention_tail(const AttnParams& a, int s, int qt, uint32_t ep)
     __syncthreads();
     const float amax = amax_s;
     const float inv = 127.0f / amax;
-    int8_t* qr = a.q8 + size_t(s) * a.kp;
     unrolled<NO>([&](auto i) {
-        if (h0 + 2 * i < HQ) qr[xq_offset((hb + h0 + 2 * i) * D + d)] = quant_i8(val[i], inv);
+        if (h0 + 2 * i < HQ) a.q8[bq_pos(s, xq_offset((hb + h0 + 2 * i) * D + d), a.kp)] = quant_i8(val[i], inv);
     });
     if (qt == 0 && tid == 0) a.act[s] = amax / 127.0f;
 }
@@ -1019,7 +1018,7 @@ __global__ __launch_bounds__(kSeqThreads) void seq_attention_kernel(AttnParams a
     lds_sync();
     const float amax = S.amax;
     const float inv = 127.0f / amax;
-    if (tid < G * D) a.q8[size_t(z) * a.kp + xq_offset(g * G * D + tid)] = quant_i8(val, inv);
+    if (tid < G * D) a.q8[bq_pos(z, xq_offset(g * G * D + tid), a.kp)] = quant_i8(val, inv);
     if (g == 0 && tid == 0) a.act[z] = amax / 127.0f;
 }
 
@@ -1259,14 +1258,10 @@ __global__ __launch_bounds__(kCombineThreads) void batch_combine_quant_kernel(At
     for (int w = 1; w < T / kWave; ++w) amax = fmaxf(amax, wred[w]);
     amax = fmaxf(amax, 1e-5f);
     const float inv = 127.0f / amax;
-    int8_t* qr = a.q8 + size_t(z) * a.kp;
 #pragma unroll
     for (int i = 0; i < NO; ++i) {
         const int hh = h0 + HPP * i;
-        if (hh < H) {
-            const int e = hh * D + d;
-            qr[(e & ~7) + ((e & 1) ? 4 + ((e & 7) >> 1) : ((e & 7) >> 1))] = quant_i8(val[i], inv);
-        }
+        if (hh < H) a.q8[bq_pos(z, xq_offset(hh * D + d), a.kp)] = quant_i8(val[i], inv);
     }
     if (tid == 0) a.act[z] = amax / 127.0f;
 }

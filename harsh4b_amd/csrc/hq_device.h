@@ -336,6 +336,21 @@ __device__ __forceinline__ int xq_offset(int i)
 }
 
 // Symmetric int8 quantization of one value with inv = 127 / amax.
+// Byte position of de-interleaved column byte c (c = xq_offset(column)) of
+// row `row` in a batched GEMM input of row stride kp: the rows go in tiles
+// of 16 (tile t spans bytes [16 t kp, 16 (t + 1) kp), as 16 rows of kp
+// would), and within a tile every double step of 128 columns is two 1 KB
+// blocks, block h holding bytes 32 q + 16 h .. + 15 of the step for rows
+// r = 0..15 at (16 q + r) * 16 -- the order in which the 64 lanes of an
+// MFMA B operand (lane 16 q + r: row r, bytes 32 q + 16 h of the step) load
+// them, so each wave load of the operand reads 1 KB of contiguous memory
+// instead of a half of 16 rows' cache lines.
+__device__ __forceinline__ size_t bq_pos(int row, int c, int kp)
+{
+    return size_t(row >> 4) * 16 * size_t(kp) + size_t(c >> 7) * 2048 + size_t((c >> 4) & 1) * 1024 +
+           size_t((c >> 5) & 3) * 256 + size_t(row & 15) * 16 + size_t(c & 15);
+}
+
 __device__ __forceinline__ int8_t quant_i8(float v, float inv)
 {
     float q = __builtin_rintf(v * inv);

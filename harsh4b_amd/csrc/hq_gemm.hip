@@ -49,9 +49,6 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
         aok[rg] = row < p.n;
         arow[rg] = p.w + size_t(aok[rg] ? row : 0) * size_t(half);
     }
-    const int8_t* brow[BT];
-#pragma unroll
-    for (int b = 0; b < BT; ++b) brow[b] = p.x + size_t(min(16 * b + r16, p.m - 1)) * size_t(p.kp);
 
     i32x4 acc[RG][BT];
 #pragma unroll
@@ -72,9 +69,11 @@ __global__ __launch_bounds__(kWave * W) void gemm_kernel(GemmParams p)
                                 : make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int b = 0; b < BT; ++b) {
-                const int8_t* xp = brow[b] + 2 * pb;             // columns 2pb .. 2pb + 32 (zero past K)
+                // columns 2pb .. 2pb + 32 of row 16 b + r16 (zero past K; bq_pos;
+                // rows past m re-read row m - 1)
+                const int8_t* xp = p.x + bq_pos(min(16 * b + r16, p.m - 1), 2 * pb, p.kp);
                 xb[j][b][0] = j < nd ? *reinterpret_cast<const uint4*>(xp) : make_uint4(0, 0, 0, 0);
-                xb[j][b][1] = j < nd ? *reinterpret_cast<const uint4*>(xp + 16) : make_uint4(0, 0, 0, 0);
+                xb[j][b][1] = j < nd ? *reinterpret_cast<const uint4*>(xp + 1024) : make_uint4(0, 0, 0, 0);
             }
         }
 #pragma unroll
@@ -162,11 +161,10 @@ __global__ __launch_bounds__(kActQuantThreads) void batch_act_quant_kernel(const
     for (int w = 1; w < kActQuantThreads / kWave; ++w) amax = fmaxf(amax, wred[w]);
     amax = fmaxf(amax, 1e-5f);
     const float inv = 127.0f / amax;
-    int8_t* qr = q + size_t(m) * kp;
 #pragma unroll
     for (int j = 0; j < kActQuantNPT; ++j) {
         const int i = t + kActQuantThreads * j;
-        if (i < n) qr[(i & ~7) + ((i & 1) ? 4 + ((i & 7) >> 1) : ((i & 7) >> 1))] = quant_i8(v[j], inv);
+        if (i < n) q[bq_pos(m, xq_offset(i), kp)] = quant_i8(v[j], inv);
     }
     if (t == 0) act[m] = amax / 127.0f;
 }
@@ -208,7 +206,7 @@ __global__ __launch_bounds__(kBlock) void batch_quant_kernel(const float* x, int
             const float4 a = v[2 * i], b = v[2 * i + 1];
             const uint32_t ev = b8(a.x) | (b8(a.z) << 8) | (b8(b.x) << 16) | (b8(b.z) << 24);
             const uint32_t od = b8(a.y) | (b8(a.w) << 8) | (b8(b.y) << 16) | (b8(b.w) << 24);
-            *reinterpret_cast<uint2*>(q + size_t(m) * kp + c) = make_uint2(ev, od);
+            *reinterpret_cast<uint2*>(q + bq_pos(m, c, kp)) = make_uint2(ev, od);
             if (q_out) {
                 const uint32_t lo = b8(a.x) | (b8(a.y) << 8) | (b8(a.z) << 16) | (b8(a.w) << 24);
                 const uint32_t hi = b8(b.x) | (b8(b.y) << 8) | (b8(b.z) << 16) | (b8(b.w) << 24);
@@ -231,7 +229,7 @@ __global__ __launch_bounds__(kBlock) void batch_deinterleave_kernel(const int8_t
         const uint2 v = *reinterpret_cast<const uint2*>(x + size_t(m) * k + c);
         uint32_t ev, od;
         deinterleave8(v.x, v.y, ev, od);
-        *reinterpret_cast<uint2*>(q + size_t(m) * kp + c) = make_uint2(ev, od);
+        *reinterpret_cast<uint2*>(q + bq_pos(m, c, kp)) = make_uint2(ev, od);
     }
 }
 

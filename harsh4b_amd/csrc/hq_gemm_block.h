@@ -138,11 +138,10 @@ __device__ void gemm_tail_row(const GemmParams& p, int s, uint32_t ep, float* re
         for (int w = 1; w < kBlock / kWave; ++w) amax = fmaxf(amax, wmax[w]);
         amax = fmaxf(amax, 1e-5f);
         const float inv = 127.0f / amax;
-        int8_t* qr = T.q + size_t(s) * T.kq;
 #pragma unroll
         for (int j = 0; j < NPT; ++j) {
             const int i = tid + kBlock * j;
-            if (i < k) qr[xq_offset(i)] = quant_i8(v[j], inv);
+            if (i < k) T.q[bq_pos(s, xq_offset(i), T.kq)] = quant_i8(v[j], inv);
         }
         if (tid == 0) T.act[s] = amax / 127.0f;
     }
@@ -219,10 +218,9 @@ __device__ inline void gemm_swiglu_tail_row(const GemmParams& p, int s, int qt, 
         for (int w = 1; w < kBlock / kWave; ++w) amax = fmaxf(amax, wmax[w]);
         amax = fmaxf(amax, 1e-5f);
         const float inv = 127.0f / amax;
-        int8_t* qr = T.q + size_t(s) * T.kq;
         unrolled<10>([&](auto j) {
             const int i = i0 + kBlock * j;
-            if (i < n) qr[xq_offset(i)] = quant_i8(bits_f32(uint32_t(e[j])), inv);
+            if (i < n) T.q[bq_pos(s, xq_offset(i), T.kq)] = quant_i8(bits_f32(uint32_t(e[j])), inv);
         });
         if (qt == 0 && tid == 0) T.act[s] = amax / 127.0f;
     }
@@ -303,14 +301,17 @@ __device__ __forceinline__ void gemm_lds_block(const GemmParams& p, uint8_t* a_s
     uint4 xb[DS][BT][2];
 #pragma unroll
     for (int b = 0; b < BT; ++b) {
-        const int8_t* brow = p.x + size_t(min(16 * b + r16, p.m - 1)) * size_t(p.kp);
 #pragma unroll
         for (int j = 0; j < DS; ++j) {
-            // columns 2pb .. 2pb + 32 of a double step inside the row (the
-            // MFMAs of the steps past the wave's range are skipped)
-            const int8_t* xp = brow + 2 * (min(ds0 + j, nds - 1) * 64 + 16 * q);
+            // columns 2pb .. 2pb + 32 of a double step of row 16 b + r16
+            // (bq_pos: 1 KB contiguous per wave load; rows past m re-read
+            // row m - 1, whose lines the load fetches anyway, and land in
+            // discarded columns; the MFMAs of the steps past the wave's
+            // range are skipped)
+            const int8_t* xp =
+                p.x + bq_pos(min(16 * b + r16, p.m - 1), 2 * (min(ds0 + j, nds - 1) * 64 + 16 * q), p.kp);
             xb[j][b][0] = *reinterpret_cast<const uint4*>(xp);
-            xb[j][b][1] = *reinterpret_cast<const uint4*>(xp + 16);
+            xb[j][b][1] = *reinterpret_cast<const uint4*>(xp + 1024);
         }
     }
     // the epilogue's activation and row scales, fetched with the rest

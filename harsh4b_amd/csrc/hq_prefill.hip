@@ -173,11 +173,10 @@ __global__ __launch_bounds__(THREADS) void prefill_rows_kernel(RowParams p)
     for (int w = 1; w < THREADS / kWave; ++w) amax = fmaxf(amax, wmax[w]);
     amax = fmaxf(amax, 1e-5f);
     const float inv = 127.0f / amax;
-    int8_t* qr = p.q + size_t(m) * p.kp;
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
         const int i = tid + THREADS * j;
-        if (i < k) qr[deint_offset(i)] = quant_i8(v[j], inv);
+        if (i < k) p.q[bq_pos(m, deint_offset(i), p.kp)] = quant_i8(v[j], inv);
     }
     if (tid == 0) p.act[m] = amax / 127.0f;
 }
@@ -413,11 +412,10 @@ __global__ __launch_bounds__(kBlock) void batch_begin_kernel(BatchTable t, Batch
     for (int w = 1; w < kBlock / kWave; ++w) amax = fmaxf(amax, wmax[w]);
     amax = fmaxf(amax, 1e-5f);
     const float inv = 127.0f / amax;
-    int8_t* qr = q + size_t(m) * kq;
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
         const int i = tid + kBlock * j;
-        if (i < hidden) qr[deint_offset(i)] = quant_i8(v[j], inv);
+        if (i < hidden) q[bq_pos(m, deint_offset(i), kq)] = quant_i8(v[j], inv);
     }
     if (tid == 0) act[m] = amax / 127.0f;
 }

@@ -155,8 +155,10 @@ int hq_sample_token(const float* logits, int n, const int32_t* generated, int n_
  * sum crosses blocks.  `workspace` (hq_gemm_workspace_bytes(m, rows, width)
  * bytes, 16-byte aligned, zero-filled before its first use) holds the
  * activations re-laid out for the MFMA operands: m rows padded to a
- * multiple of 16, width padded to a multiple of 256 columns, even/odd
- * columns de-interleaved per 8, then (hq_quant_int4_gemm) the m activation
+ * multiple of 32, width padded to a multiple of 256 columns, even/odd
+ * columns de-interleaved per 8, stored in tiles of 16 rows in the order the
+ * 64 lanes of an MFMA B operand load them (each 128-column step of a tile
+ * as two 1 KB blocks), then (hq_quant_int4_gemm) the m activation
  * scales.  A call never writes the padding, which must stay zero, so a
  * workspace may be reused by later calls of the same m and width; give
  * calls of other shapes their own workspace.  width % 32 == 0, weights
