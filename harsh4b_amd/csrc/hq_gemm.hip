@@ -287,8 +287,10 @@ static bool launch_staged(const GemmParams& p, bool two_groups, hipStream_t s)
     const int half = p.k >> 1;
     if (half <= 1280) {
         // two sequence tiles share each weight row over 32 rows (M = 32:
-        // gate_up 18.8 -> 16.9 us, the LM head 106.8 -> 81.7 us)
-        if (two_groups || BT == 2) launch_gemm_lds<2, 4, BT, 1280>(p, s);
+        // gate_up 18.8 -> 16.9 us, the LM head 106.8 -> 81.7 us) where that
+        // still leaves a block per CU (the qkv GEMM's 192 blocks of 32 rows
+        // took longer than its 384 of 16: 2.488 -> 2.473 ms per M = 32 step)
+        if (two_groups || (BT == 2 && (p.n + 31) / 32 >= 256)) launch_gemm_lds<2, 4, BT, 1280>(p, s);
         else launch_gemm_lds<1, 4, BT, 1280>(p, s);
     } else if (half <= 2048) {
         launch_gemm_lds<1, 8, BT, 2048>(p, s);
