@@ -106,13 +106,15 @@ def qwen():
     return model
 
 
-@pytest.mark.parametrize("m,big", [(8, False), (32, False), (8, True), (16, False), (1, False)])
+@pytest.mark.parametrize("m,big", [(8, False), (32, False), (8, True), (16, False), (16, True), (1, False)])
 def test_qwen3_4b_batch_matches_single_steps(qwen, m, big):
     # M sequences with histories of 1 .. 300 positions (one to five chunks
     # of attention, one to two chunk groups), stepped together and alone
-    # (up to 16 sequences the qkv GEMM runs in the attention's launch);
-    # with `big` one state holds 600 positions (more than eight chunks: the
-    # attention's chunk partials go through the separate combine kernel)
+    # (up to 8 sequences the qkv GEMM runs in the attention's launch, from
+    # 9 on one attention block per sequence and kv head); with `big` one
+    # state holds 600 positions (more than eight chunks: the split attention
+    # whose blocks walk further splits and whose tails combine the chunk
+    # partials in batches of eight)
     model = qwen
     rng = np.random.default_rng(100 + m)
     lengths = [int(v) for v in rng.integers(1, 300, m)]
