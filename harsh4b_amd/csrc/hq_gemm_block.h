@@ -293,9 +293,23 @@ __device__ __forceinline__ void gemm_lds_block(const GemmParams& p, uint8_t* a_s
             return wb + size_t(c) * 16;
         }
     };
+    // SwiGLU in two stages: chunks j < CPT / 2 of a thread hold gate rows,
+    // the rest up rows, and the activation loads go out between the two,
+    // so the gate rows' MFMAs run while the up rows stream
+    constexpr bool TWO = SWIGLU && (CPT % 2 == 0);
+    static_assert(!TWO || (CPT / 2) * kWave * W * 16 >= 16 * HMAX, "half the chunks cover 16 rows");
+    const int gcn = 16 * cpr;   // SwiGLU: the gate rows' chunks
+    auto chunk_of = [&](int j) {
+        if constexpr (TWO) {
+            const int jj = j < CPT / 2 ? j : j - CPT / 2;
+            return (j < CPT / 2 ? 0 : gcn) + min(tid + kWave * W * jj, gcn - 1);
+        } else {
+            return min(tid + kWave * W * j, total - 1);
+        }
+    };
     uint4 v[CPT];
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) v[j] = load16_nt(chunk_addr(min(tid + kWave * W * j, total - 1)));
+    for (int j = 0; j < (TWO ? CPT / 2 : CPT); ++j) v[j] = load16_nt(chunk_addr(chunk_of(j)));
     const int nds = (p.k + 127) >> 7;
     const int ds0 = nds * wave / W, ds1 = nds * (wave + 1) / W;
     uint4 xb[DS][BT][2];
@@ -313,6 +327,10 @@ __device__ __forceinline__ void gemm_lds_block(const GemmParams& p, uint8_t* a_s
             xb[j][b][0] = *reinterpret_cast<const uint4*>(xp);
             xb[j][b][1] = *reinterpret_cast<const uint4*>(xp + 1024);
         }
+    }
+    if constexpr (TWO) {
+#pragma unroll
+        for (int j = CPT / 2; j < CPT; ++j) v[j] = load16_nt(chunk_addr(chunk_of(j)));
     }
     // the epilogue's activation and row scales, fetched with the rest
     // (SwiGLU: element e = sequence e / 16, column e % 16 of the gate and up
@@ -332,13 +350,18 @@ __device__ __forceinline__ void gemm_lds_block(const GemmParams& p, uint8_t* a_s
             ws_e[i] = p.ws[min(row0 + e % R, p.n - 1)];
         }
     }
+    auto stage = [&](int j0, int j1) {
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int c = min(tid + kWave * W * j, total - 1);
-        const int r = int(unsigned(c) / unsigned(cpr));
-        *reinterpret_cast<uint4*>(a_s + r * RS + (c - r * cpr) * 16) = v[j];
-    }
-    lds_sync();
+        for (int j = 0; j < CPT; ++j) {
+            if (j >= j0 && j < j1) {
+                const int c = chunk_of(j);
+                const int r = int(unsigned(c) / unsigned(cpr));
+                *reinterpret_cast<uint4*>(a_s + r * RS + (c - r * cpr) * 16) = v[j];
+            }
+        }
+        lds_sync();
+    };
+    stage(0, TWO ? CPT / 2 : CPT);
 
     i32x4 acc[RG][BT];
 #pragma unroll
@@ -346,27 +369,38 @@ __device__ __forceinline__ void gemm_lds_block(const GemmParams& p, uint8_t* a_s
 #pragma unroll
         for (int b = 0; b < BT; ++b) acc[rg][b] = i32x4{0, 0, 0, 0};
     constexpr uint32_t m4 = 0xF0F0F0F0u;
+    // the MFMAs of row groups [rg0, rg1) over the wave's double steps
+    auto products = [&](int rg0, int rg1) {
 #pragma unroll
-    for (int j = 0; j < DS; ++j) {
-        const int pb = (ds0 + j) * 64 + 16 * q;        // this lane's 16 packed bytes of the row
-        if (ds0 + j < ds1) {
+        for (int j = 0; j < DS; ++j) {
+            const int pb = (ds0 + j) * 64 + 16 * q;        // this lane's 16 packed bytes of the row
+            if (ds0 + j < ds1) {
 #pragma unroll
-            for (int rg = 0; rg < RG; ++rg) {
-                // past K the activations are zero, so the padding read there adds 0
-                const uint4 w = pb < half ? *reinterpret_cast<const uint4*>(a_s + (16 * rg + r16) * RS + pb)
-                                          : make_uint4(0, 0, 0, 0);
-                const i32x4 a0 = {int((w.x << 4) & m4), int(w.x & m4), int((w.y << 4) & m4), int(w.y & m4)};
-                const i32x4 a1 = {int((w.z << 4) & m4), int(w.z & m4), int((w.w << 4) & m4), int(w.w & m4)};
+                for (int rg = 0; rg < RG; ++rg) {
+                    if (rg < rg0 || rg >= rg1) continue;
+                    // past K the activations are zero, so the padding read there adds 0
+                    const uint4 w = pb < half ? *reinterpret_cast<const uint4*>(a_s + (16 * rg + r16) * RS + pb)
+                                              : make_uint4(0, 0, 0, 0);
+                    const i32x4 a0 = {int((w.x << 4) & m4), int(w.x & m4), int((w.y << 4) & m4), int(w.y & m4)};
+                    const i32x4 a1 = {int((w.z << 4) & m4), int(w.z & m4), int((w.w << 4) & m4), int(w.w & m4)};
 #pragma unroll
-                for (int b = 0; b < BT; ++b) {
-                    const uint4 x0 = xb[j][b][0], x1 = xb[j][b][1];
-                    acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        a0, i32x4{int(x0.x), int(x0.y), int(x0.z), int(x0.w)}, acc[rg][b], 0, 0, 0);
-                    acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        a1, i32x4{int(x1.x), int(x1.y), int(x1.z), int(x1.w)}, acc[rg][b], 0, 0, 0);
+                    for (int b = 0; b < BT; ++b) {
+                        const uint4 x0 = xb[j][b][0], x1 = xb[j][b][1];
+                        acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            a0, i32x4{int(x0.x), int(x0.y), int(x0.z), int(x0.w)}, acc[rg][b], 0, 0, 0);
+                        acc[rg][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            a1, i32x4{int(x1.x), int(x1.y), int(x1.z), int(x1.w)}, acc[rg][b], 0, 0, 0);
+                    }
                 }
             }
         }
+    };
+    if constexpr (TWO) {
+        products(0, 1);         // gate rows (LDS rows 0-15), while the up rows stream
+        stage(CPT / 2, CPT);    // (the up rows go to LDS rows 16-31)
+        products(1, 2);
+    } else {
+        products(0, RG);
     }
     lds_sync();   // every wave's A reads are done: the partials reuse the LDS
     int32_t (*red)[NRED][kWave] = reinterpret_cast<int32_t (*)[NRED][kWave]>(a_s);
